@@ -1,0 +1,639 @@
+// C-ABI of libdbi_kv.so: handle state, argument validation, host<->device
+// staging, prefix-cache file I/O and readback. Kernels live in append.hip and
+// attention.hip.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kv_internal.hpp"
+
+struct dbi_kv {
+  dbi_kv_config cfg{};
+  dbi::KvGeom geom{};
+  dbi::KvStore store{};
+  dbi::Workspace ws{};
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t n_seen = 0;
+  int device = 0;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+dbi_status fail(dbi_status st, const std::string& msg) {
+  g_error = msg;
+  return st;
+}
+
+dbi_status hip_fail(hipError_t e, const char* what) {
+  return fail(DBI_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                  \
+  do {                                       \
+    hipError_t e_ = (expr);                  \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+template <typename T>
+hipError_t dalloc(T** p, size_t n) {
+  *p = nullptr;
+  if (n == 0) return hipSuccess;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T));
+  if (e != hipSuccess) return e;
+  return hipMemset(*p, 0, n * sizeof(T));
+}
+
+void free_store(dbi::KvStore& s) {
+  void* ptrs[] = {s.k, s.v, s.k8, s.v8, s.k_scale, s.v_scale, s.k_raw, s.k_sink, s.v_sink,
+                  s.rope_cs};
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  s = dbi::KvStore{};
+}
+
+void free_ws(dbi::Workspace& w) {
+  if (w.part) (void)hipFree(w.part);
+  if (w.counters) (void)hipFree(w.counters);
+  if (w.staging) (void)hipFree(w.staging);
+  w = dbi::Workspace{};
+}
+
+// device staging buffer for host-pointer calls (grown on demand)
+dbi_status need_staging(dbi_kv* kv, size_t floats) {
+  if (kv->ws.staging_floats >= floats) return DBI_OK;
+  if (kv->ws.staging) (void)hipFree(kv->ws.staging);
+  kv->ws.staging = nullptr;
+  kv->ws.staging_floats = 0;
+  if (hipMalloc(reinterpret_cast<void**>(&kv->ws.staging), floats * sizeof(float)) != hipSuccess)
+    return fail(DBI_ERR_NOMEM, "device staging allocation failed");
+  kv->ws.staging_floats = floats;
+  return DBI_OK;
+}
+
+dbi_status check_layer(const dbi_kv* kv, uint32_t layer) {
+  if (layer >= kv->cfg.n_layers)
+    return fail(DBI_ERR_INVALID, "layer " + std::to_string(layer) + " out of range");
+  return DBI_OK;
+}
+
+// dense caches hold positions [0, capacity); a ring wraps any position
+dbi_status check_rows(const dbi_kv* kv, uint64_t pos0, uint64_t n) {
+  if (!kv->geom.ring && pos0 + n > static_cast<uint64_t>(kv->geom.cap))
+    return fail(DBI_ERR_INVALID, "position " + std::to_string(pos0 + n - 1) +
+                                     " exceeds cache capacity " + std::to_string(kv->geom.cap));
+  if (pos0 + n > 0x7fffffffull) return fail(DBI_ERR_INVALID, "position out of range");
+  return DBI_OK;
+}
+
+dbi::RingView ring_view(const dbi_kv* kv, uint32_t n_seen) {
+  dbi::RingView r{};
+  const uint32_t s = kv->cfg.n_sink, W = kv->cfg.window;
+  r.s = static_cast<int>(s);
+  r.W = static_cast<int>(W);
+  const bool full = n_seen > s && n_seen - s > W;
+  r.n_res = full ? static_cast<int>(s + W) : static_cast<int>(n_seen);
+  r.base = full ? static_cast<int>((n_seen - s) % W) : 0;
+  return r;
+}
+
+dbi_status ensure_workspace(dbi_kv* kv, const dbi::AttnCall& c) {
+  size_t part = 0, counters = 0;
+  dbi::attention_workspace_need(kv->geom, c, &part, &counters);
+  if (part > kv->ws.part_floats) {
+    HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+    if (kv->ws.part) (void)hipFree(kv->ws.part);
+    kv->ws.part = nullptr;
+    kv->ws.part_floats = 0;
+    if (hipMalloc(reinterpret_cast<void**>(&kv->ws.part), part * sizeof(float)) != hipSuccess)
+      return fail(DBI_ERR_NOMEM, "attention workspace allocation failed");
+    kv->ws.part_floats = part;
+  }
+  if (counters > kv->ws.n_counters) {
+    HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+    if (kv->ws.counters) (void)hipFree(kv->ws.counters);
+    kv->ws.counters = nullptr;
+    kv->ws.n_counters = 0;
+    if (dalloc(&kv->ws.counters, counters) != hipSuccess)
+      return fail(DBI_ERR_NOMEM, "attention counter allocation failed");
+    kv->ws.n_counters = counters;
+  }
+  return DBI_OK;
+}
+
+dbi_status check_attend(const dbi_kv* kv, uint32_t layer, uint32_t n_heads, const void* q,
+                        const void* out) {
+  if (dbi_status st = check_layer(kv, layer)) return st;
+  if (q == nullptr || out == nullptr) return fail(DBI_ERR_INVALID, "null q or out");
+  if (n_heads == 0 || n_heads % kv->cfg.n_kv_heads != 0)
+    return fail(DBI_ERR_INVALID, "n_heads must be a positive multiple of n_kv_heads");
+  if (!dbi::attention_supported(kv->geom, static_cast<int>(n_heads)))
+    return fail(DBI_ERR_UNSUPPORTED,
+                "no attention kernel for head_dim " + std::to_string(kv->cfg.head_dim) +
+                    " and gqa " + std::to_string(n_heads / kv->cfg.n_kv_heads) +
+                    " (served: head_dim 64/128, gqa 1-8)");
+  return DBI_OK;
+}
+
+dbi_status decode_impl(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads, float scale,
+                       const float* q_dev, float* out_dev) {
+  if (dbi_status st = check_rows(kv, pos, 1)) return st;
+  dbi::AttnCall c{};
+  c.layer = static_cast<int>(layer);
+  c.rows = 1;
+  c.pos0 = static_cast<int>(pos);
+  c.n_heads = static_cast<int>(n_heads);
+  c.scale = scale;
+  c.q = q_dev;
+  c.out = out_dev;
+  if (kv->geom.ring) c.ring = ring_view(kv, pos + 1);
+  if (dbi_status st = ensure_workspace(kv, c)) return st;
+  HIP_TRY(dbi::launch_attention(kv->geom, kv->store, kv->ws, c, kv->stream), "attention launch");
+  return DBI_OK;
+}
+
+dbi_status chunk_impl(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, uint32_t n_heads,
+                      float scale, const float* q_dev, float* out_dev) {
+  if (kv->geom.ring)
+    return fail(DBI_ERR_UNSUPPORTED, "chunk attention serves the dense layouts only");
+  if (n == 0) return DBI_OK;
+  if (dbi_status st = check_rows(kv, pos0, n)) return st;
+  dbi::AttnCall c{};
+  c.layer = static_cast<int>(layer);
+  c.rows = static_cast<int>(n);
+  c.pos0 = static_cast<int>(pos0);
+  c.n_heads = static_cast<int>(n_heads);
+  c.scale = scale;
+  c.q = q_dev;
+  c.out = out_dev;
+  if (n > 65535) return fail(DBI_ERR_INVALID, "chunk longer than 65535 rows");
+  if (dbi_status st = ensure_workspace(kv, c)) return st;
+  HIP_TRY(dbi::launch_attention(kv->geom, kv->store, kv->ws, c, kv->stream), "attention launch");
+  return DBI_OK;
+}
+
+dbi_status append_impl(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, const float* k_dev,
+                       const float* v_dev) {
+  HIP_TRY(dbi::launch_append(kv->geom, kv->store, static_cast<int>(layer),
+                             static_cast<int>(pos0), static_cast<int>(n), k_dev, v_dev,
+                             kv->stream),
+          "append launch");
+  kv->n_seen = pos0 + n;
+  return DBI_OK;
+}
+
+dbi_status append_check(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, const void* k,
+                        const void* v) {
+  if (dbi_status st = check_layer(kv, layer)) return st;
+  if (n > 0 && (k == nullptr || v == nullptr)) return fail(DBI_ERR_INVALID, "null k or v");
+  return check_rows(kv, pos0, n);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dbi_last_error(void) { return g_error.c_str(); }
+
+dbi_status dbi_kv_create(const dbi_kv_config* cfg, dbi_kv** out) {
+  if (cfg == nullptr || out == nullptr) return fail(DBI_ERR_INVALID, "null argument");
+  *out = nullptr;
+  if (cfg->n_layers == 0 || cfg->n_kv_heads == 0 || cfg->head_dim == 0)
+    return fail(DBI_ERR_INVALID, "n_layers, n_kv_heads and head_dim must be positive");
+  if (cfg->dtype != DBI_KV_F32 && cfg->dtype != DBI_KV_INT8)
+    return fail(DBI_ERR_INVALID, "unknown dtype");
+  const uint64_t cap = cfg->window > 0 ? uint64_t(cfg->n_sink) + cfg->window : cfg->max_seq;
+  if (cap == 0 || cap > 0x7fffffffull) return fail(DBI_ERR_INVALID, "capacity out of range");
+  if (cfg->window > 0 && !(cfg->rope_theta > 0.0f))
+    return fail(DBI_ERR_INVALID, "ring cache needs rope_theta > 0");
+
+  dbi_kv* kv = new (std::nothrow) dbi_kv();
+  if (kv == nullptr) return fail(DBI_ERR_NOMEM, "out of host memory");
+  kv->cfg = *cfg;
+  dbi::KvGeom& g = kv->geom;
+  g.n_layers = static_cast<int>(cfg->n_layers);
+  g.cap = static_cast<int>(cap);
+  g.nkv = static_cast<int>(cfg->n_kv_heads);
+  g.hd = static_cast<int>(cfg->head_dim);
+  g.nb = (g.hd + dbi::kBlock - 1) / dbi::kBlock;
+  g.ring = cfg->window > 0;
+  g.int8 = cfg->dtype == DBI_KV_INT8;
+  g.window = static_cast<int>(cfg->window);
+  g.n_sink = static_cast<int>(cfg->n_sink);
+  g.ngroups = (g.cap + dbi::kKGroup - 1) / dbi::kKGroup;
+  (void)hipGetDevice(&kv->device);
+
+  const size_t cells = size_t(g.n_layers) * g.nkv * g.cap * g.hd;
+  const size_t scales = size_t(g.n_layers) * g.nkv * g.cap * g.nb;
+  dbi::KvStore& s = kv->store;
+  hipError_t e = hipSuccess;
+  auto A = [&](auto** p, size_t n) {
+    if (e == hipSuccess) e = dalloc(p, n);
+  };
+  if (!g.int8) {
+    A(&s.k, cells);
+    A(&s.v, cells);
+  } else {
+    A(&s.k8, cells);
+    A(&s.v8, cells);
+    A(&s.v_scale, scales);
+    if (g.ring) {
+      A(&s.k_scale, scales);
+    } else {
+      A(&s.k_scale, size_t(g.n_layers) * g.nkv * g.ngroups * g.hd);
+      A(&s.k_raw, size_t(g.n_layers) * dbi::kKGroup * g.nkv * g.hd);
+      if (g.n_sink > 0) {
+        A(&s.k_sink, size_t(g.n_layers) * g.nkv * g.n_sink * g.hd);
+        A(&s.v_sink, size_t(g.n_layers) * g.nkv * g.n_sink * g.hd);
+      }
+    }
+  }
+  if (e == hipSuccess && g.ring && g.hd >= 2) {
+    // cos/sin of every cache-relative rope position, evaluated in fp64 with the
+    // expressions of ops.cpp:27-30 and rounded to fp32
+    const int half = g.hd / 2;
+    std::vector<float2> tab(size_t(g.cap) * half);
+    for (int p = 0; p < g.cap; ++p)
+      for (int j = 0; j < half; ++j) {
+        const double inv = std::pow(static_cast<double>(cfg->rope_theta),
+                                    -2.0 * static_cast<double>(j) / static_cast<double>(g.hd));
+        const double ang = static_cast<double>(p) * inv;
+        tab[size_t(p) * half + j] = make_float2(static_cast<float>(std::cos(ang)),
+                                                static_cast<float>(std::sin(ang)));
+      }
+    A(&s.rope_cs, tab.size());
+    if (e == hipSuccess)
+      e = hipMemcpy(s.rope_cs, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice);
+  }
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&kv->own_stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    free_store(s);
+    delete kv;
+    return fail(e == hipErrorOutOfMemory ? DBI_ERR_NOMEM : DBI_ERR_DEVICE,
+                std::string("kv cache allocation failed: ") + hipGetErrorString(e));
+  }
+  kv->stream = kv->own_stream;
+  *out = kv;
+  return DBI_OK;
+}
+
+void dbi_kv_destroy(dbi_kv* kv) {
+  if (kv == nullptr) return;
+  (void)hipStreamSynchronize(kv->stream);
+  free_store(kv->store);
+  free_ws(kv->ws);
+  if (kv->own_stream) (void)hipStreamDestroy(kv->own_stream);
+  delete kv;
+}
+
+dbi_status dbi_kv_get_config(const dbi_kv* kv, dbi_kv_config* out) {
+  if (kv == nullptr || out == nullptr) return fail(DBI_ERR_INVALID, "null argument");
+  *out = kv->cfg;
+  return DBI_OK;
+}
+
+dbi_status dbi_kv_set_stream(dbi_kv* kv, void* hip_stream) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  kv->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : kv->own_stream;
+  return DBI_OK;
+}
+
+dbi_status dbi_kv_sync(dbi_kv* kv) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+  return DBI_OK;
+}
+
+dbi_status dbi_kv_append(dbi_kv* kv, uint32_t layer, uint32_t pos, const float* k,
+                         const float* v) {
+  return dbi_kv_append_n(kv, layer, pos, 1, k, v);
+}
+
+dbi_status dbi_kv_append_n(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, const float* k,
+                           const float* v) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (dbi_status st = append_check(kv, layer, pos0, n, k, v)) return st;
+  if (n == 0) return DBI_OK;
+  const size_t elems = size_t(n) * kv->cfg.n_kv_heads * kv->cfg.head_dim;
+  if (dbi_status st = need_staging(kv, 2 * elems)) return st;
+  float* kd = kv->ws.staging;
+  float* vd = kv->ws.staging + elems;
+  HIP_TRY(hipMemcpyAsync(kd, k, elems * sizeof(float), hipMemcpyHostToDevice, kv->stream),
+          "copy k");
+  HIP_TRY(hipMemcpyAsync(vd, v, elems * sizeof(float), hipMemcpyHostToDevice, kv->stream),
+          "copy v");
+  if (dbi_status st = append_impl(kv, layer, pos0, n, kd, vd)) return st;
+  HIP_TRY(hipStreamSynchronize(kv->stream), "append sync");
+  return DBI_OK;
+}
+
+dbi_status dbi_kv_append_async(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                               const float* k_dev, const float* v_dev) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (dbi_status st = append_check(kv, layer, pos0, n, k_dev, v_dev)) return st;
+  if (n == 0) return DBI_OK;
+  return append_impl(kv, layer, pos0, n, k_dev, v_dev);
+}
+
+dbi_status dbi_kv_truncate(dbi_kv* kv, uint32_t n_seen) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (!kv->geom.ring && n_seen > static_cast<uint32_t>(kv->geom.cap))
+    return fail(DBI_ERR_INVALID, "n_seen exceeds cache capacity");
+  kv->n_seen = n_seen;
+  return DBI_OK;
+}
+
+uint32_t dbi_kv_n_seen(const dbi_kv* kv) { return kv ? kv->n_seen : 0; }
+uint32_t dbi_kv_capacity(const dbi_kv* kv) { return kv ? static_cast<uint32_t>(kv->geom.cap) : 0; }
+
+dbi_status dbi_kv_slot_for(const dbi_kv* kv, uint32_t pos, uint32_t* slot) {
+  if (kv == nullptr || slot == nullptr) return fail(DBI_ERR_INVALID, "null argument");
+  if (!kv->geom.ring) return fail(DBI_ERR_UNSUPPORTED, "slot_for is defined for a ring only");
+  const uint32_t s = kv->cfg.n_sink, W = kv->cfg.window;
+  *slot = pos < s ? pos : s + (pos - s) % W;
+  return DBI_OK;
+}
+
+dbi_status dbi_kv_residents(const dbi_kv* kv, uint32_t* slot, int32_t* rope_pos, uint32_t cap,
+                            uint32_t* count) {
+  if (kv == nullptr || count == nullptr) return fail(DBI_ERR_INVALID, "null argument");
+  if (!kv->geom.ring) return fail(DBI_ERR_UNSUPPORTED, "residents is defined for a ring only");
+  const uint32_t s = kv->cfg.n_sink, W = kv->cfg.window, n_seen = kv->n_seen;
+  const uint32_t sinks = n_seen < s ? n_seen : s;
+  uint32_t ws = s;
+  if (n_seen > s && n_seen - s > W) ws = n_seen - W;
+  const uint32_t total = sinks + (n_seen > ws ? n_seen - ws : 0);
+  if (total > cap || (total > 0 && (slot == nullptr || rope_pos == nullptr)))
+    return fail(DBI_ERR_INVALID, "residents output too small");
+  uint32_t c = 0;
+  for (uint32_t t = 0; t < sinks; ++t) {
+    slot[c] = t;
+    rope_pos[c] = static_cast<int32_t>(t);
+    ++c;
+  }
+  for (uint32_t t = ws; t < n_seen; ++t) {
+    slot[c] = s + (t - s) % W;
+    rope_pos[c] = static_cast<int32_t>(s + (t - ws));
+    ++c;
+  }
+  *count = c;
+  return DBI_OK;
+}
+
+dbi_status dbi_attn_decode(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
+                           float scale, const float* q, float* out) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (dbi_status st = check_attend(kv, layer, n_heads, q, out)) return st;
+  const size_t elems = size_t(n_heads) * kv->cfg.head_dim;
+  if (dbi_status st = need_staging(kv, 2 * elems)) return st;
+  float* qd = kv->ws.staging;
+  float* od = kv->ws.staging + elems;
+  HIP_TRY(hipMemcpyAsync(qd, q, elems * sizeof(float), hipMemcpyHostToDevice, kv->stream),
+          "copy q");
+  if (dbi_status st = decode_impl(kv, layer, pos, n_heads, scale, qd, od)) return st;
+  HIP_TRY(hipMemcpyAsync(out, od, elems * sizeof(float), hipMemcpyDeviceToHost, kv->stream),
+          "copy out");
+  HIP_TRY(hipStreamSynchronize(kv->stream), "attention sync");
+  return DBI_OK;
+}
+
+dbi_status dbi_attn_decode_async(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
+                                 float scale, const float* q_dev, float* out_dev) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (dbi_status st = check_attend(kv, layer, n_heads, q_dev, out_dev)) return st;
+  return decode_impl(kv, layer, pos, n_heads, scale, q_dev, out_dev);
+}
+
+dbi_status dbi_attn_chunk(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                          uint32_t n_heads, float scale, const float* q, float* out) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (dbi_status st = check_attend(kv, layer, n_heads, q, out)) return st;
+  if (n == 0) return DBI_OK;
+  const size_t elems = size_t(n) * n_heads * kv->cfg.head_dim;
+  if (dbi_status st = need_staging(kv, 2 * elems)) return st;
+  float* qd = kv->ws.staging;
+  float* od = kv->ws.staging + elems;
+  HIP_TRY(hipMemcpyAsync(qd, q, elems * sizeof(float), hipMemcpyHostToDevice, kv->stream),
+          "copy q");
+  if (dbi_status st = chunk_impl(kv, layer, pos0, n, n_heads, scale, qd, od)) return st;
+  HIP_TRY(hipMemcpyAsync(out, od, elems * sizeof(float), hipMemcpyDeviceToHost, kv->stream),
+          "copy out");
+  HIP_TRY(hipStreamSynchronize(kv->stream), "attention sync");
+  return DBI_OK;
+}
+
+dbi_status dbi_attn_chunk_async(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                                uint32_t n_heads, float scale, const float* q_dev,
+                                float* out_dev) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (dbi_status st = check_attend(kv, layer, n_heads, q_dev, out_dev)) return st;
+  return chunk_impl(kv, layer, pos0, n, n_heads, scale, q_dev, out_dev);
+}
+
+// ---------------------------------------------------------------------------
+// prefix cache, DBKVCACH v1 (model.cpp:1023-1033): little-endian magic, u32
+// version, u32 n_layers, n_kv_heads, head_dim, prefix_len, i32 tokens, fp32 K
+// [L][len][nkv][hd], fp32 V in the same layout.
+
+static const unsigned char kMagic[8] = {'D', 'B', 'K', 'V', 'C', 'A', 'C', 'H'};
+static const uint32_t kVersion = 1;
+
+dbi_status dbi_kv_prefix_save(dbi_kv* kv, const char* path, const int32_t* tokens,
+                              uint32_t len) {
+  if (kv == nullptr || path == nullptr) return fail(DBI_ERR_INVALID, "null argument");
+  // checks in the order of model.cpp:1074-1079
+  if (kv->geom.ring || kv->geom.int8)
+    return fail(DBI_ERR_UNSUPPORTED, "kv prefix cache supports only the dense fp32 cache");
+  if (len == 0) return fail(DBI_ERR_INVALID, "kv prefix is empty");
+  if (tokens == nullptr) return fail(DBI_ERR_INVALID, "null tokens");
+  if (kv->n_seen < len) return fail(DBI_ERR_INVALID, "cache holds fewer positions than the prefix");
+
+  const dbi::KvGeom& g = kv->geom;
+  const size_t elems = size_t(g.n_layers) * len * g.nkv * g.hd;
+  const size_t hdr = 8 + 5 * 4 + size_t(len) * 4;
+  std::vector<unsigned char> buf;
+  try {
+    buf.resize(hdr + 2 * elems * sizeof(float));
+  } catch (...) {
+    return fail(DBI_ERR_NOMEM, "out of host memory");
+  }
+  std::memcpy(buf.data(), kMagic, 8);
+  const uint32_t h[5] = {kVersion, kv->cfg.n_layers, kv->cfg.n_kv_heads, kv->cfg.head_dim, len};
+  std::memcpy(buf.data() + 8, h, sizeof h);
+  std::memcpy(buf.data() + 28, tokens, size_t(len) * 4);
+
+  float* dev = nullptr;
+  if (hipMalloc(reinterpret_cast<void**>(&dev), elems * sizeof(float)) != hipSuccess)
+    return fail(DBI_ERR_NOMEM, "prefix staging allocation failed");
+  hipError_t e = dbi::launch_prefix_pack(g, kv->store.k, dev, static_cast<int>(len), kv->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(buf.data() + hdr, dev, elems * sizeof(float), hipMemcpyDeviceToHost,
+                       kv->stream);
+  if (e == hipSuccess)
+    e = dbi::launch_prefix_pack(g, kv->store.v, dev, static_cast<int>(len), kv->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(buf.data() + hdr + elems * sizeof(float), dev, elems * sizeof(float),
+                       hipMemcpyDeviceToHost, kv->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(kv->stream);
+  (void)hipFree(dev);
+  if (e != hipSuccess) return hip_fail(e, "prefix readback");
+
+  std::FILE* f = std::fopen(path, "wb");
+  if (f == nullptr)
+    return fail(DBI_ERR_IO, std::string("cannot open kv prefix cache for writing ") + path);
+  const size_t wrote = std::fwrite(buf.data(), 1, buf.size(), f);
+  const bool ok = wrote == buf.size() && std::ferror(f) == 0;
+  if (std::fclose(f) != 0 || !ok)
+    return fail(DBI_ERR_IO, std::string("write error on kv prefix cache ") + path);
+  return DBI_OK;
+}
+
+dbi_status dbi_kv_prefix_load(dbi_kv* kv, const char* path, const int32_t* tokens,
+                              uint32_t n_tokens, uint32_t* out_len) {
+  if (kv == nullptr || path == nullptr) return fail(DBI_ERR_INVALID, "null argument");
+  if (kv->geom.ring || kv->geom.int8)
+    return fail(DBI_ERR_UNSUPPORTED, "kv prefix cache supports only the dense fp32 cache");
+  std::FILE* f = std::fopen(path, "rb");
+  if (f == nullptr) return fail(DBI_ERR_IO, std::string("cannot open kv prefix cache ") + path);
+  std::vector<unsigned char> data;
+  {
+    unsigned char chunk[65536];
+    size_t got = 0;
+    while ((got = std::fread(chunk, 1, sizeof chunk, f)) > 0) data.insert(data.end(), chunk, chunk + got);
+  }
+  const bool rd_ok = std::ferror(f) == 0;
+  std::fclose(f);
+  if (!rd_ok) return fail(DBI_ERR_IO, std::string("read error on kv prefix cache ") + path);
+
+  // validation in the order of model.cpp:1117-1148
+  size_t p = 0;
+  auto need = [&](size_t n) { return p + n <= data.size(); };
+  for (int i = 0; i < 8; ++i) {
+    if (!need(1)) return fail(DBI_ERR_FORMAT, "kv prefix cache truncated");
+    if (data[p] != kMagic[i]) return fail(DBI_ERR_FORMAT, "kv prefix cache bad magic");
+    ++p;
+  }
+  uint32_t u[5];
+  for (int i = 0; i < 5; ++i) {
+    if (!need(4)) return fail(DBI_ERR_FORMAT, "kv prefix cache truncated");
+    std::memcpy(&u[i], data.data() + p, 4);
+    p += 4;
+    if (i == 0 && u[0] != kVersion)
+      return fail(DBI_ERR_FORMAT,
+                  "kv prefix cache version " + std::to_string(u[0]) + " unsupported");
+  }
+  const uint32_t n_layers = u[1], n_kv = u[2], hd = u[3], prefix_len = u[4];
+  if (n_layers != kv->cfg.n_layers || n_kv != kv->cfg.n_kv_heads || hd != kv->cfg.head_dim)
+    return fail(DBI_ERR_FORMAT, "kv prefix cache hyperparams do not match this model");
+  if (prefix_len == 0) return fail(DBI_ERR_FORMAT, "kv prefix cache has a zero-length prefix");
+  if (prefix_len > n_tokens) return fail(DBI_ERR_FORMAT, "kv prefix is longer than the prompt");
+  if (prefix_len > static_cast<uint32_t>(kv->geom.cap))
+    return fail(DBI_ERR_FORMAT, "kv prefix exceeds cache capacity");
+  if (tokens == nullptr) return fail(DBI_ERR_INVALID, "null tokens");
+  for (uint32_t i = 0; i < prefix_len; ++i) {
+    if (!need(4)) return fail(DBI_ERR_FORMAT, "kv prefix cache truncated");
+    int32_t saved;
+    std::memcpy(&saved, data.data() + p, 4);
+    p += 4;
+    if (saved != tokens[i])
+      return fail(DBI_ERR_FORMAT,
+                  "prompt prefix differs from saved cache at token " + std::to_string(i));
+  }
+  const dbi::KvGeom& g = kv->geom;
+  const size_t elems = size_t(g.n_layers) * prefix_len * g.nkv * g.hd;
+  if (p + 2 * elems * sizeof(float) != data.size())
+    return fail(DBI_ERR_FORMAT, "kv prefix cache payload size mismatch");
+
+  float* dev = nullptr;
+  if (hipMalloc(reinterpret_cast<void**>(&dev), 2 * elems * sizeof(float)) != hipSuccess)
+    return fail(DBI_ERR_NOMEM, "prefix staging allocation failed");
+  hipError_t e = hipMemcpyAsync(dev, data.data() + p, 2 * elems * sizeof(float),
+                                hipMemcpyHostToDevice, kv->stream);
+  if (e == hipSuccess)
+    e = dbi::launch_prefix_unpack(g, dev, kv->store.k, static_cast<int>(prefix_len), kv->stream);
+  if (e == hipSuccess)
+    e = dbi::launch_prefix_unpack(g, dev + elems, kv->store.v, static_cast<int>(prefix_len),
+                                  kv->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(kv->stream);
+  (void)hipFree(dev);
+  if (e != hipSuccess) return hip_fail(e, "prefix upload");
+  kv->n_seen = prefix_len;
+  if (out_len) *out_len = prefix_len;
+  return DBI_OK;
+}
+
+// ---------------------------------------------------------------------------
+// readback in the reference's layout
+
+size_t dbi_kv_export_bytes(const dbi_kv* kv, uint32_t what) {
+  if (kv == nullptr) return 0;
+  const dbi::KvGeom& g = kv->geom;
+  const size_t P = size_t(g.nkv) * g.hd;
+  switch (what) {
+    case DBI_EXPORT_K:
+    case DBI_EXPORT_V: return g.int8 ? 0 : size_t(g.cap) * P * 4;
+    case DBI_EXPORT_K8:
+    case DBI_EXPORT_V8: return g.int8 ? size_t(g.cap) * P : 0;
+    case DBI_EXPORT_V_SCALE: return g.int8 ? size_t(g.cap) * g.nkv * g.nb * 4 : 0;
+    case DBI_EXPORT_K_SCALE:
+      if (!g.int8) return 0;
+      return g.ring ? size_t(g.cap) * g.nkv * g.nb * 4 : size_t(g.ngroups) * P * 4;
+    case DBI_EXPORT_K_SINK:
+    case DBI_EXPORT_V_SINK: return (g.int8 && !g.ring) ? size_t(g.n_sink) * P * 4 : 0;
+    case DBI_EXPORT_K_RAW: return (g.int8 && !g.ring) ? size_t(dbi::kKGroup) * P * 4 : 0;
+    default: return 0;
+  }
+}
+
+dbi_status dbi_kv_export(dbi_kv* kv, uint32_t what, uint32_t layer, void* dst, size_t bytes) {
+  if (kv == nullptr || dst == nullptr) return fail(DBI_ERR_INVALID, "null argument");
+  if (dbi_status st = check_layer(kv, layer)) return st;
+  const size_t need = dbi_kv_export_bytes(kv, what);
+  if (need == 0) return fail(DBI_ERR_UNSUPPORTED, "array not present in this layout");
+  if (bytes != need) return fail(DBI_ERR_INVALID, "export size mismatch");
+  const dbi::KvGeom& g = kv->geom;
+  const dbi::KvStore& s = kv->store;
+  // head-major device arrays: [nkv][rows][inner] -> reference [rows][nkv][inner]
+  const void* src = nullptr;
+  size_t rows = 0, inner = 0, esz = 4;
+  bool head_major = true;
+  switch (what) {
+    case DBI_EXPORT_K: src = s.k; rows = g.cap; inner = g.hd; break;
+    case DBI_EXPORT_V: src = s.v; rows = g.cap; inner = g.hd; break;
+    case DBI_EXPORT_K8: src = s.k8; rows = g.cap; inner = g.hd; esz = 1; break;
+    case DBI_EXPORT_V8: src = s.v8; rows = g.cap; inner = g.hd; esz = 1; break;
+    case DBI_EXPORT_V_SCALE: src = s.v_scale; rows = g.cap; inner = g.nb; break;
+    case DBI_EXPORT_K_SCALE:
+      src = s.k_scale;
+      rows = g.ring ? g.cap : g.ngroups;
+      inner = g.ring ? g.nb : g.hd;
+      break;
+    case DBI_EXPORT_K_SINK: src = s.k_sink; rows = g.n_sink; inner = g.hd; break;
+    case DBI_EXPORT_V_SINK: src = s.v_sink; rows = g.n_sink; inner = g.hd; break;
+    case DBI_EXPORT_K_RAW: src = s.k_raw; rows = dbi::kKGroup; inner = g.hd; head_major = false; break;
+    default: return fail(DBI_ERR_UNSUPPORTED, "unknown export");
+  }
+  const size_t layer_bytes = size_t(g.nkv) * rows * inner * esz;
+  std::vector<unsigned char> tmp(layer_bytes);
+  hipError_t e = hipMemcpyAsync(tmp.data(), static_cast<const unsigned char*>(src) + layer * layer_bytes,
+                                layer_bytes, hipMemcpyDeviceToHost, kv->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(kv->stream);
+  if (e != hipSuccess) return hip_fail(e, "export readback");
+  unsigned char* out = static_cast<unsigned char*>(dst);
+  if (!head_major) {
+    std::memcpy(out, tmp.data(), layer_bytes);
+    return DBI_OK;
+  }
+  const size_t row_bytes = inner * esz;
+  for (size_t kh = 0; kh < size_t(g.nkv); ++kh)
+    for (size_t r = 0; r < rows; ++r)
+      std::memcpy(out + (r * g.nkv + kh) * row_bytes, tmp.data() + (kh * rows + r) * row_bytes,
+                  row_bytes);
+  return DBI_OK;
+}
+
+}  // extern "C"

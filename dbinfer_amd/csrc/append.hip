@@ -1,0 +1,225 @@
+// Append kernels: one launch writes n consecutive positions of one layer and
+// leaves the storage exactly as n sequential KVCache::append calls would
+// (model.cpp:357-404).
+//
+// Bit-exactness of the int8 paths rests on three facts: max|x| is
+// order-free, x / 127.0f and 1.0f / s are IEEE correctly rounded divisions
+// (HIP's default, never fast-math), and the code is round-half-away of one
+// fp32 product, clamped to [-127, 127] (quant_code below).
+#include "kv_internal.hpp"
+
+namespace dbi {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float max_f(float a, float b) { return (a < b) ? b : a; }
+
+// clamp(lround(x * inv), -127, 127) as glibc computes it on x86-64: lround of a
+// NaN, an infinity or |x| >= 2^63 yields LONG_MIN, which clamps to -127.
+__device__ __forceinline__ int8_t quant_code(float x, float inv) {
+  const float r = x * inv;
+  if (!(fabsf(r) < 9223372036854775808.0f)) return -127;
+  const float t = roundf(r);
+  return static_cast<int8_t>(t > 127.0f ? 127 : (t < -127.0f ? -127 : static_cast<int>(t)));
+}
+
+// quant_head of one block (model.cpp:303-317): block [0, len) of src.
+__device__ __forceinline__ void quant_block(const float* src, int len, int8_t* dst, float* scale) {
+  float max_abs = 0.0f;
+  for (int i = 0; i < len; ++i) max_abs = max_f(max_abs, fabsf(src[i]));
+  const float s = max_abs / 127.0f;
+  *scale = s;
+  const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+  for (int i = 0; i < len; ++i) dst[i] = quant_code(src[i], inv);
+}
+
+__device__ __forceinline__ int slot_for(int pos, int s, int W) {
+  return pos < s ? pos : s + (pos - s) % W;
+}
+
+// In a batch, a ring row is overwritten by row p + W when that row is in the
+// same batch; only the last writer of each slot stores (sequential result).
+__device__ __forceinline__ bool ring_row_final(int p, int end, int s, int W) {
+  return p < s || p + W >= end;
+}
+
+// fp32 copy into dense slot pos or ring slot slot_for(pos) (model.cpp:386-402).
+__global__ __launch_bounds__(kThreads) void append_f32_kernel(KvGeom g, float* kst, float* vst,
+                                                              int layer, int pos0, int n,
+                                                              const float* __restrict__ k,
+                                                              const float* __restrict__ v) {
+  const int P = g.nkv * g.hd;
+  const size_t total = static_cast<size_t>(n) * P;
+  for (size_t idx = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; idx < total;
+       idx += static_cast<size_t>(gridDim.x) * kThreads) {
+    const int r = static_cast<int>(idx / P);
+    const int c = static_cast<int>(idx % P);
+    const int p = pos0 + r;
+    int slot = p;
+    if (g.ring) {
+      if (!ring_row_final(p, pos0 + n, g.n_sink, g.window)) continue;
+      slot = slot_for(p, g.n_sink, g.window);
+    }
+    const int kh = c / g.hd, i = c % g.hd;
+    const size_t dst = ((static_cast<size_t>(layer) * g.nkv + kh) * g.cap + slot) * g.hd + i;
+    kst[dst] = k[idx];
+    vst[dst] = v[idx];
+  }
+}
+
+// Ring int8: quant_head of K and V per kv head into slot_for(pos)
+// (model.cpp:386-396). One thread per (row, kv head, block).
+__global__ __launch_bounds__(kThreads) void append_i8_ring_kernel(KvGeom g, KvStore s, int layer,
+                                                                  int pos0, int n,
+                                                                  const float* __restrict__ k,
+                                                                  const float* __restrict__ v) {
+  const int P = g.nkv * g.hd;
+  const size_t total = static_cast<size_t>(n) * g.nkv * g.nb;
+  for (size_t idx = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; idx < total;
+       idx += static_cast<size_t>(gridDim.x) * kThreads) {
+    const int b = static_cast<int>(idx % g.nb);
+    const int kh = static_cast<int>((idx / g.nb) % g.nkv);
+    const int r = static_cast<int>(idx / (static_cast<size_t>(g.nb) * g.nkv));
+    const int p = pos0 + r;
+    if (!ring_row_final(p, pos0 + n, g.n_sink, g.window)) continue;
+    const int slot = slot_for(p, g.n_sink, g.window);
+    const int start = b * kBlock;
+    const int len = min(kBlock, g.hd - start);
+    const size_t src = static_cast<size_t>(r) * P + kh * g.hd + start;
+    const size_t row = (static_cast<size_t>(layer) * g.nkv + kh) * g.cap + slot;
+    quant_block(k + src, len, s.k8 + row * g.hd + start, s.k_scale + row * g.nb + b);
+    quant_block(v + src, len, s.v8 + row * g.hd + start, s.v_scale + row * g.nb + b);
+  }
+}
+
+// Dense int8 (model.cpp:358-384). Blocks [0, n_kblocks) run the key side, one
+// thread per channel c of [0, n_kv*hd): for every 32-token group the batch
+// touches, in order, stage the group's new rows into k_raw[pos % 32] and
+// requantize the group over raw rows [0, within] that are not sinks
+// (requantize_kgroup, model.cpp:329-355). Each channel only ever reads and
+// writes its own column of k_raw, k_scale and k8, so threads never interact.
+// The remaining blocks run the value side, one thread per (row, kv head,
+// block): fp32 sink copy for pos < n_sink, else quant_head of V.
+__global__ __launch_bounds__(kThreads) void append_i8_dense_kernel(KvGeom g, KvStore s, int layer,
+                                                                   int pos0, int n, int n_kblocks,
+                                                                   const float* __restrict__ k,
+                                                                   const float* __restrict__ v) {
+  const int P = g.nkv * g.hd;
+  if (static_cast<int>(blockIdx.x) < n_kblocks) {
+    const int c = blockIdx.x * kThreads + threadIdx.x;
+    if (c >= P) return;
+    const int kh = c / g.hd, i = c % g.hd;
+    float* raw = s.k_raw + static_cast<size_t>(layer) * kKGroup * P + c;
+    const size_t head = static_cast<size_t>(layer) * g.nkv + kh;
+    const int end = pos0 + n;
+    int p = pos0;
+    while (p < end) {
+      const int grp = p / kKGroup;
+      const int first = grp * kKGroup;
+      const int hi = min(end - 1, first + kKGroup - 1);
+      for (int q = p; q <= hi; ++q)
+        raw[static_cast<size_t>(q % kKGroup) * P] = k[static_cast<size_t>(q - pos0) * P + c];
+      const int within = hi - first;
+      float mx = 0.0f;
+      for (int w = 0; w <= within; ++w)
+        if (first + w >= g.n_sink) mx = max_f(mx, fabsf(raw[static_cast<size_t>(w) * P]));
+      const float sc = mx / 127.0f;
+      s.k_scale[(head * g.ngroups + grp) * g.hd + i] = sc;
+      const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
+      for (int w = 0; w <= within; ++w) {
+        if (first + w < g.n_sink) continue;
+        s.k8[(head * g.cap + first + w) * g.hd + i] =
+            quant_code(raw[static_cast<size_t>(w) * P], inv);
+      }
+      p = hi + 1;
+    }
+    return;
+  }
+  const size_t idx = (blockIdx.x - n_kblocks) * static_cast<size_t>(kThreads) + threadIdx.x;
+  const size_t total = static_cast<size_t>(n) * g.nkv * g.nb;
+  if (idx >= total) return;
+  const int b = static_cast<int>(idx % g.nb);
+  const int kh = static_cast<int>((idx / g.nb) % g.nkv);
+  const int r = static_cast<int>(idx / (static_cast<size_t>(g.nb) * g.nkv));
+  const int p = pos0 + r;
+  const int start = b * kBlock;
+  const int len = min(kBlock, g.hd - start);
+  const size_t src = static_cast<size_t>(r) * P + kh * g.hd + start;
+  const size_t head = static_cast<size_t>(layer) * g.nkv + kh;
+  if (p < g.n_sink) {
+    const size_t dst = (head * g.n_sink + p) * g.hd + start;
+    for (int i = 0; i < len; ++i) {
+      s.k_sink[dst + i] = k[src + i];
+      s.v_sink[dst + i] = v[src + i];
+    }
+    return;
+  }
+  const size_t row = head * g.cap + p;
+  quant_block(v + src, len, s.v8 + row * g.hd + start, s.v_scale + row * g.nb + b);
+}
+
+int grid_for(size_t work) {
+  const size_t blocks = (work + kThreads - 1) / kThreads;
+  return static_cast<int>(blocks < 65536 ? (blocks == 0 ? 1 : blocks) : 65536);
+}
+
+// [L][len][nkv][hd] <-> [L][nkv][cap][hd]
+__global__ __launch_bounds__(kThreads) void prefix_pack_kernel(KvGeom g, const float* store,
+                                                               float* dst, int len, int unpack) {
+  const size_t P = static_cast<size_t>(g.nkv) * g.hd;
+  const size_t total = static_cast<size_t>(g.n_layers) * len * P;
+  for (size_t idx = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; idx < total;
+       idx += static_cast<size_t>(gridDim.x) * kThreads) {
+    const size_t l = idx / (len * P);
+    const size_t rem = idx % (len * P);
+    const size_t p = rem / P;
+    const size_t kh = (rem % P) / g.hd;
+    const size_t i = rem % g.hd;
+    const size_t st = ((l * g.nkv + kh) * g.cap + p) * g.hd + i;
+    if (unpack)
+      const_cast<float*>(store)[st] = dst[idx];
+    else
+      dst[idx] = store[st];
+  }
+}
+
+}  // namespace
+
+hipError_t launch_append(const KvGeom& g, const KvStore& s, int layer, int pos0, int n,
+                         const float* k, const float* v, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const size_t P = static_cast<size_t>(g.nkv) * g.hd;
+  if (!g.int8) {
+    hipLaunchKernelGGL(append_f32_kernel, dim3(grid_for(n * P)), dim3(kThreads), 0, st, g, s.k,
+                       s.v, layer, pos0, n, k, v);
+  } else if (g.ring) {
+    hipLaunchKernelGGL(append_i8_ring_kernel, dim3(grid_for(static_cast<size_t>(n) * g.nkv * g.nb)),
+                       dim3(kThreads), 0, st, g, s, layer, pos0, n, k, v);
+  } else {
+    const int n_kblocks = static_cast<int>((P + kThreads - 1) / kThreads);
+    const size_t vwork = static_cast<size_t>(n) * g.nkv * g.nb;
+    const int n_vblocks = static_cast<int>((vwork + kThreads - 1) / kThreads);
+    hipLaunchKernelGGL(append_i8_dense_kernel, dim3(n_kblocks + n_vblocks), dim3(kThreads), 0, st,
+                       g, s, layer, pos0, n, n_kblocks, k, v);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_prefix_pack(const KvGeom& g, const float* src_store, float* dst, int len,
+                              hipStream_t st) {
+  const size_t total = static_cast<size_t>(g.n_layers) * len * g.nkv * g.hd;
+  hipLaunchKernelGGL(prefix_pack_kernel, dim3(grid_for(total)), dim3(kThreads), 0, st, g,
+                     src_store, dst, len, 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefix_unpack(const KvGeom& g, const float* src, float* dst_store, int len,
+                                hipStream_t st) {
+  const size_t total = static_cast<size_t>(g.n_layers) * len * g.nkv * g.hd;
+  hipLaunchKernelGGL(prefix_pack_kernel, dim3(grid_for(total)), dim3(kThreads), 0, st, g,
+                     dst_store, const_cast<float*>(src), len, 1);
+  return hipGetLastError();
+}
+
+}  // namespace dbi

@@ -1,0 +1,191 @@
+"""Python handle over the C-ABI, named after the reference KVCache API.
+
+``HipKV`` mirrors ``dbinfer::model::KVCache`` (src/model/model.hpp:108-214):
+``append``, ``slot_for``, ``residents``, ``n_seen``, ``reset``,
+``mark_position``, ``capacity``; plus the attention entry points of
+``Model::attend_*`` (model.cpp:567-728) and the chunk attention of
+``decode_layer_chunk`` (model.cpp:956-981), and prefix save/load
+(model.cpp:1072-1156). Host-array methods take numpy float32 arrays; the
+``*_async`` methods take device pointers (e.g. ``torch.Tensor.data_ptr()``).
+Every call goes through libdbi_kv.so; failures raise ``DbiError``.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+
+F32 = _lib.DBI_KV_F32
+INT8 = _lib.DBI_KV_INT8
+
+
+class DbiError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[dbi status {status}] {message}")
+        self.status = status
+        self.message = message
+
+
+def _check(lib, st: int) -> None:
+    if st != _lib.DBI_OK:
+        raise DbiError(st, lib.dbi_last_error().decode())
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+class HipKV:
+    """KV cache of one model on the current HIP device."""
+
+    def __init__(self, n_layers: int, max_seq: int, n_kv_heads: int, head_dim: int,
+                 n_sink: int = 0, window: int = 0, dtype: int = F32, rope_theta: float = 1e4):
+        self._lib = _lib.load()
+        cfg = _lib.KvConfig(n_layers, max_seq, n_kv_heads, head_dim, n_sink, window, dtype,
+                            rope_theta)
+        h = ctypes.c_void_p()
+        _check(self._lib, self._lib.dbi_kv_create(ctypes.byref(cfg), ctypes.byref(h)))
+        self._h = h
+        self.n_layers, self.n_kv_heads, self.head_dim = n_layers, n_kv_heads, head_dim
+        self.n_sink, self.window, self.dtype, self.rope_theta = n_sink, window, dtype, rope_theta
+        self.pos_stride = n_kv_heads * head_dim
+        self.n_blocks = (head_dim + 31) // 32
+
+    # ---- lifetime
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.dbi_kv_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    # ---- state
+    @property
+    def capacity(self) -> int:
+        return int(self._lib.dbi_kv_capacity(self._h))
+
+    @property
+    def n_seen(self) -> int:
+        return int(self._lib.dbi_kv_n_seen(self._h))
+
+    def ring(self) -> bool:
+        return self.window > 0
+
+    def int8(self) -> bool:
+        return self.dtype == INT8
+
+    def truncate(self, n_seen: int) -> None:
+        _check(self._lib, self._lib.dbi_kv_truncate(self._h, n_seen))
+
+    def reset(self) -> None:
+        self.truncate(0)
+
+    def mark_position(self, pos: int) -> None:
+        self.truncate(pos + 1)
+
+    def set_stream(self, stream_ptr: int | None) -> None:
+        _check(self._lib, self._lib.dbi_kv_set_stream(self._h, stream_ptr or None))
+
+    def sync(self) -> None:
+        _check(self._lib, self._lib.dbi_kv_sync(self._h))
+
+    # ---- append
+    def append(self, layer: int, pos: int, k, v) -> None:
+        k, v = _f32(k), _f32(v)
+        assert k.size == self.pos_stride and v.size == self.pos_stride
+        _check(self._lib, self._lib.dbi_kv_append(self._h, layer, pos, _ptr(k), _ptr(v)))
+
+    def append_n(self, layer: int, pos0: int, k, v) -> None:
+        k, v = _f32(k), _f32(v)
+        n = k.size // self.pos_stride
+        assert k.size == n * self.pos_stride and v.size == k.size
+        _check(self._lib, self._lib.dbi_kv_append_n(self._h, layer, pos0, n, _ptr(k), _ptr(v)))
+
+    def append_async(self, layer: int, pos0: int, n: int, k_dev: int, v_dev: int) -> None:
+        _check(self._lib, self._lib.dbi_kv_append_async(self._h, layer, pos0, n, k_dev, v_dev))
+
+    # ---- ring mapping
+    def slot_for(self, pos: int) -> int:
+        out = ctypes.c_uint32()
+        _check(self._lib, self._lib.dbi_kv_slot_for(self._h, pos, ctypes.byref(out)))
+        return int(out.value)
+
+    def residents(self) -> tuple[np.ndarray, np.ndarray]:
+        cap = self.capacity
+        slot = np.zeros(cap, np.uint32)
+        rp = np.zeros(cap, np.int32)
+        cnt = ctypes.c_uint32()
+        _check(self._lib, self._lib.dbi_kv_residents(self._h, _ptr(slot), _ptr(rp), cap,
+                                                     ctypes.byref(cnt)))
+        return slot[: cnt.value].copy(), rp[: cnt.value].copy()
+
+    # ---- attention
+    def attend(self, layer: int, pos: int, q, n_heads: int, scale: float) -> np.ndarray:
+        q = _f32(q)
+        assert q.size == n_heads * self.head_dim
+        out = np.empty(n_heads * self.head_dim, np.float32)
+        _check(self._lib, self._lib.dbi_attn_decode(self._h, layer, pos, n_heads, scale, _ptr(q),
+                                                    _ptr(out)))
+        return out
+
+    def attend_async(self, layer: int, pos: int, n_heads: int, scale: float, q_dev: int,
+                     out_dev: int) -> None:
+        _check(self._lib, self._lib.dbi_attn_decode_async(self._h, layer, pos, n_heads, scale,
+                                                          q_dev, out_dev))
+
+    def attend_chunk(self, layer: int, pos0: int, q, n_heads: int, scale: float) -> np.ndarray:
+        q = _f32(q)
+        n = q.size // (n_heads * self.head_dim)
+        assert q.size == n * n_heads * self.head_dim
+        out = np.empty(q.size, np.float32)
+        _check(self._lib, self._lib.dbi_attn_chunk(self._h, layer, pos0, n, n_heads, scale,
+                                                   _ptr(q), _ptr(out)))
+        return out
+
+    def attend_chunk_async(self, layer: int, pos0: int, n: int, n_heads: int, scale: float,
+                           q_dev: int, out_dev: int) -> None:
+        _check(self._lib, self._lib.dbi_attn_chunk_async(self._h, layer, pos0, n, n_heads, scale,
+                                                         q_dev, out_dev))
+
+    # ---- prefix cache
+    def save_prefix(self, path: str, tokens) -> None:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        _check(self._lib, self._lib.dbi_kv_prefix_save(self._h, path.encode(), _ptr(t), t.size))
+
+    def load_prefix(self, path: str, tokens) -> int:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        n = ctypes.c_uint32()
+        _check(self._lib, self._lib.dbi_kv_prefix_load(self._h, path.encode(), _ptr(t), t.size,
+                                                       ctypes.byref(n)))
+        return int(n.value)
+
+    # ---- readback in the reference layout
+    def export(self, what: str, layer: int) -> np.ndarray:
+        code = _lib.EXPORT[what]
+        nbytes = int(self._lib.dbi_kv_export_bytes(self._h, code))
+        if nbytes == 0:
+            raise DbiError(_lib.DBI_ERR_UNSUPPORTED, f"{what} not present in this layout")
+        dt = np.int8 if what in ("k8", "v8") else np.float32
+        out = np.empty(nbytes // np.dtype(dt).itemsize, dt)
+        _check(self._lib, self._lib.dbi_kv_export(self._h, code, layer, _ptr(out), nbytes))
+        return out

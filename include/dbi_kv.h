@@ -1,0 +1,177 @@
+/*
+ * dbi_kv.h -- C-ABI of the MI355X KV-cache + attention hot path.
+ *
+ * This is the drop-in boundary for the reference engine's KV cache
+ * (src/model/model.hpp:102-214, src/model/model.cpp:258-474), its three
+ * single-query attention kernels and the causal chunk attention
+ * (model.cpp:567-728, 956-981), and its prefix cache I/O
+ * (model.cpp:1023-1156). Plain C types only; no exceptions cross it.
+ *
+ * Conventions
+ *  - Every entry point returns a dbi_status. On failure the handle's state is
+ *    unchanged and dbi_last_error() (thread-local) holds a message, so the
+ *    caller can fall back to its CPU path (the reference's own pattern on a
+ *    backend error, model.cpp:887-907).
+ *  - Plain entry points take HOST pointers, block until the results are in the
+ *    caller's buffers, and are what a CPU call site swaps in. The *_async
+ *    variants take DEVICE pointers and enqueue on the handle's HIP stream.
+ *  - Element layouts are the reference's: k, v per position [n_kv_heads][head_dim]
+ *    (model.hpp:117-122), q and out [n_heads][head_dim] (model.cpp:574-600).
+ *  - One handle per host thread; calls on a handle are ordered on its stream
+ *    (the reference KVCache is not thread-safe either).
+ */
+#ifndef DBI_KV_H
+#define DBI_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DBI_KV_ABI_VERSION 1
+
+typedef struct dbi_kv dbi_kv;
+typedef int32_t dbi_status;
+
+enum {
+  DBI_OK = 0,
+  DBI_ERR_INVALID = 1,     /* bad argument: null pointer, layer/pos out of range */
+  DBI_ERR_UNSUPPORTED = 2, /* layout or shape this entry point does not serve */
+  DBI_ERR_NOMEM = 3,       /* device or host allocation failed */
+  DBI_ERR_DEVICE = 4,      /* HIP runtime error */
+  DBI_ERR_IO = 5,          /* prefix file open/read/write failed */
+  DBI_ERR_FORMAT = 6       /* prefix file failed validation */
+};
+
+/* KvDtype (model.hpp:78) */
+enum { DBI_KV_F32 = 0, DBI_KV_INT8 = 1 };
+
+/* KvPolicy (model.hpp:96-100) plus the cache geometry the KVCache constructor
+ * takes (model.hpp:119-120) and the rope base the ring path needs
+ * (Config::rope_theta, model.hpp:30). */
+typedef struct dbi_kv_config {
+  uint32_t n_layers;
+  uint32_t max_seq;    /* dense capacity; ignored when window > 0 */
+  uint32_t n_kv_heads;
+  uint32_t head_dim;
+  uint32_t n_sink;     /* ring: pinned sinks; dense int8: fp32 sink tokens */
+  uint32_t window;     /* 0 = dense full-context cache, > 0 = ring of n_sink + window */
+  uint32_t dtype;      /* DBI_KV_F32 or DBI_KV_INT8 */
+  float rope_theta;    /* ring only: rope base for cache-relative re-rope */
+} dbi_kv_config;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* dbi_last_error(void);
+
+/* KVCache::KVCache (model.hpp:119-120, model.cpp:258-297) and
+ * Model::configure_kv (model.hpp:284). Allocates and zero-fills all device
+ * storage on the current HIP device. */
+dbi_status dbi_kv_create(const dbi_kv_config* cfg, dbi_kv** out);
+void dbi_kv_destroy(dbi_kv* kv);
+dbi_status dbi_kv_get_config(const dbi_kv* kv, dbi_kv_config* out);
+
+/* Use this HIP stream (a hipStream_t) for every later call; NULL = the
+ * handle's own stream. */
+dbi_status dbi_kv_set_stream(dbi_kv* kv, void* hip_stream);
+/* Block until all work enqueued on the handle's stream has finished. */
+dbi_status dbi_kv_sync(dbi_kv* kv);
+
+/* KVCache::append (model.hpp:122, model.cpp:357-404): one position of every
+ * kv head of one layer; k, v are host [n_kv_heads*head_dim]. Int8 layouts
+ * quantize on append (dense: per-channel K over 32-token groups + per-block V
+ * + fp32 sinks; ring: per-block K and V). Sets n_seen = pos + 1. */
+dbi_status dbi_kv_append(dbi_kv* kv, uint32_t layer, uint32_t pos, const float* k,
+                         const float* v);
+/* n sequential appends at pos0..pos0+n-1 (the append loop of
+ * decode_layer_chunk, model.cpp:935-954); k, v host [n][n_kv_heads*head_dim].
+ * The final state equals n calls of dbi_kv_append. */
+dbi_status dbi_kv_append_n(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                           const float* k, const float* v);
+/* As dbi_kv_append_n with device pointers, enqueued on the handle's stream. */
+dbi_status dbi_kv_append_async(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                               const float* k_dev, const float* v_dev);
+
+/* Sets n_seen. reset() (model.hpp:164) is truncate(0), mark_position(p)
+ * (model.hpp:182-184) is truncate(p+1), and a speculative rollback
+ * (speculative.cpp:82) is truncate(pos + accepted + 1). Slots past n_seen are
+ * not scrubbed: the next append overwrites them, exactly as in the reference. */
+dbi_status dbi_kv_truncate(dbi_kv* kv, uint32_t n_seen);
+uint32_t dbi_kv_n_seen(const dbi_kv* kv);   /* KVCache::n_seen (model.hpp:161) */
+uint32_t dbi_kv_capacity(const dbi_kv* kv); /* KVCache::capacity (model.hpp:160) */
+
+/* KVCache::slot_for (model.hpp:171, model.cpp:321-324); ring only. */
+dbi_status dbi_kv_slot_for(const dbi_kv* kv, uint32_t pos, uint32_t* slot);
+/* KVCache::residents (model.hpp:175, model.cpp:406-418); ring only. Writes up
+ * to cap entries (sinks first, then the window oldest to newest) and the
+ * count. */
+dbi_status dbi_kv_residents(const dbi_kv* kv, uint32_t* slot, int32_t* rope_pos, uint32_t cap,
+                            uint32_t* count);
+
+/* Single-query GQA attention of one layer at position pos, for the cache's
+ * layout: Model::attend_dense_f32 (model.cpp:567-603), attend_dense_int8
+ * (model.cpp:605-660) or attend_ring (model.cpp:662-728), and the dense-only
+ * Backend::attention seam (backend.hpp:126-131). q, out host [n_heads*head_dim];
+ * scale is the caller's 1/sqrt(head_dim) (model.cpp:757). Dense layouts read
+ * positions [0, pos] with q already roped (model.cpp:759-763). A ring reads
+ * the residents of n_seen = pos + 1 (append pos first, as model.cpp:668 does),
+ * and q is un-roped: it is roped at n_res - 1 and every resident key at its
+ * cache-relative position (model.cpp:669-700). */
+dbi_status dbi_attn_decode(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
+                           float scale, const float* q, float* out);
+dbi_status dbi_attn_decode_async(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
+                                 float scale, const float* q_dev, float* out_dev);
+
+/* Causal chunk attention of decode_layer_chunk (model.cpp:956-981): row c of
+ * q [n][n_heads][head_dim] attends [0, pos0 + c] and writes row c of out.
+ * Every row must have been appended first (model.cpp:933-954). Dense fp32
+ * and dense int8 (rows attend with the int8 rule of model.cpp:605-660 over
+ * the cache as it stands after all n appends); rings are not served. */
+dbi_status dbi_attn_chunk(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                          uint32_t n_heads, float scale, const float* q, float* out);
+dbi_status dbi_attn_chunk_async(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                                uint32_t n_heads, float scale, const float* q_dev,
+                                float* out_dev);
+
+/* Model::save_kv_prefix (model.hpp:292-293, model.cpp:1072-1107): writes the
+ * DBKVCACH v1 file of positions [0, len) with the token ids. Dense fp32 only. */
+dbi_status dbi_kv_prefix_save(dbi_kv* kv, const char* path, const int32_t* tokens,
+                              uint32_t len);
+/* Model::load_kv_prefix (model.hpp:298-299, model.cpp:1109-1156): validates
+ * magic, version, hyperparameters, length, token ids and exact size in the
+ * reference's order, then restores K/V and sets n_seen = prefix length
+ * (written to *out_len). Leaves the cache untouched on any error. */
+dbi_status dbi_kv_prefix_load(dbi_kv* kv, const char* path, const int32_t* tokens,
+                              uint32_t n_tokens, uint32_t* out_len);
+
+/* Read back one layer of a storage array in the reference's layout, for
+ * bit-exact comparison with the CPU path. Mirrors the accessors of
+ * model.cpp:420-455. Shapes (per layer):
+ *   DBI_EXPORT_K, _V            fp32 [capacity][n_kv][head_dim]    (fp32 layouts)
+ *   DBI_EXPORT_K8, _V8          int8 [capacity][n_kv][head_dim]    (int8 layouts)
+ *   DBI_EXPORT_V_SCALE          fp32 [capacity][n_kv][n_blocks]    (int8)
+ *   DBI_EXPORT_K_SCALE          ring int8: fp32 [capacity][n_kv][n_blocks];
+ *                               dense int8: fp32 [n_groups][n_kv][head_dim]
+ *   DBI_EXPORT_K_SINK, _V_SINK  fp32 [n_sink][n_kv][head_dim]      (dense int8)
+ *   DBI_EXPORT_K_RAW            fp32 [32][n_kv][head_dim]          (dense int8)
+ * bytes must equal the array's size (dbi_kv_export_bytes). */
+enum {
+  DBI_EXPORT_K = 0,
+  DBI_EXPORT_V = 1,
+  DBI_EXPORT_K8 = 2,
+  DBI_EXPORT_V8 = 3,
+  DBI_EXPORT_K_SCALE = 4,
+  DBI_EXPORT_V_SCALE = 5,
+  DBI_EXPORT_K_SINK = 6,
+  DBI_EXPORT_V_SINK = 7,
+  DBI_EXPORT_K_RAW = 8
+};
+size_t dbi_kv_export_bytes(const dbi_kv* kv, uint32_t what);
+dbi_status dbi_kv_export(dbi_kv* kv, uint32_t what, uint32_t layer, void* dst, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DBI_KV_H */

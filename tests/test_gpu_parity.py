@@ -1,0 +1,274 @@
+"""GPU parity of the HIP path (through the C-ABI) against the CPU oracle, on
+identical seeded inputs fed from one host buffer.
+
+Bar: int8 codes, scales, sinks, raw staging, ring slots/residents and
+rollback state bit-exact; fp32 attention |a - b| <= 1e-5 + 1e-4 |b|.
+Shapes cover tests/metal_ops_test.cpp:164-170 (nh/nkv 14/2, 8/8; hd 64/128;
+n_pos 1, 2, 64, 300) and every gqa factor of the five configs (8, 4, 3, 7, 4).
+"""
+import numpy as np
+import pytest
+
+import pyoracle
+from dbinfer_amd.kv import F32, INT8, DbiError, HipKV
+from helpers import assert_close, normal
+
+pytestmark = pytest.mark.gpu
+
+
+def scale_of(hd):
+    return np.float32(1.0) / np.sqrt(np.float32(hd))
+
+
+def pair(L, cap, nkv, hd, n_sink=0, window=0, dtype=F32, theta=1e4):
+    return (HipKV(L, cap, nkv, hd, n_sink, window, dtype, theta),
+            pyoracle.OracleKV(L, cap, nkv, hd, n_sink, window, dtype, theta))
+
+
+def same_bits(a, b, what):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.shape == b.shape, (what, a.shape, b.shape)
+    if a.dtype == np.float32:
+        a, b = a.view(np.uint32), b.view(np.uint32)
+    diff = np.nonzero(a != b)[0]
+    assert diff.size == 0, f"{what}: {diff.size} differing elements, first at {diff[:5]}"
+
+
+def compare_store(g, o, layers, names):
+    for l in layers:
+        for n in names:
+            same_bits(g.export(n, l), o.export(n, l), f"{n} layer {l}")
+
+
+# ---------------------------------------------------------------- append
+
+
+@pytest.mark.parametrize("hd", [64, 128, 40])
+def test_append_dense_f32(hd):
+    g, o = pair(2, 50, 3, hd)
+    K, V = normal(1, 2, 50, 3 * hd), normal(2, 2, 50, 3 * hd)
+    for l in range(2):
+        for p in range(37):
+            g.append(l, p, K[l, p], V[l, p])
+            o.append(l, p, K[l, p], V[l, p])
+        g.append_n(l, 37, K[l, 37:50], V[l, 37:50])
+        o.append_n(l, 37, K[l, 37:50], V[l, 37:50])
+    assert g.n_seen == o.n_seen == 50
+    compare_store(g, o, [0, 1], ["k", "v"])
+
+
+INT8_DENSE = ["k8", "v8", "k_scale", "v_scale", "k_raw"]
+
+
+@pytest.mark.parametrize("hd,nkv,n_sink", [(128, 8, 4), (64, 2, 0), (40, 3, 4), (128, 1, 37)])
+def test_append_int8_dense_bit_exact(hd, nkv, n_sink):
+    L, cap = 2, 130
+    g, o = pair(L, cap, nkv, hd, n_sink=n_sink, dtype=INT8)
+    P = nkv * hd
+    K, V = normal(3, L, cap, P), normal(4, L, cap, P)
+    K[:, :, 7] *= 8.0  # outlier channel
+    V[:, :, 3] *= 8.0
+    K[:, 60, :32] = 0.0  # zero block / zero rows
+    names = INT8_DENSE + (["k_sink", "v_sink"] if n_sink else [])
+    for l in range(L):
+        for p in range(45):  # one by one, crossing a group boundary
+            g.append(l, p, K[l, p], V[l, p])
+            o.append(l, p, K[l, p], V[l, p])
+        compare_store(g, o, [l], names)
+        g.append_n(l, 45, K[l, 45:110], V[l, 45:110])  # batch over 3 groups
+        o.append_n(l, 45, K[l, 45:110], V[l, 45:110])
+        compare_store(g, o, [l], names)
+
+
+def test_int8_rollback_across_group_boundary():
+    """Rollback then re-append: the staging-row aliasing of the reference
+    (k_raw indexed by pos % 32) is reproduced bit for bit."""
+    L, cap, nkv, hd = 1, 96, 2, 64
+    g, o = pair(L, cap, nkv, hd, n_sink=4, dtype=INT8)
+    P = nkv * hd
+    K, V = normal(5, 80, P), normal(6, 80, P)
+    for p in range(41):
+        g.append(0, p, K[p], V[p])
+        o.append(0, p, K[p], V[p])
+    for kv in (g, o):
+        kv.truncate(30)
+    assert g.n_seen == o.n_seen == 30
+    knew, vnew = normal(7, 5, P), normal(8, 5, P)
+    g.append_n(0, 30, knew, vnew)  # crosses back into group 1
+    for r in range(5):
+        o.append(0, 30 + r, knew[r], vnew[r])
+    compare_store(g, o, [0], INT8_DENSE + ["k_sink", "v_sink"])
+
+
+@pytest.mark.parametrize("dtype", [F32, INT8])
+@pytest.mark.parametrize("n_sink,window", [(4, 16), (0, 8), (2, 5)])
+def test_ring_append_slots_residents(dtype, n_sink, window):
+    nkv, hd = 2, 64
+    g, o = pair(1, 0, nkv, hd, n_sink, window, dtype, 1e6)
+    P = nkv * hd
+    K, V = normal(9, 120, P), normal(10, 120, P)
+    names = ["k", "v"] if dtype == F32 else ["k8", "v8", "k_scale", "v_scale"]
+    for t in range(60):
+        g.append(0, t, K[t], V[t])
+        o.append(0, t, K[t], V[t])
+        assert g.slot_for(t) == o.slot_for(t)
+        gs, gr = g.residents()
+        os_, or_ = o.residents()
+        same_bits(gs, os_, "slots")
+        same_bits(gr, or_, "rope_pos")
+    compare_store(g, o, [0], names)
+    g.append_n(0, 60, K[60:120], V[60:120])  # batch longer than the window
+    o.append_n(0, 60, K[60:120], V[60:120])
+    compare_store(g, o, [0], names)
+    for kv in (g, o):
+        kv.truncate(100)
+    same_bits(g.residents()[0], o.residents()[0], "slots after rollback")
+
+
+# ---------------------------------------------------------------- decode
+
+
+def fill_both(g, o, L, n, seed, outlier=False):
+    P = g.pos_stride
+    K, V = normal(seed, L, n, P), normal(seed + 1, L, n, P)
+    if outlier:
+        ch = np.random.default_rng(seed).choice(P, max(1, P // 100), replace=False)
+        K[:, :, ch] *= 8.0
+        V[:, :, ch] *= 8.0
+    for l in range(L):
+        g.append_n(l, 0, K[l], V[l])
+        o.append_n(l, 0, K[l], V[l])
+    return K, V
+
+
+@pytest.mark.parametrize("nh,nkv", [(14, 2), (8, 8), (32, 4), (32, 8), (24, 8), (28, 4)])
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("n_pos", [1, 2, 64, 300])
+def test_decode_dense_f32(nh, nkv, hd, n_pos):
+    g, o = pair(1, 320, nkv, hd)
+    fill_both(g, o, 1, n_pos, 20 + n_pos)
+    q = normal(21, nh * hd)
+    got = g.attend(0, n_pos - 1, q, nh, scale_of(hd))
+    want = o.attend(0, n_pos - 1, q, nh, scale_of(hd))
+    assert_close(got, want, what=f"nh{nh} nkv{nkv} hd{hd} n{n_pos}")
+
+
+@pytest.mark.parametrize("nh,nkv,hd", [(24, 8, 128), (32, 8, 128), (32, 4, 64), (28, 4, 128),
+                                       (8, 8, 64)])
+@pytest.mark.parametrize("n_sink", [0, 4])
+@pytest.mark.parametrize("n_pos", [1, 3, 33, 300, 1000])
+def test_decode_dense_int8(nh, nkv, hd, n_sink, n_pos):
+    g, o = pair(1, 1024, nkv, hd, n_sink=n_sink, dtype=INT8)
+    fill_both(g, o, 1, n_pos, 30 + n_pos, outlier=True)
+    q = normal(31, nh * hd)
+    got = g.attend(0, n_pos - 1, q, nh, scale_of(hd))
+    want = o.attend(0, n_pos - 1, q, nh, scale_of(hd))
+    assert_close(got, want, what=f"int8 nh{nh} nkv{nkv} hd{hd} sink{n_sink} n{n_pos}")
+
+
+@pytest.mark.parametrize("dtype", [F32, INT8])
+@pytest.mark.parametrize("nh,nkv,hd,n_sink,window", [(28, 4, 128, 4, 64), (8, 2, 64, 0, 40),
+                                                     (32, 8, 128, 4, 100)])
+def test_decode_ring_stream(dtype, nh, nkv, hd, n_sink, window):
+    """Stream past several wraps with a decode every step (config 4 pattern)."""
+    g, o = pair(1, 0, nkv, hd, n_sink, window, dtype, 1e6)
+    steps = 3 * (n_sink + window) + 7
+    for t in range(steps):
+        q = normal(100 + t, nh * hd)
+        k = normal(200 + t, nkv * hd)
+        v = normal(300 + t, nkv * hd)
+        g.append(0, t, k, v)
+        got = g.attend(0, t, q, nh, scale_of(hd))
+        want = o.attend_ring(0, t, q, k, v, nh, scale_of(hd))
+        assert_close(got, want, what=f"ring step {t}")
+
+
+# ---------------------------------------------------------------- chunk
+
+
+@pytest.mark.parametrize("dtype", [F32, INT8])
+@pytest.mark.parametrize("nh,nkv,hd,pos0,n", [(32, 8, 64, 0, 64), (32, 8, 64, 256, 100),
+                                              (32, 8, 128, 2047, 5), (24, 8, 128, 70, 9),
+                                              (14, 2, 64, 3, 1)])
+def test_chunk_attention(dtype, nh, nkv, hd, pos0, n):
+    g, o = pair(1, 2100, nkv, hd, n_sink=4, dtype=dtype)
+    fill_both(g, o, 1, pos0 + n, 40 + n)
+    q = normal(41, n, nh * hd)
+    got = g.attend_chunk(0, pos0, q, nh, scale_of(hd))
+    want = o.attend_chunk(0, pos0, q, nh, scale_of(hd))
+    assert_close(got, want, what=f"chunk dtype{dtype} pos0 {pos0} n {n}")
+
+
+# ---------------------------------------------------------------- long context
+
+
+@pytest.mark.parametrize("dtype,nh,nkv,hd,n_pos", [
+    (INT8, 24, 8, 128, 8192),   # config 3 shape at its context
+    (F32, 24, 8, 128, 8192),
+    (F32, 32, 8, 128, 16384),   # config 5 shape at its final context
+    (F32, 32, 4, 64, 1025),     # config 1 shape
+])
+def test_decode_long_context(dtype, nh, nkv, hd, n_pos):
+    g, o = pair(1, n_pos, nkv, hd, n_sink=4, dtype=dtype)
+    fill_both(g, o, 1, n_pos, 50, outlier=dtype == INT8)
+    if dtype == INT8:
+        compare_store(g, o, [0], INT8_DENSE + ["k_sink", "v_sink"])
+    for pos in (n_pos - 1, n_pos // 2 + 5):
+        q = normal(51 + pos, nh * hd)
+        got = g.attend(0, pos, q, nh, scale_of(hd))
+        want = o.attend(0, pos, q, nh, scale_of(hd), n_threads=8)
+        assert_close(got, want, what=f"long ctx pos {pos}")
+
+
+# ---------------------------------------------------------------- prefix + errors
+
+
+def test_prefix_save_load_matches_oracle(tmp_path):
+    L, cap, nkv, hd = 3, 64, 2, 64
+    g, o = pair(L, cap, nkv, hd)
+    fill_both(g, o, L, 40, 60)
+    toks = np.arange(1000, 1030, dtype=np.int32)
+    gp, op = str(tmp_path / "g.kv"), str(tmp_path / "o.kv")
+    g.save_prefix(gp, toks)
+    o.save_prefix(op, toks)
+    assert open(gp, "rb").read() == open(op, "rb").read()
+    fresh = HipKV(L, cap, nkv, hd)
+    assert fresh.load_prefix(op, np.concatenate([toks, [1, 2]])) == 30
+    assert fresh.n_seen == 30
+    for l in range(L):
+        got = fresh.export("k", l).reshape(cap, -1)[:30]
+        same_bits(got, o.export("k", l).reshape(cap, -1)[:30], f"k layer {l}")
+    # error leaves the GPU cache untouched
+    bad = str(tmp_path / "bad.kv")
+    open(bad, "wb").write(open(op, "rb").read()[:-4])
+    before = fresh.export("v", 1)
+    with pytest.raises(DbiError) as e:
+        fresh.load_prefix(bad, toks)
+    assert e.value.message == "kv prefix cache payload size mismatch"
+    assert fresh.n_seen == 30
+    same_bits(fresh.export("v", 1), before, "v untouched")
+    with pytest.raises(DbiError) as e:
+        fresh.load_prefix(op, toks[:10])
+    assert e.value.message == "kv prefix is longer than the prompt"
+
+
+def test_abi_errors_leave_state():
+    g = HipKV(2, 16, 2, 64)
+    k = normal(1, 128)
+    g.append(0, 3, k, k)
+    with pytest.raises(DbiError):
+        g.append(2, 0, k, k)  # layer out of range
+    with pytest.raises(DbiError):
+        g.append(0, 16, k, k)  # past capacity
+    with pytest.raises(DbiError):
+        g.attend(0, 3, normal(2, 3 * 64), 3, 0.125)  # 3 heads over 2 kv heads
+    with pytest.raises(DbiError) as e:
+        g.attend(0, 3, normal(2, 40 * 64), 40, 0.125)  # gqa 20: no kernel
+    assert e.value.status == 2
+    with pytest.raises(DbiError):
+        g.residents()  # dense cache has no ring mapping
+    assert g.n_seen == 4
+    i8 = HipKV(1, 16, 1, 64, dtype=INT8)
+    with pytest.raises(DbiError) as e:
+        i8.save_prefix("/tmp/never.kv", [1])
+    assert "dense fp32" in e.value.message
