@@ -1,0 +1,302 @@
+"""Benchmark of the KV-cache decode hot path on one MI355X.
+
+Workload (BASELINE.json metric, quoted at 8k context): the Llama-3.2-3B
+attention shape of config 3 -- 28 layers, 24 query / 8 kv heads, head_dim
+128 -- with the dense int8 cache (per-channel K over 32-token groups,
+per-block V, 4 fp32 sinks) holding 8192 positions of synthetic N(0,1) keys
+and values with 1% outlier channels x8. One step decodes one token through
+all 28 layers: per layer, quantize-on-append at position 8191 then GQA decode
+attention over the 8192 resident keys. Inputs (q, k, v) are resident in HBM
+before the timed region; the step is replayed from a HIP graph.
+
+The same step over the fp32 cache of that shape (the reference point of
+BASELINE.md) is reported beside it. The working sets (529 MB int8, 1.9 GB
+fp32) exceed the 256 MB MALL, so each layer's KV is re-read from HBM.
+
+Printed: one JSON line (rank 0) with value = algorithmic HBM GB/s of the
+int8 step, the per-layer microseconds, the roofline of the dominant kernel
+(int8 decode attention) and the CPU oracle baseline.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GQA decode attn µs/token/layer + achieved HBM GB/s at 8k ctx, int8 & fp32 KV"
+PEAK_GBS = 8000.0  # MI355X HBM3E vendor peak
+
+L, NH, NKV, HD, CTX, NSINK = 28, 24, 8, 128, 8192, 4
+POS = CTX - 1
+
+
+def attn_bytes(dtype: str, n: int = CTX, s: int = NSINK) -> int:
+    """Algorithmic HBM bytes of one decode-attention call of one layer."""
+    P = NKV * HD
+    nb = (HD + 31) // 32
+    if dtype == "f32":
+        return 2 * n * P * 4
+    return (2 * (n - s) * P + -(-n // 32) * P * 4 + (n - s) * NKV * nb * 4 + 2 * s * P * 4)
+
+
+def make_inputs(torch, seed: int):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    P = NKV * HD
+    K = torch.randn(L, CTX, P, device="cuda", generator=g)
+    V = torch.randn(L, CTX, P, device="cuda", generator=g)
+    # 1% outlier channels x8, a seeded choice per layer shared by K and V
+    rng = np.random.default_rng(seed)
+    for layer in range(L):
+        ch = torch.as_tensor(rng.choice(P, round(0.01 * P), replace=False), device="cuda")
+        K[layer, :, ch] *= 8.0
+        V[layer, :, ch] *= 8.0
+    q = torch.randn(L, NH * HD, device="cuda", generator=g)
+    return K, V, q
+
+
+def build_cache(torch, HipKV, dtype_code, K, V):
+    kv = HipKV(L, CTX, NKV, HD, n_sink=NSINK, dtype=dtype_code)
+    kv.set_stream(torch.cuda.current_stream().cuda_stream)
+    for layer in range(L):
+        kv.append_async(layer, 0, CTX, K[layer].data_ptr(), V[layer].data_ptr())
+    torch.cuda.synchronize()
+    return kv
+
+
+def step(kv, K, V, q, out, scale, attention_only=False):
+    """One decode token through all layers: append at POS then attend."""
+    for layer in range(L):
+        if not attention_only:
+            kv.append_async(layer, POS, 1, K[layer, POS].data_ptr(), V[layer, POS].data_ptr())
+        kv.attend_async(layer, POS, NH, scale, q[layer].data_ptr(), out[layer].data_ptr())
+
+
+def capture(torch, fn):
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(s)  # warm-up on the capture stream (workspace allocation happens here)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        fn(s)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, reps: int) -> float:
+    """ms per replay, HIP events on the replay stream."""
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def eager_kernel_us(torch, kv, q, out, scale, reps: int) -> float:
+    """Average duration of one decode-attention launch: an event pair around
+    every launch on the kernel's own stream, layers rotated."""
+    pairs = []
+    for r in range(reps):
+        for layer in range(L):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            kv.attend_async(layer, POS, NH, scale, q[layer].data_ptr(), out[layer].data_ptr())
+            b.record()
+            pairs.append((a, b))
+    torch.cuda.synchronize()
+    return 1000.0 * statistics.median(a.elapsed_time(b) for a, b in pairs)
+
+
+def measure(torch, HipKV, code, name, K, V, q, args, scale):
+    kv = build_cache(torch, HipKV, code, K, V)
+    out = torch.empty(L, NH * HD, device="cuda")
+    res = {}
+
+    def full(s):
+        kv.set_stream(s.cuda_stream)
+        step(kv, K, V, q, out, scale)
+
+    def attn_only(s):
+        kv.set_stream(s.cuda_stream)
+        step(kv, K, V, q, out, scale, attention_only=True)
+
+    g_full = capture(torch, full)
+    g_attn = capture(torch, attn_only)
+    for _ in range(args.warmup):
+        g_full.replay()
+    torch.cuda.synchronize()
+    ms = time_graph(torch, g_full, args.steps)
+    res["ms_per_step"] = ms
+    res["us_per_token_layer"] = 1000.0 * ms / L
+    res["step_gbs"] = attn_bytes(name) * L / (ms * 1e-3) / 1e9
+    ms_attn = time_graph(torch, g_attn, args.steps)
+    res["attn_us_graph"] = 1000.0 * ms_attn / L
+    kv.set_stream(torch.cuda.current_stream().cuda_stream)
+    res["attn_us_events"] = eager_kernel_us(torch, kv, q, out, scale, max(2, args.steps // 20))
+    res["attn_bytes"] = attn_bytes(name)
+    kv.close()
+    del g_full, g_attn
+    torch.cuda.synchronize()
+    return res
+
+
+def cpu_baseline(budget_s: float):
+    """The CPU oracle (the reference's attend_dense_int8 restated, head-parallel
+    like its thread pool) on one layer of the same workload."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle  # checker / baseline only
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    rng = np.random.default_rng(7)
+    P = NKV * HD
+    kv = pyoracle.OracleKV(1, CTX, NKV, HD, n_sink=NSINK, dtype=pyoracle.INT8)
+    K = rng.standard_normal((CTX, P), dtype=np.float32)
+    V = rng.standard_normal((CTX, P), dtype=np.float32)
+    ch = rng.choice(P, round(0.01 * P), replace=False)
+    K[:, ch] *= 8
+    V[:, ch] *= 8
+    t0 = time.perf_counter()
+    for p in range(CTX):
+        kv.append(0, p, K[p], V[p])
+    append_s = time.perf_counter() - t0
+    q = rng.standard_normal(NH * HD, dtype=np.float32)
+    scale = np.float32(1.0) / np.sqrt(np.float32(HD))
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 or time.perf_counter() < t_end:
+        t = time.perf_counter()
+        kv.attend(0, POS, q, NH, scale, n_threads=threads)
+        times.append(time.perf_counter() - t)
+        if len(times) >= 200:
+            break
+    med = statistics.median(times)
+    return {
+        "value": round(1e6 * med, 3),
+        "unit": "us/token/layer",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle attend_dense_int8, 1 layer of the workload (ctx {CTX}, 24q/8kv, "
+                   f"hd 128, 4 sinks), median of {len(times)} calls over ~{budget_s:.0f}s; "
+                   f"cache filled by {CTX} oracle appends in {append_s:.1f}s"),
+        "gbs_equiv": round(attn_bytes("int8") / med / 1e9, 3),
+        "cpu_model": _cpu_model(),
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (PMC calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards by kv head with no exchange, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from dbinfer_amd.kv import F32, INT8, HipKV
+
+    torch.cuda.set_device(0)
+    if args.calibrate_copy_mib:
+        n = args.calibrate_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration_copy_bytes": n * 4, "launches": 5}))
+        return
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(HD)))
+    # every launch and event goes on one non-default stream (the kernels'
+    # stream), so events bracket exactly the work they time
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        K, V, q = make_inputs(torch, 1234)
+        i8 = measure(torch, HipKV, INT8, "int8", K, V, q, args, scale)
+        f32 = measure(torch, HipKV, F32, "f32", K, V, q, args, scale)
+        del K, V
+    torch.cuda.synchronize()
+
+    dom_us = i8["attn_us_graph"]
+    achieved = i8["attn_bytes"] / (dom_us * 1e-6) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(i8["step_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(i8["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) q/K/V, 1% outlier channels x8)",
+        "config": {
+            "workload": "config 3: Llama-3.2-3B attention shape, dense int8 KV (per-channel K, "
+                        "per-block V, 4 fp32 sinks), decode step at ctx 8192 over 28 layers "
+                        "(append + GQA decode attention per layer, HIP-graph replay)",
+            "n_layers": L, "n_heads": NH, "n_kv_heads": NKV, "head_dim": HD, "ctx": CTX,
+            "parallelism": "single GPU",
+        },
+        "us_per_token_layer": round(i8["us_per_token_layer"], 3),
+        "attn_us_per_layer": round(dom_us, 3),
+        "attn_us_per_layer_events": round(i8["attn_us_events"], 3),
+        "fp32": {
+            "us_per_token_layer": round(f32["us_per_token_layer"], 3),
+            "attn_us_per_layer": round(f32["attn_us_graph"], 3),
+            "attn_us_per_layer_events": round(f32["attn_us_events"], 3),
+            "step_gbs": round(f32["step_gbs"], 2),
+            "attn_gbs": round(f32["attn_bytes"] / (f32["attn_us_graph"] * 1e-6) / 1e9, 2),
+            "frac_of_peak": round(f32["attn_bytes"] / (f32["attn_us_graph"] * 1e-6) / 1e9
+                                  / PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "attn_kernel<HD=128,G=3,EPL=16,int8 dense>",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": i8["attn_bytes"],
+        },
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(args.cpu_seconds),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -58,7 +58,6 @@ void free_store(dbi::KvStore& s) {
 
 void free_ws(dbi::Workspace& w) {
   if (w.part) (void)hipFree(w.part);
-  if (w.counters) (void)hipFree(w.counters);
   if (w.staging) (void)hipFree(w.staging);
   w = dbi::Workspace{};
 }
@@ -102,8 +101,7 @@ dbi::RingView ring_view(const dbi_kv* kv, uint32_t n_seen) {
 }
 
 dbi_status ensure_workspace(dbi_kv* kv, const dbi::AttnCall& c) {
-  size_t part = 0, counters = 0;
-  dbi::attention_workspace_need(kv->geom, c, &part, &counters);
+  const size_t part = dbi::attention_workspace_need(kv->geom, c);
   if (part > kv->ws.part_floats) {
     HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
     if (kv->ws.part) (void)hipFree(kv->ws.part);
@@ -112,15 +110,6 @@ dbi_status ensure_workspace(dbi_kv* kv, const dbi::AttnCall& c) {
     if (hipMalloc(reinterpret_cast<void**>(&kv->ws.part), part * sizeof(float)) != hipSuccess)
       return fail(DBI_ERR_NOMEM, "attention workspace allocation failed");
     kv->ws.part_floats = part;
-  }
-  if (counters > kv->ws.n_counters) {
-    HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
-    if (kv->ws.counters) (void)hipFree(kv->ws.counters);
-    kv->ws.counters = nullptr;
-    kv->ws.n_counters = 0;
-    if (dalloc(&kv->ws.counters, counters) != hipSuccess)
-      return fail(DBI_ERR_NOMEM, "attention counter allocation failed");
-    kv->ws.n_counters = counters;
   }
   return DBI_OK;
 }

@@ -121,17 +121,21 @@ __global__ __launch_bounds__(kThreads) void append_i8_dense_kernel(KvGeom g, KvS
       for (int q = p; q <= hi; ++q)
         raw[static_cast<size_t>(q % kKGroup) * P] = k[static_cast<size_t>(q - pos0) * P + c];
       const int within = hi - first;
+      // all 32 staging rows in flight at once (rows past `within` are unused)
+      float rv[kKGroup];
+#pragma unroll
+      for (int w = 0; w < kKGroup; ++w) rv[w] = raw[static_cast<size_t>(w) * P];
       float mx = 0.0f;
-      for (int w = 0; w <= within; ++w)
-        if (first + w >= g.n_sink) mx = max_f(mx, fabsf(raw[static_cast<size_t>(w) * P]));
+#pragma unroll
+      for (int w = 0; w < kKGroup; ++w)
+        if (w <= within && first + w >= g.n_sink) mx = max_f(mx, fabsf(rv[w]));
       const float sc = mx / 127.0f;
       s.k_scale[(head * g.ngroups + grp) * g.hd + i] = sc;
       const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
-      for (int w = 0; w <= within; ++w) {
-        if (first + w < g.n_sink) continue;
-        s.k8[(head * g.cap + first + w) * g.hd + i] =
-            quant_code(raw[static_cast<size_t>(w) * P], inv);
-      }
+#pragma unroll
+      for (int w = 0; w < kKGroup; ++w)
+        if (w <= within && first + w >= g.n_sink)
+          s.k8[(head * g.cap + first + w) * g.hd + i] = quant_code(rv[w], inv);
       p = hi + 1;
     }
     return;

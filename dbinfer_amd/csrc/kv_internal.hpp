@@ -45,13 +45,10 @@ struct KvStore {
   float2* rope_cs = nullptr;
 };
 
-// Split-K workspace: partial (m, l, o) of every split plus a self-resetting
-// arrival counter per (row, kv head).
+// Split-K workspace: partial (o, m, l) of every split of one attention call.
 struct Workspace {
   float* part = nullptr;
   size_t part_floats = 0;
-  unsigned* counters = nullptr;
-  size_t n_counters = 0;
   float* staging = nullptr;  // device staging for host-pointer calls
   size_t staging_floats = 0;
 };
@@ -82,9 +79,8 @@ hipError_t launch_append(const KvGeom& g, const KvStore& s, int layer, int pos0,
 // Returns hipErrorNotSupported for shapes without a kernel instance.
 hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws,
                             const AttnCall& c, hipStream_t st);
-// Number of partial floats / counters one call needs (for workspace sizing).
-void attention_workspace_need(const KvGeom& g, const AttnCall& c, size_t* part_floats,
-                              size_t* counters);
+// Number of partial floats one call needs (for workspace sizing).
+size_t attention_workspace_need(const KvGeom& g, const AttnCall& c);
 bool attention_supported(const KvGeom& g, int n_heads);
 
 // Prefix pack/unpack between [L][len][nkv][hd] and the head-major store.
