@@ -24,14 +24,18 @@ __device__ __forceinline__ int8_t quant_code(float x, float inv) {
   return static_cast<int8_t>(t > 127.0f ? 127 : (t < -127.0f ? -127 : static_cast<int>(t)));
 }
 
-// quant_head of one block (model.cpp:303-317): block [0, len) of src.
-__device__ __forceinline__ void quant_block(const float* src, int len, int8_t* dst, float* scale) {
-  float max_abs = 0.0f;
-  for (int i = 0; i < len; ++i) max_abs = max_f(max_abs, fabsf(src[i]));
-  const float s = max_abs / 127.0f;
+// quant_head (model.cpp:303-317) of one block with one lane per element: lanes of an aligned
+// 32-lane group hold the block's elements (inactive tail lanes pass 0), the
+// block max comes from xor shuffles inside the group. Every lane returns its
+// code; the block scale is returned through *scale.
+__device__ __forceinline__ int8_t quant_lane(float x, float* scale) {
+  float m = fabsf(x);
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) m = max_f(m, __shfl_xor(m, off, 32));
+  const float s = m / 127.0f;
   *scale = s;
   const float inv = s > 0.0f ? 1.0f / s : 0.0f;
-  for (int i = 0; i < len; ++i) dst[i] = quant_code(src[i], inv);
+  return quant_code(x, inv);
 }
 
 __device__ __forceinline__ int slot_for(int pos, int s, int W) {
@@ -69,27 +73,38 @@ __global__ __launch_bounds__(kThreads) void append_f32_kernel(KvGeom g, float* k
 }
 
 // Ring int8: quant_head of K and V per kv head into slot_for(pos)
-// (model.cpp:386-396). One thread per (row, kv head, block).
+// (model.cpp:386-396). One lane per element, 32 lanes per block.
 __global__ __launch_bounds__(kThreads) void append_i8_ring_kernel(KvGeom g, KvStore s, int layer,
                                                                   int pos0, int n,
                                                                   const float* __restrict__ k,
                                                                   const float* __restrict__ v) {
   const int P = g.nkv * g.hd;
-  const size_t total = static_cast<size_t>(n) * g.nkv * g.nb;
-  for (size_t idx = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; idx < total;
-       idx += static_cast<size_t>(gridDim.x) * kThreads) {
-    const int b = static_cast<int>(idx % g.nb);
-    const int kh = static_cast<int>((idx / g.nb) % g.nkv);
-    const int r = static_cast<int>(idx / (static_cast<size_t>(g.nb) * g.nkv));
-    const int p = pos0 + r;
-    if (!ring_row_final(p, pos0 + n, g.n_sink, g.window)) continue;
-    const int slot = slot_for(p, g.n_sink, g.window);
-    const int start = b * kBlock;
-    const int len = min(kBlock, g.hd - start);
-    const size_t src = static_cast<size_t>(r) * P + kh * g.hd + start;
-    const size_t row = (static_cast<size_t>(layer) * g.nkv + kh) * g.cap + slot;
-    quant_block(k + src, len, s.k8 + row * g.hd + start, s.k_scale + row * g.nb + b);
-    quant_block(v + src, len, s.v8 + row * g.hd + start, s.v_scale + row * g.nb + b);
+  const size_t blocks = static_cast<size_t>(n) * g.nkv * g.nb;
+  const size_t bidx = (blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x) / kBlock;
+  const int t = threadIdx.x % kBlock;
+  if (bidx >= blocks) return;  // whole 32-lane groups leave together
+  const int b = static_cast<int>(bidx % g.nb);
+  const int kh = static_cast<int>((bidx / g.nb) % g.nkv);
+  const int r = static_cast<int>(bidx / (static_cast<size_t>(g.nb) * g.nkv));
+  const int p = pos0 + r;
+  const int i = b * kBlock + t;
+  const bool in = i < g.hd;
+  const size_t src = static_cast<size_t>(r) * P + kh * g.hd + i;
+  const float kx = in ? k[src] : 0.0f;
+  const float vx = in ? v[src] : 0.0f;
+  float ks, vs;
+  const int8_t kc = quant_lane(kx, &ks);
+  const int8_t vc = quant_lane(vx, &vs);
+  if (!ring_row_final(p, pos0 + n, g.n_sink, g.window)) return;
+  const int slot = slot_for(p, g.n_sink, g.window);
+  const size_t row = (static_cast<size_t>(layer) * g.nkv + kh) * g.cap + slot;
+  if (in) {
+    s.k8[row * g.hd + i] = kc;
+    s.v8[row * g.hd + i] = vc;
+  }
+  if (t == 0) {
+    s.k_scale[row * g.nb + b] = ks;
+    s.v_scale[row * g.nb + b] = vs;
   }
 }
 
@@ -99,8 +114,8 @@ __global__ __launch_bounds__(kThreads) void append_i8_ring_kernel(KvGeom g, KvSt
 // requantize the group over raw rows [0, within] that are not sinks
 // (requantize_kgroup, model.cpp:329-355). Each channel only ever reads and
 // writes its own column of k_raw, k_scale and k8, so threads never interact.
-// The remaining blocks run the value side, one thread per (row, kv head,
-// block): fp32 sink copy for pos < n_sink, else quant_head of V.
+// The remaining blocks run the value side, one lane per element, 32 lanes per
+// (row, kv head, block): fp32 sink copy for pos < n_sink, else quant_head of V.
 __global__ __launch_bounds__(kThreads) void append_i8_dense_kernel(KvGeom g, KvStore s, int layer,
                                                                    int pos0, int n, int n_kblocks,
                                                                    const float* __restrict__ k,
@@ -140,27 +155,33 @@ __global__ __launch_bounds__(kThreads) void append_i8_dense_kernel(KvGeom g, KvS
     }
     return;
   }
-  const size_t idx = (blockIdx.x - n_kblocks) * static_cast<size_t>(kThreads) + threadIdx.x;
-  const size_t total = static_cast<size_t>(n) * g.nkv * g.nb;
-  if (idx >= total) return;
-  const int b = static_cast<int>(idx % g.nb);
-  const int kh = static_cast<int>((idx / g.nb) % g.nkv);
-  const int r = static_cast<int>(idx / (static_cast<size_t>(g.nb) * g.nkv));
+  const size_t blocks = static_cast<size_t>(n) * g.nkv * g.nb;
+  const size_t bidx =
+      ((blockIdx.x - n_kblocks) * static_cast<size_t>(kThreads) + threadIdx.x) / kBlock;
+  const int t = threadIdx.x % kBlock;
+  if (bidx >= blocks) return;  // whole 32-lane groups leave together
+  const int b = static_cast<int>(bidx % g.nb);
+  const int kh = static_cast<int>((bidx / g.nb) % g.nkv);
+  const int r = static_cast<int>(bidx / (static_cast<size_t>(g.nb) * g.nkv));
   const int p = pos0 + r;
-  const int start = b * kBlock;
-  const int len = min(kBlock, g.hd - start);
-  const size_t src = static_cast<size_t>(r) * P + kh * g.hd + start;
+  const int i = b * kBlock + t;
+  const bool in = i < g.hd;
+  const size_t src = static_cast<size_t>(r) * P + kh * g.hd + i;
   const size_t head = static_cast<size_t>(layer) * g.nkv + kh;
-  if (p < g.n_sink) {
-    const size_t dst = (head * g.n_sink + p) * g.hd + start;
-    for (int i = 0; i < len; ++i) {
-      s.k_sink[dst + i] = k[src + i];
-      s.v_sink[dst + i] = v[src + i];
+  const float vx = in ? v[src] : 0.0f;
+  if (p < g.n_sink) {  // uniform over the 32-lane group
+    if (in) {
+      const size_t dst = (head * g.n_sink + p) * g.hd + i;
+      s.k_sink[dst] = k[src];
+      s.v_sink[dst] = vx;
     }
     return;
   }
+  float vs;
+  const int8_t vc = quant_lane(vx, &vs);
   const size_t row = head * g.cap + p;
-  quant_block(v + src, len, s.v8 + row * g.hd + start, s.v_scale + row * g.nb + b);
+  if (in) s.v8[row * g.hd + i] = vc;
+  if (t == 0) s.v_scale[row * g.nb + b] = vs;
 }
 
 int grid_for(size_t work) {
@@ -198,11 +219,12 @@ hipError_t launch_append(const KvGeom& g, const KvStore& s, int layer, int pos0,
     hipLaunchKernelGGL(append_f32_kernel, dim3(grid_for(n * P)), dim3(kThreads), 0, st, g, s.k,
                        s.v, layer, pos0, n, k, v);
   } else if (g.ring) {
-    hipLaunchKernelGGL(append_i8_ring_kernel, dim3(grid_for(static_cast<size_t>(n) * g.nkv * g.nb)),
+    const size_t lanes = static_cast<size_t>(n) * g.nkv * g.nb * kBlock;
+    hipLaunchKernelGGL(append_i8_ring_kernel, dim3((lanes + kThreads - 1) / kThreads),
                        dim3(kThreads), 0, st, g, s, layer, pos0, n, k, v);
   } else {
     const int n_kblocks = static_cast<int>((P + kThreads - 1) / kThreads);
-    const size_t vwork = static_cast<size_t>(n) * g.nkv * g.nb;
+    const size_t vwork = static_cast<size_t>(n) * g.nkv * g.nb * kBlock;
     const int n_vblocks = static_cast<int>((vwork + kThreads - 1) / kThreads);
     hipLaunchKernelGGL(append_i8_dense_kernel, dim3(n_kblocks + n_vblocks), dim3(kThreads), 0, st,
                        g, s, layer, pos0, n, n_kblocks, k, v);

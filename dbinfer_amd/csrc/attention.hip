@@ -215,10 +215,12 @@ struct Cfg {
   static constexpr int NCH = EPL / CH;
   // positions per lane per step, from a VGPR budget: q (or q*ks) and o take
   // 2*G*EPL, each in-flight position its raw K/V, scales and rope table
+  // (two step buffers are live: the current one and the prefetched next one)
   static constexpr int kBudget = (kInt8 && G >= 7) ? 150 : 170;
   static constexpr int PER_POS = !kInt8 ? 2 * EPL + (kRing ? EPL : 0)
                                         : EPL / 2 + NCH + (kRing ? NCH + EPL : 0);
-  static constexpr int UFIT = (kBudget - 2 * G * EPL - (kInt8 ? EPL : 0)) / PER_POS;
+  static constexpr int FIXED = 2 * G * EPL + (kInt8 ? EPL : 0) + (KIND == kI8Dense ? 2 * EPL : 0);
+  static constexpr int UFIT = (kBudget - FIXED) / (2 * PER_POS);
   static constexpr int UMAX = kInt8 ? 4 : 2;
   static constexpr int UCAP = UFIT < 1 ? 1 : (UFIT > UMAX ? UMAX : UFIT);
   static constexpr int UPOW = UCAP >= 4 ? 4 : (UCAP >= 2 ? 2 : 1);
@@ -258,15 +260,19 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
   const int t_end = min(t_begin + P.tiles_per_split, ntiles);
   const size_t head_rows = static_cast<size_t>(kh) * P.cap;  // first row of this kv head
 
-  // ---- raw loads of one step: issued early, consumed by compute_step
-  VT kraw[U][NCH], vraw[U][NCH];       // int8 codes
-  float4 kf4[U][NCH], vf4[U][NCH];     // fp32 rows
-  float vsc[U][NCH];                   // int8 V block scales
-  float ksc[U][NCH];                   // ring int8 K block scales
-  float2 cs[U][(NCH / 2) * CH + 1];    // ring rope cos/sin of each key
-  float ksv[EPL];                      // dense int8 per-channel K scales of the tile
-  int pu[U];
-  bool valid[U];
+  // ---- raw loads of one step (U positions per lane row); two buffers so the
+  // next step's loads are in flight while the current one is computed
+  struct StepBuf {
+    VT kraw[U][NCH], vraw[U][NCH];      // int8 codes
+    float4 kf4[U][NCH], vf4[U][NCH];    // fp32 rows
+    float vsc[U][NCH];                  // int8 V block scales
+    float ksc[U][NCH];                  // ring int8 K block scales
+    float2 cs[U][(NCH / 2) * CH + 1];   // ring rope cos/sin of each key
+    float ksv[EPL];                     // dense int8 per-channel K scales of the tile
+    int pu[U];
+    bool valid[U];
+  };
+  StepBuf cur, nxt;
 
   auto rope_pos = [&](int slot) {
     if (slot < P.ring_s) return slot;
@@ -275,42 +281,42 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
     return P.ring_s + r;
   };
 
-  auto issue = [&](int tile, int st) {
+  auto issue = [&](int tile, int st, StepBuf& b) {
     const int tb = tile * kTile;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int p = tb + (st + u) * RPW + rw;
-      valid[u] = p < nkeys && (KIND != kI8Dense || p >= P.n_sink);
-      pu[u] = min(p, nkeys - 1);
+      b.valid[u] = p < nkeys && (KIND != kI8Dense || p >= P.n_sink);
+      b.pu[u] = min(p, nkeys - 1);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const size_t row = head_rows + pu[u];
+      const size_t row = head_rows + b.pu[u];
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
         if constexpr (!C::kInt8) {
-          kf4[u][j] = *reinterpret_cast<const float4*>(P.kf + row * HD + C::dim(j, 0, lr));
-          vf4[u][j] = *reinterpret_cast<const float4*>(P.vf + row * HD + C::dim(j, 0, lr));
+          b.kf4[u][j] = *reinterpret_cast<const float4*>(P.kf + row * HD + C::dim(j, 0, lr));
+          b.vf4[u][j] = *reinterpret_cast<const float4*>(P.vf + row * HD + C::dim(j, 0, lr));
         } else {
-          kraw[u][j] = *reinterpret_cast<const VT*>(P.k8 + row * HD + C::dim(j, 0, lr));
-          vraw[u][j] = *reinterpret_cast<const VT*>(P.v8 + row * HD + C::dim(j, 0, lr));
+          b.kraw[u][j] = *reinterpret_cast<const VT*>(P.k8 + row * HD + C::dim(j, 0, lr));
+          b.vraw[u][j] = *reinterpret_cast<const VT*>(P.v8 + row * HD + C::dim(j, 0, lr));
         }
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const size_t row = head_rows + pu[u];
+      const size_t row = head_rows + b.pu[u];
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
-        if constexpr (C::kInt8) vsc[u][j] = P.vs[row * NB + C::dim(j, 0, lr) / kBlock];
-        if constexpr (KIND == kI8Ring) ksc[u][j] = P.ks[row * NB + C::dim(j, 0, lr) / kBlock];
+        if constexpr (C::kInt8) b.vsc[u][j] = P.vs[row * NB + C::dim(j, 0, lr) / kBlock];
+        if constexpr (KIND == kI8Ring) b.ksc[u][j] = P.ks[row * NB + C::dim(j, 0, lr) / kBlock];
       }
       if constexpr (C::kRing) {
-        const float2* cst = P.rope + static_cast<size_t>(rope_pos(pu[u])) * (HD / 2);
+        const float2* cst = P.rope + static_cast<size_t>(rope_pos(b.pu[u])) * (HD / 2);
 #pragma unroll
         for (int j = 0; j < NCH / 2; ++j)
 #pragma unroll
-          for (int t = 0; t < CH; ++t) cs[u][j * CH + t] = cst[C::dim(j, t, lr)];
+          for (int t = 0; t < CH; ++t) b.cs[u][j * CH + t] = cst[C::dim(j, t, lr)];
       }
     }
     if constexpr (KIND == kI8Dense) {
@@ -320,14 +326,14 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
 #pragma unroll
         for (int j = 0; j < NCH; ++j)
 #pragma unroll
-          for (int t = 0; t < CH; ++t) ksv[j * CH + t] = ksr[C::dim(j, t, lr)];
+          for (int t = 0; t < CH; ++t) b.ksv[j * CH + t] = ksr[C::dim(j, t, lr)];
       }
     }
   };
 
   // first step's loads go out before the query is staged
   const int first_tile = t_begin + wave;
-  if (first_tile < t_end) issue(first_tile, 0);
+  if (first_tile < t_end) issue(first_tile, 0, cur);
 
   // ---- stage the query group in LDS: rope (ring), scale to the log2 domain
   {
@@ -471,6 +477,13 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
   float qsum[KIND == kI8Dense ? G : 1];
   int tile = first_tile, st = 0;
   while (tile < t_end) {
+    // prefetch the next step of this wave
+    int ntile = tile, nst = st + U;
+    if (nst == C::STEPS) {
+      nst = 0;
+      ntile += kWaves;
+    }
+    if (ntile < t_end) issue(ntile, nst, nxt);
     if constexpr (KIND == kI8Dense) {
       if (st == 0) {
 #pragma unroll
@@ -480,7 +493,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
           for (int j = 0; j < NCH; ++j)
 #pragma unroll
             for (int t = 0; t < CH; ++t) {
-              qs[g][j * CH + t] = s_q[g][C::dim(j, t, lr)] * ksv[j * CH + t];
+              qs[g][j * CH + t] = s_q[g][C::dim(j, t, lr)] * cur.ksv[j * CH + t];
               qsum[g] += qs[g][j * CH + t];
             }
           qsum[g] *= 128.0f;
@@ -494,10 +507,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
       for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int j = 0; j < NCH; ++j) {
-          kx[u][j * 4 + 0] = kf4[u][j].x;
-          kx[u][j * 4 + 1] = kf4[u][j].y;
-          kx[u][j * 4 + 2] = kf4[u][j].z;
-          kx[u][j * 4 + 3] = kf4[u][j].w;
+          kx[u][j * 4 + 0] = cur.kf4[u][j].x;
+          kx[u][j * 4 + 1] = cur.kf4[u][j].y;
+          kx[u][j * 4 + 2] = cur.kf4[u][j].z;
+          kx[u][j * 4 + 3] = cur.kf4[u][j].w;
         }
       if constexpr (C::kRing) {
 #pragma unroll
@@ -506,7 +519,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
           for (int j = 0; j < NCH / 2; ++j)
 #pragma unroll
             for (int t = 0; t < CH; ++t) {
-              const float2 c = cs[u][j * CH + t];
+              const float2 c = cur.cs[u][j * CH + t];
               const float a = kx[u][j * CH + t];
               const float b = kx[u][(j + NCH / 2) * CH + t];
               kx[u][j * CH + t] = a * c.x - b * c.y;
@@ -521,17 +534,17 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
 #pragma unroll
           for (int e = 0; e < EPL; ++e) acc += qv[g][e] * kx[u][e];
           acc = row_sum<LPR>(acc);
-          s[g][u] = valid[u] ? acc : -INFINITY;
+          s[g][u] = cur.valid[u] ? acc : -INFINITY;
         }
       update(
           s,
           [&](int u, float* x, float* mul) {
 #pragma unroll
             for (int j = 0; j < NCH; ++j) {
-              x[j * 4 + 0] = vf4[u][j].x;
-              x[j * 4 + 1] = vf4[u][j].y;
-              x[j * 4 + 2] = vf4[u][j].z;
-              x[j * 4 + 3] = vf4[u][j].w;
+              x[j * 4 + 0] = cur.vf4[u][j].x;
+              x[j * 4 + 1] = cur.vf4[u][j].y;
+              x[j * 4 + 2] = cur.vf4[u][j].z;
+              x[j * 4 + 3] = cur.vf4[u][j].w;
               mul[j] = 1.0f;
             }
           },
@@ -541,18 +554,18 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
       for (int u = 0; u < U; ++u) {
         float kx[EPL];
 #pragma unroll
-        for (int j = 0; j < NCH; ++j) unpack_biased<CH>(kraw[u][j], kx + j * CH);
+        for (int j = 0; j < NCH; ++j) unpack_biased<CH>(cur.kraw[u][j], kx + j * CH);
         if constexpr (KIND == kI8Ring) {
           // dequantize (ks * code, model.cpp:689-690), then rope
 #pragma unroll
           for (int j = 0; j < NCH; ++j)
 #pragma unroll
-            for (int t = 0; t < CH; ++t) kx[j * CH + t] = ksc[u][j] * (kx[j * CH + t] - 128.0f);
+            for (int t = 0; t < CH; ++t) kx[j * CH + t] = cur.ksc[u][j] * (kx[j * CH + t] - 128.0f);
 #pragma unroll
           for (int j = 0; j < NCH / 2; ++j)
 #pragma unroll
             for (int t = 0; t < CH; ++t) {
-              const float2 c = cs[u][j * CH + t];
+              const float2 c = cur.cs[u][j * CH + t];
               const float a = kx[j * CH + t];
               const float b = kx[(j + NCH / 2) * CH + t];
               kx[j * CH + t] = a * c.x - b * c.y;
@@ -572,7 +585,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
             for (int e = 0; e < EPL; ++e) acc += qv[g][e] * kx[e];
           }
           acc = row_sum<LPR>(acc);
-          s[g][u] = valid[u] ? acc : -INFINITY;
+          s[g][u] = cur.valid[u] ? acc : -INFINITY;
         }
       }
       update(
@@ -580,19 +593,15 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
           [&](int u, float* x, float* mul) {
 #pragma unroll
             for (int j = 0; j < NCH; ++j) {
-              unpack_biased<CH>(vraw[u][j], x + j * CH);
-              mul[j] = vsc[u][j];
+              unpack_biased<CH>(cur.vraw[u][j], x + j * CH);
+              mul[j] = cur.vsc[u][j];
             }
           },
           Biased{});
     }
-    // next step
-    st += U;
-    if (st == C::STEPS) {
-      st = 0;
-      tile += kWaves;
-    }
-    if (tile < t_end) issue(tile, st);
+    cur = nxt;
+    tile = ntile;
+    st = nst;
   }
 
   // ---- sum the lane rows of this wave (m is already the wave maximum)
@@ -719,10 +728,21 @@ __global__ __launch_bounds__(HD) void merge_kernel(const float* __restrict__ par
 // ---------------------------------------------------------------------------
 // dispatch
 
+// Elements per lane: 16 keeps the lane-row count (and the end-of-wave row
+// merge) small; 8 halves the q / o registers where G is large or int8 wants
+// more positions in flight.
+template <int HD, int G, int KIND>
+constexpr int epl_for() {
+#ifdef DBI_EPL_RULE
+  return DBI_EPL_RULE;
+#else
+  return (KIND == kI8Dense || KIND == kI8Ring) ? 8 : (G <= 2 ? 16 : 8);
+#endif
+}
+
 template <int HD, int G, int KIND>
 void* kernel_for() {
-  constexpr int EPL = G <= 4 ? 16 : 8;
-  return reinterpret_cast<void*>(&attn_kernel<HD, G, EPL, KIND>);
+  return reinterpret_cast<void*>(&attn_kernel<HD, G, epl_for<HD, G, KIND>(), KIND>);
 }
 
 template <int HD, int KIND>
