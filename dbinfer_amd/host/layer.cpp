@@ -1,0 +1,98 @@
+// Reference call sites over the device KV cache (see layer.hpp).
+#include "layer.hpp"
+
+#include <cmath>
+
+namespace dbinfer_amd::model {
+
+void rope(float* x, const std::int32_t* positions, float theta, std::size_t n_heads,
+          std::size_t seq, std::size_t head_dim) {
+  const std::size_t half = head_dim / 2;
+  for (std::size_t h = 0; h < n_heads; ++h) {
+    for (std::size_t s = 0; s < seq; ++s) {
+      float* row = x + (h * seq + s) * head_dim;
+      const double p = static_cast<double>(positions[s]);
+      for (std::size_t j = 0; j < half; ++j) {
+        const double freq = std::pow(static_cast<double>(theta),
+                                     -2.0 * static_cast<double>(j) / static_cast<double>(head_dim));
+        const double angle = p * freq;
+        const double c = std::cos(angle), sn = std::sin(angle);
+        const float a = row[j], b = row[j + half];
+        row[j] = static_cast<float>(a * c - b * sn);
+        row[j + half] = static_cast<float>(b * c + a * sn);
+      }
+    }
+  }
+}
+
+namespace {
+
+float attn_scale(const Config& cfg) {
+  return 1.0f / std::sqrt(static_cast<float>(cfg.head_dim));  // model.cpp:757
+}
+
+}  // namespace
+
+bool decode_attention(KVCache& kv, const Config& cfg, std::size_t layer, std::int32_t pos,
+                      float* q, float* k, const float* v, float* attn_out) {
+  const auto l = static_cast<std::uint32_t>(layer);
+  const auto p = static_cast<std::uint32_t>(pos);
+  if (!kv.ring()) {
+    rope(q, &pos, cfg.rope_theta, cfg.n_heads, 1, cfg.head_dim);
+    rope(k, &pos, cfg.rope_theta, cfg.n_kv_heads, 1, cfg.head_dim);
+  }
+  kv.append(layer, p, k, v);
+  if (!kv.ok()) return false;
+  return kv.check(dbi_attn_decode(kv.handle(), l, p, static_cast<std::uint32_t>(cfg.n_heads),
+                                  attn_scale(cfg), q, attn_out));
+}
+
+bool chunk_attention(KVCache& kv, const Config& cfg, std::size_t layer, std::int32_t pos0,
+                     std::size_t n, float* q, float* k, const float* v, float* attn_out) {
+  const std::size_t qrow = cfg.n_heads * cfg.head_dim, krow = cfg.n_kv_heads * cfg.head_dim;
+  for (std::size_t c = 0; c < n; ++c) {
+    const std::int32_t p = pos0 + static_cast<std::int32_t>(c);
+    rope(q + c * qrow, &p, cfg.rope_theta, cfg.n_heads, 1, cfg.head_dim);
+    rope(k + c * krow, &p, cfg.rope_theta, cfg.n_kv_heads, 1, cfg.head_dim);
+  }
+  kv.append_n(layer, static_cast<std::size_t>(pos0), n, k, v);
+  if (!kv.ok()) return false;
+  return kv.check(dbi_attn_chunk(kv.handle(), static_cast<std::uint32_t>(layer),
+                                 static_cast<std::uint32_t>(pos0), static_cast<std::uint32_t>(n),
+                                 static_cast<std::uint32_t>(cfg.n_heads), attn_scale(cfg), q,
+                                 attn_out));
+}
+
+Result<Unit> save_kv_prefix(const KVCache& kv, const std::string& path,
+                            std::span<const std::int32_t> prefix_tokens) {
+  const dbi_status st = dbi_kv_prefix_save(kv.handle(), path.c_str(), prefix_tokens.data(),
+                                           static_cast<std::uint32_t>(prefix_tokens.size()));
+  if (st != DBI_OK) return Error{dbi_last_error(), path, 0};
+  return Unit{};
+}
+
+Result<std::size_t> load_kv_prefix(KVCache& kv, const std::string& path,
+                                   std::span<const std::int32_t> prefix_tokens) {
+  std::uint32_t len = 0;
+  const dbi_status st = dbi_kv_prefix_load(kv.handle(), path.c_str(), prefix_tokens.data(),
+                                           static_cast<std::uint32_t>(prefix_tokens.size()), &len);
+  if (st != DBI_OK) return Error{dbi_last_error(), path, 0};
+  return static_cast<std::size_t>(len);
+}
+
+std::size_t speculative_merge(std::span<const std::int32_t> draft,
+                              std::span<const std::int32_t> target,
+                              std::vector<std::int32_t>& out) {
+  std::size_t j = 0;
+  while (j < draft.size() && draft[j] == target[j]) out.push_back(draft[j++]);
+  out.push_back(target[j]);  // correction at the first mismatch, or the bonus token
+  return j;
+}
+
+std::int32_t speculative_commit(KVCache& kv, std::int32_t pos, std::size_t accepted) {
+  const std::int32_t next = pos + static_cast<std::int32_t>(accepted) + 1;
+  kv.truncate(static_cast<std::size_t>(next));
+  return next;
+}
+
+}  // namespace dbinfer_amd::model

@@ -1,0 +1,380 @@
+// C++ parity tests of the MI355X KV cache through the engine-facing host
+// layer (dbinfer_amd/host), written like the reference's own ctest mains:
+//   kv_ring_test.cpp:26-97        ring slots, residents, sinks, rope packing
+//   kv_int8_test.cpp:33-137       per-channel K round trip, int8 vs fp32 attention
+//   kv_prefix_cache_test.cpp:79-130  save -> load -> identical next attention
+//   chunked_prefill_test.cpp:19-70   chunk == per-token (here within tolerance)
+//   speculative_test.cpp:104-150     merge vectors, rollback state
+// plus decode/chunk parity against the CPU oracle (oracle/kv_oracle.h), which
+// is the checker only. `host_test --cpu-only` runs the parts that need no GPU.
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kv_cache.hpp"
+#include "kv_oracle.h"
+#include "layer.hpp"
+
+namespace {
+
+using dbinfer_amd::model::Config;
+using dbinfer_amd::model::KVCache;
+using dbinfer_amd::model::KvDtype;
+using dbinfer_amd::model::KvPolicy;
+
+int g_failures = 0;
+
+void check(bool ok, const std::string& what) {
+  std::printf("%s %s\n", ok ? "PASS" : "FAIL", what.c_str());
+  if (!ok) ++g_failures;
+}
+
+struct Lcg {  // kv_int8_test.cpp:24-31
+  std::uint64_t s;
+  float next() {
+    s = s * 6364136223846793005ULL + 1442695040888963407ULL;
+    const auto hi = static_cast<std::uint32_t>(s >> 32);
+    return static_cast<float>(hi) / 2147483648.0f - 1.0f;
+  }
+};
+
+bool close(const std::vector<float>& got, const std::vector<float>& want, double* worst) {
+  double w = 0.0;
+  bool ok = got.size() == want.size();
+  for (std::size_t i = 0; ok && i < got.size(); ++i) {
+    const double err = std::fabs(static_cast<double>(got[i]) - want[i]);
+    const double bound = 1e-5 + 1e-4 * std::fabs(static_cast<double>(want[i]));
+    w = std::max(w, err / bound);
+    ok = ok && err <= bound;
+  }
+  if (worst) *worst = w;
+  return ok;
+}
+
+// ---------------------------------------------------------------- CPU only
+
+void test_speculative_merge() {
+  using dbinfer_amd::model::speculative_merge;
+  {
+    const std::int32_t d[3] = {10, 20, 30}, t[4] = {10, 20, 30, 40};
+    std::vector<std::int32_t> out;
+    const std::size_t a = speculative_merge({d, 3}, {t, 4}, out);
+    check(a == 3 && out == std::vector<std::int32_t>{10, 20, 30, 40}, "merge all-accept emits bonus");
+  }
+  {
+    const std::int32_t d[3] = {10, 99, 30}, t[4] = {10, 20, 30, 40};
+    std::vector<std::int32_t> out;
+    const std::size_t a = speculative_merge({d, 3}, {t, 4}, out);
+    check(a == 1 && out == std::vector<std::int32_t>{10, 20}, "merge reject-at-1 emits correction");
+  }
+  {
+    const std::int32_t d[2] = {5, 6}, t[3] = {9, 8, 7};
+    std::vector<std::int32_t> out;
+    const std::size_t a = speculative_merge({d, 2}, {t, 3}, out);
+    check(a == 0 && out == std::vector<std::int32_t>{9}, "merge reject-at-0 emits target argmax");
+  }
+}
+
+void test_rope_matches_oracle() {
+  const std::size_t heads = 3, hd = 128;
+  const std::int32_t pos[2] = {7, 32767};
+  Lcg rng{0x5EED};
+  std::vector<float> a(heads * 2 * hd);
+  for (auto& x : a) x = rng.next();
+  std::vector<float> b = a;
+  dbinfer_amd::model::rope(a.data(), pos, 1e6f, heads, 2, hd);
+  ok_rope(b.data(), pos, 1e6f, heads, 2, hd);
+  check(std::memcmp(a.data(), b.data(), a.size() * 4) == 0, "host rope bitwise == oracle rope");
+}
+
+// ---------------------------------------------------------------- GPU
+
+void test_ring_case(std::size_t n_sink, std::size_t window, std::size_t n_seen) {
+  KVCache kv(1, 0, 1, 1, KvPolicy{n_sink, window, KvDtype::F32}, 1e6f);
+  bool slots_ok = true;
+  for (std::size_t t = 0; t < n_seen; ++t) {
+    const float payload = static_cast<float>(t);
+    const std::size_t want = t < n_sink ? t : n_sink + (t - n_sink) % window;
+    slots_ok = slots_ok && kv.slot_for(t) == want;
+    kv.append(0, t, &payload, &payload);
+  }
+  char name[160];
+  std::snprintf(name, sizeof name, "(sink=%zu win=%zu seen=%zu)", n_sink, window, n_seen);
+  check(kv.ok() && slots_ok, std::string("slot_for matches reference ") + name);
+  std::vector<KVCache::Resident> res(kv.capacity());
+  const std::size_t n_res = kv.residents(res.data());
+  const std::vector<float> keys = kv.export_f32(DBI_EXPORT_K, 0);
+  const std::size_t sinks = std::min(n_seen, n_sink);
+  std::size_t ws = n_sink;
+  if (n_seen > n_sink && n_seen - n_sink > window) ws = n_seen - window;
+  const std::size_t wlen = n_seen > n_sink ? n_seen - ws : 0;
+  check(n_res == sinks + wlen, std::string("n_res == sinks+window ") + name);
+  bool pinned = true, recent = true, packed = true;
+  for (std::size_t r = 0; r < sinks; ++r)
+    pinned = pinned && res[r].slot == r && keys[res[r].slot] == static_cast<float>(r);
+  for (std::size_t r = sinks; r < n_res; ++r)
+    recent = recent && keys[res[r].slot] == static_cast<float>(ws + (r - sinks));
+  std::vector<std::size_t> slots;
+  for (std::size_t r = 0; r < n_res; ++r) {
+    packed = packed && res[r].rope_pos == static_cast<std::int32_t>(r);
+    slots.push_back(res[r].slot);
+  }
+  std::sort(slots.begin(), slots.end());
+  check(pinned, std::string("sinks never evicted ") + name);
+  check(recent, std::string("window holds most recent tokens ") + name);
+  check(packed, std::string("rope positions pack to [0,n_res) ") + name);
+  check(std::adjacent_find(slots.begin(), slots.end()) == slots.end(),
+        std::string("resident slots are distinct ") + name);
+}
+
+void test_int8_roundtrip() {
+  const std::size_t nkv = 3, hd = 40, slots = 5;
+  Lcg rng{0xC0FFEE};
+  KVCache kv(1, slots, nkv, hd, KvPolicy{0, 0, KvDtype::Int8});
+  std::vector<float> k(nkv * hd), v(nkv * hd);
+  bool ok = true;
+  for (std::size_t s = 0; s < slots; ++s) {
+    for (auto& x : k) x = rng.next() * 7.0f;
+    for (auto& x : v) x = rng.next() * 0.03f;
+    kv.append(0, s, k.data(), v.data());
+    const auto k8 = kv.export_i8(DBI_EXPORT_K8, 0);
+    const auto ks = kv.export_f32(DBI_EXPORT_K_SCALE, 0);
+    for (std::size_t h = 0; h < nkv; ++h)
+      for (std::size_t i = 0; i < hd; ++i) {
+        const float sc = ks[(s / 32 * nkv + h) * hd + i];
+        const float err = std::fabs(k[h * hd + i] - sc * static_cast<float>(k8[(s * nkv + h) * hd + i]));
+        ok = ok && err <= sc + 1e-6f;
+      }
+  }
+  check(kv.ok() && ok, "per-channel key quant/dequant error within one scale step");
+}
+
+void test_int8_attention_vs_fp32() {
+  const std::size_t hd = 64, keys = 48;
+  Lcg rng{0x1357};
+  std::vector<float> q(hd), k(keys * hd), v(keys * hd);
+  for (auto& x : q) x = rng.next();
+  for (auto& x : k) x = rng.next();
+  for (auto& x : v) x = rng.next();
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+  KVCache f(1, keys, 1, hd), i8(1, keys, 1, hd, KvPolicy{0, 0, KvDtype::Int8});
+  f.append_n(0, 0, keys, k.data(), v.data());
+  i8.append_n(0, 0, keys, k.data(), v.data());
+  std::vector<float> ref(hd), got(hd);
+  f.check(dbi_attn_decode(f.handle(), 0, keys - 1, 1, scale, q.data(), ref.data()));
+  i8.check(dbi_attn_decode(i8.handle(), 0, keys - 1, 1, scale, q.data(), got.data()));
+  double num = 0, den = 0;
+  for (std::size_t j = 0; j < hd; ++j) {
+    num += (got[j] - ref[j]) * (got[j] - ref[j]);
+    den += ref[j] * ref[j];
+  }
+  const double rel = std::sqrt(num / den);
+  std::printf("int8 attention relative L2 = %.5f\n", rel);
+  check(f.ok() && i8.ok() && rel <= 0.006, "int8 attention within 0.6% relative L2 of fp32");
+}
+
+// decode_layer's attention half on the device vs the oracle's reference flow
+void test_decode_layer_parity(KvPolicy pol, const Config& cfg, std::size_t layers,
+                              std::size_t steps, const char* name) {
+  const std::size_t cap = pol.window ? 0 : steps + 1;
+  KVCache kv(layers, cap, cfg.n_kv_heads, cfg.head_dim, pol, cfg.rope_theta);
+  okv* o = okv_create(layers, cap, cfg.n_kv_heads, cfg.head_dim, pol.n_sink, pol.window,
+                      pol.dtype == KvDtype::Int8 ? OKV_INT8 : OKV_F32);
+  const std::size_t qn = cfg.n_heads * cfg.head_dim, kn = cfg.n_kv_heads * cfg.head_dim;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(cfg.head_dim));
+  Lcg rng{0xABC + steps};
+  bool ok = kv.ok();
+  double worst = 0;
+  for (std::size_t t = 0; t < steps && ok; ++t) {
+    for (std::size_t l = 0; l < layers && ok; ++l) {
+      std::vector<float> q(qn), k(kn), v(kn), out(qn), want(qn);
+      for (auto& x : q) x = rng.next();
+      for (auto& x : k) x = rng.next();
+      for (auto& x : v) x = rng.next();
+      std::vector<float> q0 = q, k0 = k;  // un-roped copies for the oracle
+      const auto pos = static_cast<std::int32_t>(t);
+      ok = dbinfer_amd::model::decode_attention(kv, cfg, l, pos, q.data(), k.data(), v.data(),
+                                                out.data());
+      if (pol.window) {
+        okv_attend_ring(o, l, t, cfg.n_heads, scale, cfg.rope_theta, q0.data(), k0.data(),
+                        v.data(), want.data(), 1);
+      } else {
+        ok_rope(q0.data(), &pos, cfg.rope_theta, cfg.n_heads, 1, cfg.head_dim);
+        ok_rope(k0.data(), &pos, cfg.rope_theta, cfg.n_kv_heads, 1, cfg.head_dim);
+        okv_append(o, l, t, k0.data(), v.data());
+        if (pol.dtype == KvDtype::Int8)
+          okv_attend_dense_int8(o, l, t, cfg.n_heads, scale, q0.data(), want.data(), 1);
+        else
+          okv_attend_dense_f32(o, l, t, cfg.n_heads, scale, q0.data(), want.data(), 1);
+      }
+      double w = 0;
+      ok = ok && close(out, want, &w);
+      worst = std::max(worst, w);
+    }
+  }
+  std::printf("  %s worst err/bound %.3f\n", name, worst);
+  check(ok, std::string("decode_layer attention parity: ") + name);
+  okv_destroy(o);
+}
+
+// chunk attention (append all, then causal rows) vs the oracle chunk, and vs
+// per-token decode on a second cache
+void test_chunk_parity(KvDtype dt) {
+  const Config cfg{32, 8, 64, 5e5f};
+  const std::size_t pos0 = 40, n = 24, cap = 80;
+  KVCache kv(1, cap, cfg.n_kv_heads, cfg.head_dim, KvPolicy{4, 0, dt});
+  KVCache tok(1, cap, cfg.n_kv_heads, cfg.head_dim, KvPolicy{4, 0, dt});
+  okv* o = okv_create(1, cap, cfg.n_kv_heads, cfg.head_dim, 4, 0,
+                      dt == KvDtype::Int8 ? OKV_INT8 : OKV_F32);
+  const std::size_t qn = cfg.n_heads * cfg.head_dim, kn = cfg.n_kv_heads * cfg.head_dim;
+  Lcg rng{0x77};
+  std::vector<float> pk(pos0 * kn), pv(pos0 * kn);
+  for (auto& x : pk) x = rng.next();
+  for (auto& x : pv) x = rng.next();
+  kv.append_n(0, 0, pos0, pk.data(), pv.data());
+  tok.append_n(0, 0, pos0, pk.data(), pv.data());
+  for (std::size_t p = 0; p < pos0; ++p) okv_append(o, 0, p, pk.data() + p * kn, pv.data() + p * kn);
+  std::vector<float> q(n * qn), k(n * kn), v(n * kn), out(n * qn), want(n * qn);
+  for (auto& x : q) x = rng.next();
+  for (auto& x : k) x = rng.next();
+  for (auto& x : v) x = rng.next();
+  std::vector<float> q0 = q, k0 = k, q1 = q, k1 = k;
+  dbinfer_amd::model::chunk_attention(kv, cfg, 0, pos0, n, q.data(), k.data(), v.data(), out.data());
+  for (std::size_t c = 0; c < n; ++c) {
+    const auto p = static_cast<std::int32_t>(pos0 + c);
+    ok_rope(q0.data() + c * qn, &p, cfg.rope_theta, cfg.n_heads, 1, cfg.head_dim);
+    ok_rope(k0.data() + c * kn, &p, cfg.rope_theta, cfg.n_kv_heads, 1, cfg.head_dim);
+    okv_append(o, 0, pos0 + c, k0.data() + c * kn, v.data() + c * kn);
+  }
+  okv_attend_chunk(o, 0, pos0, n, cfg.n_heads, 1.0f / 8.0f, q0.data(), want.data(), 1);
+  double w = 0;
+  const bool ok_oracle = kv.ok() && close(out, want, &w);
+  // per-token decode on the second cache (fp32: the chunk's rows see the
+  // same keys; int8: a row attends the cache as it stands after all n
+  // appends, so per-token decode differs by design and is not compared)
+  bool ok_tok = true;
+  if (dt == KvDtype::F32) {
+    for (std::size_t c = 0; c < n; ++c) {
+      std::vector<float> row(qn);
+      dbinfer_amd::model::decode_attention(tok, cfg, 0, static_cast<std::int32_t>(pos0 + c),
+                                           q1.data() + c * qn, k1.data() + c * kn,
+                                           v.data() + c * kn, row.data());
+      std::vector<float> ch(out.begin() + c * qn, out.begin() + (c + 1) * qn);
+      ok_tok = ok_tok && close(row, ch, nullptr);
+    }
+  }
+  check(ok_oracle, std::string("chunk attention parity vs oracle ") +
+                       (dt == KvDtype::Int8 ? "int8" : "fp32"));
+  check(ok_tok, std::string("chunk rows == per-token decode ") +
+                    (dt == KvDtype::Int8 ? "int8" : "fp32"));
+  okv_destroy(o);
+}
+
+void test_prefix_cache() {
+  const Config cfg{14, 2, 64, 1e6f};
+  const std::size_t L = 3, cap = 64, n = 20;
+  const std::vector<std::int32_t> prompt = {40, 1079, 264, 4128, 1614, 13, 7, 7, 9, 11,
+                                            12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22};
+  KVCache a(L, cap, cfg.n_kv_heads, cfg.head_dim), b(L, cap, cfg.n_kv_heads, cfg.head_dim);
+  const std::size_t qn = cfg.n_heads * cfg.head_dim, kn = cfg.n_kv_heads * cfg.head_dim;
+  Lcg rng{0x9797};
+  std::vector<float> k(n * kn), v(n * kn);
+  for (auto& x : k) x = rng.next();
+  for (auto& x : v) x = rng.next();
+  for (std::size_t l = 0; l < L; ++l) a.append_n(l, 0, n, k.data(), v.data());
+  const std::string path = "/tmp/dbi_host_test_prefix.kv";
+  auto saved = dbinfer_amd::model::save_kv_prefix(a, path, {prompt.data(), n});
+  check(static_cast<bool>(saved), "save_kv_prefix succeeds");
+  auto loaded = dbinfer_amd::model::load_kv_prefix(b, path, {prompt.data(), prompt.size()});
+  check(loaded && *loaded == n && b.n_seen() == n, "load_kv_prefix restores length");
+  // next token's attention after resume is bitwise equal (kv_prefix_cache_test.cpp:90-130)
+  std::vector<float> q(qn), kk(kn), vv(kn);
+  for (auto& x : q) x = rng.next();
+  for (auto& x : kk) x = rng.next();
+  for (auto& x : vv) x = rng.next();
+  bool same = true;
+  for (std::size_t l = 0; l < L; ++l) {
+    std::vector<float> qa = q, qb = q, ka = kk, kb = kk, oa(qn), ob(qn);
+    dbinfer_amd::model::decode_attention(a, cfg, l, n, qa.data(), ka.data(), vv.data(), oa.data());
+    dbinfer_amd::model::decode_attention(b, cfg, l, n, qb.data(), kb.data(), vv.data(), ob.data());
+    same = same && std::memcmp(oa.data(), ob.data(), qn * 4) == 0;
+  }
+  check(a.ok() && b.ok() && same, "resumed cache: next-token attention bitwise equal");
+  auto missing = dbinfer_amd::model::load_kv_prefix(b, "/tmp/does/not/exist.kv",
+                                                    {prompt.data(), prompt.size()});
+  check(!missing && missing.error().message.rfind("cannot open kv prefix cache", 0) == 0,
+        "missing prefix file is an error");
+  std::remove(path.c_str());
+}
+
+void test_speculative_rollback() {
+  // verify round: append [last, d1..d4] at pos, attend, accept a, commit;
+  // the next round's attention equals a cache that only ever saw the
+  // accepted rows (stale rejected rows are beyond n_seen and never read)
+  const Config cfg{32, 8, 128, 1e6f};
+  const std::size_t cap = 64, pos = 30, k = 4, accepted = 2;
+  const std::size_t qn = cfg.n_heads * cfg.head_dim, kn = cfg.n_kv_heads * cfg.head_dim;
+  KVCache spec(1, cap, cfg.n_kv_heads, cfg.head_dim), ref(1, cap, cfg.n_kv_heads, cfg.head_dim);
+  Lcg rng{0x5150};
+  std::vector<float> pk(pos * kn), pv(pos * kn);
+  for (auto& x : pk) x = rng.next();
+  for (auto& x : pv) x = rng.next();
+  spec.append_n(0, 0, pos, pk.data(), pv.data());
+  ref.append_n(0, 0, pos, pk.data(), pv.data());
+  std::vector<float> q((k + 1) * qn), kk((k + 1) * kn), vv((k + 1) * kn), out((k + 1) * qn);
+  for (auto& x : q) x = rng.next();
+  for (auto& x : kk) x = rng.next();
+  for (auto& x : vv) x = rng.next();
+  std::vector<float> kref = kk;
+  dbinfer_amd::model::chunk_attention(spec, cfg, 0, pos, k + 1, q.data(), kk.data(), vv.data(),
+                                      out.data());
+  const std::int32_t next = dbinfer_amd::model::speculative_commit(spec, pos, accepted);
+  check(next == static_cast<std::int32_t>(pos + accepted + 1) && spec.n_seen() == pos + accepted + 1,
+        "rollback keeps pos + accepted + 1 positions");
+  // ref: the same rows, roped the same way, but only the accepted ones
+  for (std::size_t c = 0; c <= accepted; ++c) {
+    const auto p = static_cast<std::int32_t>(pos + c);
+    dbinfer_amd::model::rope(kref.data() + c * kn, &p, cfg.rope_theta, cfg.n_kv_heads, 1,
+                             cfg.head_dim);
+  }
+  ref.append_n(0, pos, accepted + 1, kref.data(), vv.data());
+  std::vector<float> qn1(qn), kn1(kn), vn1(kn);
+  for (auto& x : qn1) x = rng.next();
+  for (auto& x : kn1) x = rng.next();
+  for (auto& x : vn1) x = rng.next();
+  std::vector<float> qa = qn1, qb = qn1, ka = kn1, kb = kn1, oa(qn), ob(qn);
+  dbinfer_amd::model::decode_attention(spec, cfg, 0, next, qa.data(), ka.data(), vn1.data(), oa.data());
+  dbinfer_amd::model::decode_attention(ref, cfg, 0, next, qb.data(), kb.data(), vn1.data(), ob.data());
+  check(spec.ok() && ref.ok() && std::memcmp(oa.data(), ob.data(), qn * 4) == 0,
+        "next round after rollback == cache without the rejected rows (bitwise)");
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu-only") == 0;
+  test_speculative_merge();
+  test_rope_matches_oracle();
+  if (!cpu_only) {
+    const std::size_t ring_cases[8][3] = {{4, 8, 40}, {4, 8, 12}, {4, 8, 11}, {0, 8, 40},
+                                          {1, 4, 40}, {4, 8, 4},  {4, 8, 2},  {4, 8, 100}};
+    for (const auto& c : ring_cases) test_ring_case(c[0], c[1], c[2]);
+    test_int8_roundtrip();
+    test_int8_attention_vs_fp32();
+    test_decode_layer_parity({0, 0, KvDtype::F32}, {32, 4, 64, 1e4f}, 2, 40, "dense fp32 gqa8 hd64");
+    test_decode_layer_parity({4, 0, KvDtype::Int8}, {24, 8, 128, 5e5f}, 2, 40, "dense int8 gqa3 hd128");
+    test_decode_layer_parity({4, 16, KvDtype::F32}, {28, 4, 128, 1e6f}, 2, 50, "ring fp32 gqa7 hd128");
+    test_decode_layer_parity({4, 16, KvDtype::Int8}, {28, 4, 128, 1e6f}, 2, 50, "ring int8 gqa7 hd128");
+    test_chunk_parity(KvDtype::F32);
+    test_chunk_parity(KvDtype::Int8);
+    test_prefix_cache();
+    test_speculative_rollback();
+  }
+  std::printf("---\n%d checks failed\n", g_failures);
+  return g_failures == 0 ? 0 : 1;
+}
