@@ -200,6 +200,11 @@ void okv_append(okv* kv, size_t layer, size_t pos, const float* k, const float* 
   kv->n_seen = pos + 1;
 }
 
+void okv_append_n(okv* kv, size_t layer, size_t pos0, size_t n, const float* k, const float* v) {
+  for (size_t r = 0; r < n; ++r)
+    okv_append(kv, layer, pos0 + r, k + r * kv->pos_stride, v + r * kv->pos_stride);
+}
+
 /* model.cpp:406-418 */
 size_t okv_residents(const okv* kv, size_t* slot, int32_t* rope_pos) {
   const size_t n_sink = kv->n_sink_policy, window = kv->window, n_seen = kv->n_seen;

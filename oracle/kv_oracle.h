@@ -75,6 +75,9 @@ void ok_quant_head(const float* src, size_t n, int8_t* dst, float* scales);
 size_t okv_slot_for(const okv* kv, size_t pos);
 /* model.cpp:357-404 (requantize_kgroup :329-355 inside) */
 void okv_append(okv* kv, size_t layer, size_t pos, const float* k, const float* v);
+/* n sequential okv_append calls at pos0..pos0+n-1 (the append loop of
+ * decode_layer_chunk, model.cpp:935-954); k, v are [n][pos_stride]. */
+void okv_append_n(okv* kv, size_t layer, size_t pos0, size_t n, const float* k, const float* v);
 /* model.cpp:406-418; writes up to capacity entries, returns the count */
 size_t okv_residents(const okv* kv, size_t* slot, int32_t* rope_pos);
 /* reset() model.hpp:164 is truncate(0); mark_position(p) model.hpp:182 is truncate(p+1) */

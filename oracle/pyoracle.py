@@ -46,6 +46,7 @@ _SIGS = {
     "okv_destroy": (None, [_P]),
     "okv_slot_for": (_sz, [_P, _sz]),
     "okv_append": (None, [_P, _sz, _sz, _vp, _vp]),
+    "okv_append_n": (None, [_P, _sz, _sz, _sz, _vp, _vp]),
     "okv_residents": (_sz, [_P, _vp, _vp]),
     "okv_truncate": (None, [_P, _sz]),
     "ok_quant_head": (None, [_vp, _sz, _vp, _vp]),
@@ -189,8 +190,8 @@ class OracleKV:
     def append_n(self, layer: int, pos0: int, k, v) -> None:
         k = _f32(k).reshape(-1, self.pos_stride)
         v = _f32(v).reshape(-1, self.pos_stride)
-        for r in range(k.shape[0]):
-            self.append(layer, pos0 + r, k[r], v[r])
+        assert k.shape == v.shape
+        self._lib.okv_append_n(self._p, layer, pos0, k.shape[0], k.ctypes.data, v.ctypes.data)
 
     def slot_for(self, pos: int) -> int:
         return int(self._lib.okv_slot_for(self._p, pos))
