@@ -40,12 +40,12 @@ dbi_status hip_fail(hipError_t e, const char* what) {
   } while (0)
 
 template <typename T>
-hipError_t dalloc(T** p, size_t n) {
+hipError_t dalloc(T** p, size_t n, int fill = 0) {
   *p = nullptr;
   if (n == 0) return hipSuccess;
   hipError_t e = hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T));
   if (e != hipSuccess) return e;
-  return hipMemset(*p, 0, n * sizeof(T));
+  return hipMemset(*p, fill, n * sizeof(T));
 }
 
 void free_store(dbi::KvStore& s) {
@@ -214,21 +214,23 @@ dbi_status dbi_kv_create(const dbi_kv_config* cfg, dbi_kv** out) {
   g.window = static_cast<int>(cfg->window);
   g.n_sink = static_cast<int>(cfg->n_sink);
   g.ngroups = (g.cap + dbi::kKGroup - 1) / dbi::kKGroup;
+  g.capg = (g.cap + dbi::kCapAlign - 1) / dbi::kCapAlign * dbi::kCapAlign;
+  g.tiled = g.hd == 64 || g.hd == 128;
   (void)hipGetDevice(&kv->device);
 
-  const size_t cells = size_t(g.n_layers) * g.nkv * g.cap * g.hd;
-  const size_t scales = size_t(g.n_layers) * g.nkv * g.cap * g.nb;
+  const size_t cells = size_t(g.n_layers) * g.nkv * dbi::head_elems(g);
+  const size_t scales = size_t(g.n_layers) * g.nkv * g.capg * g.nb;
   dbi::KvStore& s = kv->store;
   hipError_t e = hipSuccess;
-  auto A = [&](auto** p, size_t n) {
-    if (e == hipSuccess) e = dalloc(p, n);
+  auto A = [&](auto** p, size_t n, int fill = 0) {
+    if (e == hipSuccess) e = dalloc(p, n, fill);
   };
   if (!g.int8) {
     A(&s.k, cells);
     A(&s.v, cells);
   } else {
-    A(&s.k8, cells);
-    A(&s.v8, cells);
+    A(&s.k8, cells, 0x80);  // biased code of 0, like the reference's zeroed storage
+    A(&s.v8, cells, 0x80);
     A(&s.v_scale, scales);
     if (g.ring) {
       A(&s.k_scale, scales);
@@ -458,12 +460,13 @@ dbi_status dbi_kv_prefix_save(dbi_kv* kv, const char* path, const int32_t* token
   float* dev = nullptr;
   if (hipMalloc(reinterpret_cast<void**>(&dev), elems * sizeof(float)) != hipSuccess)
     return fail(DBI_ERR_NOMEM, "prefix staging allocation failed");
-  hipError_t e = dbi::launch_prefix_pack(g, kv->store.k, dev, static_cast<int>(len), kv->stream);
+  hipError_t e =
+      dbi::launch_prefix_pack(g, kv->store.k, dev, static_cast<int>(len), true, kv->stream);
   if (e == hipSuccess)
     e = hipMemcpyAsync(buf.data() + hdr, dev, elems * sizeof(float), hipMemcpyDeviceToHost,
                        kv->stream);
   if (e == hipSuccess)
-    e = dbi::launch_prefix_pack(g, kv->store.v, dev, static_cast<int>(len), kv->stream);
+    e = dbi::launch_prefix_pack(g, kv->store.v, dev, static_cast<int>(len), false, kv->stream);
   if (e == hipSuccess)
     e = hipMemcpyAsync(buf.data() + hdr + elems * sizeof(float), dev, elems * sizeof(float),
                        hipMemcpyDeviceToHost, kv->stream);
@@ -543,10 +546,11 @@ dbi_status dbi_kv_prefix_load(dbi_kv* kv, const char* path, const int32_t* token
   hipError_t e = hipMemcpyAsync(dev, data.data() + p, 2 * elems * sizeof(float),
                                 hipMemcpyHostToDevice, kv->stream);
   if (e == hipSuccess)
-    e = dbi::launch_prefix_unpack(g, dev, kv->store.k, static_cast<int>(prefix_len), kv->stream);
+    e = dbi::launch_prefix_unpack(g, dev, kv->store.k, static_cast<int>(prefix_len), true,
+                                  kv->stream);
   if (e == hipSuccess)
     e = dbi::launch_prefix_unpack(g, dev + elems, kv->store.v, static_cast<int>(prefix_len),
-                                  kv->stream);
+                                  false, kv->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(kv->stream);
   (void)hipFree(dev);
   if (e != hipSuccess) return hip_fail(e, "prefix upload");
@@ -586,42 +590,66 @@ dbi_status dbi_kv_export(dbi_kv* kv, uint32_t what, uint32_t layer, void* dst, s
   if (bytes != need) return fail(DBI_ERR_INVALID, "export size mismatch");
   const dbi::KvGeom& g = kv->geom;
   const dbi::KvStore& s = kv->store;
-  // head-major device arrays: [nkv][rows][inner] -> reference [rows][nkv][inner]
+  // head-major device arrays -> reference [rows][nkv][inner]; K/V codes and
+  // values are read back through the granule layout, int8 codes un-biased
+  enum Map { kRows, kKeys, kValues, kFlat };
   const void* src = nullptr;
-  size_t rows = 0, inner = 0, esz = 4;
-  bool head_major = true;
+  size_t rows = 0, inner = 0, esz = 4, dev_rows = 0;
+  Map map = kRows;
   switch (what) {
-    case DBI_EXPORT_K: src = s.k; rows = g.cap; inner = g.hd; break;
-    case DBI_EXPORT_V: src = s.v; rows = g.cap; inner = g.hd; break;
-    case DBI_EXPORT_K8: src = s.k8; rows = g.cap; inner = g.hd; esz = 1; break;
-    case DBI_EXPORT_V8: src = s.v8; rows = g.cap; inner = g.hd; esz = 1; break;
-    case DBI_EXPORT_V_SCALE: src = s.v_scale; rows = g.cap; inner = g.nb; break;
+    case DBI_EXPORT_K: src = s.k; map = kKeys; break;
+    case DBI_EXPORT_V: src = s.v; map = kValues; break;
+    case DBI_EXPORT_K8: src = s.k8; map = kKeys; esz = 1; break;
+    case DBI_EXPORT_V8: src = s.v8; map = kValues; esz = 1; break;
+    case DBI_EXPORT_V_SCALE: src = s.v_scale; rows = g.cap; dev_rows = g.capg; inner = g.nb; break;
     case DBI_EXPORT_K_SCALE:
       src = s.k_scale;
       rows = g.ring ? g.cap : g.ngroups;
+      dev_rows = g.ring ? g.capg : g.ngroups;
       inner = g.ring ? g.nb : g.hd;
       break;
-    case DBI_EXPORT_K_SINK: src = s.k_sink; rows = g.n_sink; inner = g.hd; break;
-    case DBI_EXPORT_V_SINK: src = s.v_sink; rows = g.n_sink; inner = g.hd; break;
-    case DBI_EXPORT_K_RAW: src = s.k_raw; rows = dbi::kKGroup; inner = g.hd; head_major = false; break;
+    case DBI_EXPORT_K_SINK: src = s.k_sink; rows = dev_rows = g.n_sink; inner = g.hd; break;
+    case DBI_EXPORT_V_SINK: src = s.v_sink; rows = dev_rows = g.n_sink; inner = g.hd; break;
+    case DBI_EXPORT_K_RAW:
+      src = s.k_raw; rows = dev_rows = dbi::kKGroup; inner = size_t(g.nkv) * g.hd; map = kFlat;
+      break;
     default: return fail(DBI_ERR_UNSUPPORTED, "unknown export");
   }
-  const size_t layer_bytes = size_t(g.nkv) * rows * inner * esz;
+  if (map == kKeys || map == kValues) {
+    rows = g.cap;
+    dev_rows = g.capg;
+    inner = g.hd;
+  }
+  const size_t layer_bytes = (map == kFlat ? 1 : size_t(g.nkv)) * dev_rows * inner * esz;
   std::vector<unsigned char> tmp(layer_bytes);
   hipError_t e = hipMemcpyAsync(tmp.data(), static_cast<const unsigned char*>(src) + layer * layer_bytes,
                                 layer_bytes, hipMemcpyDeviceToHost, kv->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(kv->stream);
   if (e != hipSuccess) return hip_fail(e, "export readback");
   unsigned char* out = static_cast<unsigned char*>(dst);
-  if (!head_major) {
+  if (map == kFlat) {
     std::memcpy(out, tmp.data(), layer_bytes);
     return DBI_OK;
   }
-  const size_t row_bytes = inner * esz;
+  if (map == kRows) {
+    const size_t row_bytes = inner * esz;
+    for (size_t kh = 0; kh < size_t(g.nkv); ++kh)
+      for (size_t r = 0; r < rows; ++r)
+        std::memcpy(out + (r * g.nkv + kh) * row_bytes, tmp.data() + (kh * dev_rows + r) * row_bytes,
+                    row_bytes);
+    return DBI_OK;
+  }
+  const size_t he = dbi::head_elems(g);
   for (size_t kh = 0; kh < size_t(g.nkv); ++kh)
-    for (size_t r = 0; r < rows; ++r)
-      std::memcpy(out + (r * g.nkv + kh) * row_bytes, tmp.data() + (kh * rows + r) * row_bytes,
-                  row_bytes);
+    for (int r = 0; r < g.cap; ++r)
+      for (int d = 0; d < g.hd; ++d) {
+        const size_t at = kh * he + (map == kKeys ? dbi::k_off(g, r, d) : dbi::v_off(g, r, d));
+        const size_t to = (size_t(r) * g.nkv + kh) * g.hd + d;
+        if (esz == 1)
+          out[to] = static_cast<unsigned char>(tmp[at] ^ 0x80u);
+        else
+          std::memcpy(out + to * 4, tmp.data() + at * 4, 4);
+      }
   return DBI_OK;
 }
 

@@ -5,7 +5,8 @@
 // Bit-exactness of the int8 paths rests on three facts: max|x| is
 // order-free, x / 127.0f and 1.0f / s are IEEE correctly rounded divisions
 // (HIP's default, never fast-math), and the code is round-half-away of one
-// fp32 product, clamped to [-127, 127] (quant_code below).
+// fp32 product, clamped to [-127, 127] (quant_code below). Codes are stored
+// biased, as the byte code + 128, in the granule layout of kv_internal.hpp.
 #include "kv_internal.hpp"
 
 namespace dbi {
@@ -38,6 +39,8 @@ __device__ __forceinline__ int8_t quant_lane(float x, float* scale) {
   return quant_code(x, inv);
 }
 
+__device__ __forceinline__ int8_t biased(int8_t code) { return static_cast<int8_t>(code ^ 0x80); }
+
 __device__ __forceinline__ int slot_for(int pos, int s, int W) {
   return pos < s ? pos : s + (pos - s) % W;
 }
@@ -66,9 +69,9 @@ __global__ __launch_bounds__(kThreads) void append_f32_kernel(KvGeom g, float* k
       slot = slot_for(p, g.n_sink, g.window);
     }
     const int kh = c / g.hd, i = c % g.hd;
-    const size_t dst = ((static_cast<size_t>(layer) * g.nkv + kh) * g.cap + slot) * g.hd + i;
-    kst[dst] = k[idx];
-    vst[dst] = v[idx];
+    const size_t hb = (static_cast<size_t>(layer) * g.nkv + kh) * head_elems(g);
+    kst[hb + k_off(g, slot, i)] = k[idx];
+    vst[hb + v_off(g, slot, i)] = v[idx];
   }
 }
 
@@ -97,10 +100,11 @@ __global__ __launch_bounds__(kThreads) void append_i8_ring_kernel(KvGeom g, KvSt
   const int8_t vc = quant_lane(vx, &vs);
   if (!ring_row_final(p, pos0 + n, g.n_sink, g.window)) return;
   const int slot = slot_for(p, g.n_sink, g.window);
-  const size_t row = (static_cast<size_t>(layer) * g.nkv + kh) * g.cap + slot;
+  const size_t head = static_cast<size_t>(layer) * g.nkv + kh;
+  const size_t row = head * g.capg + slot;
   if (in) {
-    s.k8[row * g.hd + i] = kc;
-    s.v8[row * g.hd + i] = vc;
+    s.k8[head * head_elems(g) + k_off(g, slot, i)] = biased(kc);
+    s.v8[head * head_elems(g) + v_off(g, slot, i)] = biased(vc);
   }
   if (t == 0) {
     s.k_scale[row * g.nb + b] = ks;
@@ -150,7 +154,7 @@ __global__ __launch_bounds__(kThreads) void append_i8_dense_kernel(KvGeom g, KvS
 #pragma unroll
       for (int w = 0; w < kKGroup; ++w)
         if (w <= within && first + w >= g.n_sink)
-          s.k8[(head * g.cap + first + w) * g.hd + i] = quant_code(rv[w], inv);
+          s.k8[head * head_elems(g) + k_off(g, first + w, i)] = biased(quant_code(rv[w], inv));
       p = hi + 1;
     }
     return;
@@ -179,9 +183,8 @@ __global__ __launch_bounds__(kThreads) void append_i8_dense_kernel(KvGeom g, KvS
   }
   float vs;
   const int8_t vc = quant_lane(vx, &vs);
-  const size_t row = head * g.cap + p;
-  if (in) s.v8[row * g.hd + i] = vc;
-  if (t == 0) s.v_scale[row * g.nb + b] = vs;
+  if (in) s.v8[head * head_elems(g) + v_off(g, p, i)] = biased(vc);
+  if (t == 0) s.v_scale[(head * g.capg + p) * g.nb + b] = vs;
 }
 
 int grid_for(size_t work) {
@@ -189,9 +192,10 @@ int grid_for(size_t work) {
   return static_cast<int>(blocks < 65536 ? (blocks == 0 ? 1 : blocks) : 65536);
 }
 
-// [L][len][nkv][hd] <-> [L][nkv][cap][hd]
+// [L][len][nkv][hd] <-> the head-major K (is_k) or V store
 __global__ __launch_bounds__(kThreads) void prefix_pack_kernel(KvGeom g, const float* store,
-                                                               float* dst, int len, int unpack) {
+                                                               float* dst, int len, int unpack,
+                                                               int is_k) {
   const size_t P = static_cast<size_t>(g.nkv) * g.hd;
   const size_t total = static_cast<size_t>(g.n_layers) * len * P;
   for (size_t idx = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; idx < total;
@@ -201,7 +205,9 @@ __global__ __launch_bounds__(kThreads) void prefix_pack_kernel(KvGeom g, const f
     const size_t p = rem / P;
     const size_t kh = (rem % P) / g.hd;
     const size_t i = rem % g.hd;
-    const size_t st = ((l * g.nkv + kh) * g.cap + p) * g.hd + i;
+    const size_t st = (l * g.nkv + kh) * head_elems(g) +
+                      (is_k ? k_off(g, static_cast<int>(p), static_cast<int>(i))
+                            : v_off(g, static_cast<int>(p), static_cast<int>(i)));
     if (unpack)
       const_cast<float*>(store)[st] = dst[idx];
     else
@@ -233,18 +239,18 @@ hipError_t launch_append(const KvGeom& g, const KvStore& s, int layer, int pos0,
 }
 
 hipError_t launch_prefix_pack(const KvGeom& g, const float* src_store, float* dst, int len,
-                              hipStream_t st) {
+                              bool is_k, hipStream_t st) {
   const size_t total = static_cast<size_t>(g.n_layers) * len * g.nkv * g.hd;
   hipLaunchKernelGGL(prefix_pack_kernel, dim3(grid_for(total)), dim3(kThreads), 0, st, g,
-                     src_store, dst, len, 0);
+                     src_store, dst, len, 0, is_k ? 1 : 0);
   return hipGetLastError();
 }
 
 hipError_t launch_prefix_unpack(const KvGeom& g, const float* src, float* dst_store, int len,
-                                hipStream_t st) {
+                                bool is_k, hipStream_t st) {
   const size_t total = static_cast<size_t>(g.n_layers) * len * g.nkv * g.hd;
   hipLaunchKernelGGL(prefix_pack_kernel, dim3(grid_for(total)), dim3(kThreads), 0, st, g,
-                     dst_store, const_cast<float*>(src), len, 1);
+                     dst_store, const_cast<float*>(src), len, 1, is_k ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -7,34 +7,41 @@
 //    all G = gqa query heads of that head from the same bytes, so K/V cross
 //    HBM once per kv head (the reference re-reads them per query head,
 //    model.cpp:575-596).
-//  - The query group (G x HD floats) is staged once in LDS: roped (ring) and
-//    pre-scaled by scale*log2(e) so softmax runs on exp2.
-//  - A wave owns 32-position tiles (tile t -> wave t % 8). Inside a tile each
-//    "lane row" of LPR = HD/EPL lanes holds EPL elements of one position, a
-//    wave covers 64/LPR positions per load and each load instruction reads
-//    contiguous 64-128 B runs of a row. All loads of a step (K, V and their
-//    scales) are issued before anything waits on them.
-//  - Each lane row keeps its own online-softmax state (m, l, o[EPL]); the QK
-//    partial dot is reduced over the LPR lanes with DPP row ops; lane rows are
-//    merged with DPP row_ror and the gfx950 permlane16/32 swaps (no LDS
-//    crossbar); the 8 waves merge through LDS.
+//  - A wave handles 32-position chunks (16 for the ring and for wide fp32
+//    groups), chunk t -> wave t % 8, in the granule layout of
+//    kv_internal.hpp: every load instruction reads 64 lanes x 8 elements,
+//    contiguous. A "lane row" of LPR = hd/8 lanes holds one position; RPW =
+//    64/LPR rows per instruction.
+//  - QK: each lane keeps the partial dots of its 8 dims for the NSG slots of
+//    a granule. K's slot order is permuted per lane (kslot_xor) so that the
+//    16-lane (hd 128) or 8-lane (hd 64) reduction is a transposing one: three
+//    DPP adds halve the slots and sum across lanes at once, and every lane
+//    ends up holding ONE position's full score (each position in 4 lanes).
+//    Softmax then runs once per position instead of once per lane row.
+//  - Softmax: wave-uniform running max (DPP row max, row_bcast15/31,
+//    readlane), exp2 with scale*log2(e) folded into q; weights go through a
+//    per-wave LDS buffer to the PV lane mapping (lane = 8 consecutive V dims
+//    of one position row).
+//  - Loads: K of the next chunk is issued right after QK, V of the next
+//    chunk right after PV, so one of them is always in flight.
 //  - Split-K: each split writes (o[G][HD], m[G], l[G]) of its range; a small
 //    merge kernel, the next launch on the stream, combines the splits of every
-//    (row, query head) with all loads in one round and writes out = o / l.
-//    The kernel boundary is the release/acquire: inside one kernel, making
-//    one workgroup's stores visible to another across the per-XCD L2 caches
-//    takes an agent-scope fence (a whole-L2 writeback) per workgroup.
-//  - int8 dense: a tile is exactly one 32-token K group, so the per-channel K
-//    scale folds into q once per tile (qs = q * ks, the reference's
-//    (q_i * ks_i) * k8_i); V's per-block scale folds into the softmax weight
-//    ((w * vs_b) * v8_i). Sinks (pos < n_sink) come from the fp32 arrays.
+//    (row, query head) and writes out = o / l. The kernel boundary is the
+//    release/acquire: inside one kernel, making one workgroup's stores visible
+//    to another across the per-XCD L2 caches takes an agent-scope fence (a
+//    whole-L2 writeback) per workgroup.
+//  - int8 dense: a 32-position chunk is exactly one K group, so the
+//    per-channel K scale folds into q once per chunk (the reference's
+//    (q_i * ks_i) * k8_i); codes are stored biased (+128) and converted with
+//    one v_cvt_f32_ubyteN each, the bias removed through -128 * sum(q*ks) (K)
+//    and -128 * sum(w*vs) (V). The fp32 sinks (pos < n_sink) are attended
+//    by the merge kernel as one more split.
 //  - ring: keys are stored un-roped; each resident key is dequantized (int8:
 //    per-block scale) and roped at its cache-relative position from an fp32
-//    cos/sin table once per kv head, q at n_res - 1. The lane element mapping
-//    keeps dim d and d + HD/2 in one lane, so the rotation is lane-local.
+//    cos/sin table, q at n_res - 1 (model.cpp:662-700). K lanes hold dims d
+//    and d + hd/2 together, so the rotation is lane-local.
 #include <cmath>
 #include <cstdlib>
-#include <type_traits>
 
 #include "kv_internal.hpp"
 
@@ -43,7 +50,6 @@ namespace {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kTile = 32;
 constexpr int kMaxSplits = 32;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMinit = -1.0e30f;  // finite: exp2(kMinit - kMinit) == 1, no NaN
@@ -53,20 +59,23 @@ enum Kind { kF32Dense = 0, kI8Dense = 1, kF32Ring = 2, kI8Ring = 3 };
 struct AttnParams {
   const float* kf;
   const float* vf;
-  const int8_t* k8;
-  const int8_t* v8;
+  const uint8_t* k8;
+  const uint8_t* v8;
   const float* ks;
   const float* vs;
   const float* ksink;
   const float* vsink;
   const float2* rope;
+  int rope_rows;
   const float* q;
   float* out;
   float* part;
-  int cap, ng, n_sink, nkv, n_heads;
+  int capg, ng, n_sink, nkv, n_heads;
   int rows, pos0;
   int ring_nres, ring_s, ring_W, ring_base;
-  int nsplit, tiles_per_split;
+  int nsplit;  // splits (partial records) per (row, kv head)
+  int direct;  // 1: single split and no sinks, write the output directly
+  int chunks_per_split;
   float qscale;
 };
 
@@ -79,605 +88,176 @@ __device__ __forceinline__ float dpp(float x) {
       float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 
-// Sum over the LPR consecutive lanes of a lane row (all lanes get the sum).
-template <int LPR>
-__device__ __forceinline__ float row_sum(float x) {
-  if constexpr (LPR >= 2) x += dpp<0xB1>(x);    // quad_perm [1,0,3,2]
-  if constexpr (LPR >= 4) x += dpp<0x4E>(x);    // quad_perm [2,3,0,1]
-  if constexpr (LPR >= 8) x += dpp<0x141>(x);   // row_half_mirror
-  if constexpr (LPR >= 16) x += dpp<0x140>(x);  // row_mirror
-  if constexpr (LPR >= 32) x += __shfl_xor(x, 16);
-  if constexpr (LPR >= 64) x += __shfl_xor(x, 32);
-  return x;
+// DPP controls: lane ^ 8 within a 16-lane row (row_ror:8), lane ^ 7 within
+// 8 lanes (row_half_mirror), lane ^ 2 and lane ^ 1 (quad_perm).
+constexpr int kX8 = 0x128, kX7 = 0x141, kX2 = 0x4E, kX1 = 0xB1;
+
+// Row-broadcast step of a wave reduction: rows in ROWMASK combine with the
+// last lane of the row(s) before them, the other rows with `idle`.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float bcast(float x, float idle) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, idle), __builtin_bit_cast(int, x),
+                                         CTRL, ROWMASK, 0xF, false));
 }
 
-// The gfx950 permlane swaps exchange rows between their two register
-// operands. They are emitted through asm: the compiler's builtins for them
-// fold the two results into one when both are combined (r0 + r1 compiles to
-// r0 + r0). Both operands start as the same value; afterwards {a, b} hold
-// {own, partner} in a lane-dependent order, which is all a commutative
-// combine needs. The s_nop covers the VALU-write -> permlane-read hazard.
-template <int OFF>
-__device__ __forceinline__ void swap_pair(float x, float& a, float& b) {
-  a = x;
-  b = x;
-  if constexpr (OFF == 16) {
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  } else {
-    static_assert(OFF == 32, "swap offset");
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  }
+__device__ __forceinline__ float lane63(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+
+// Wave-uniform max / sum of one value per lane.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<kX8>(v));
+  v = fmaxf(v, dpp<kX7>(v));
+  v = fmaxf(v, dpp<kX2>(v));
+  v = fmaxf(v, dpp<kX1>(v));
+  v = fmaxf(v, bcast<0x142, 0xA>(v, v));  // row_bcast:15
+  v = fmaxf(v, bcast<0x143, 0xC>(v, v));  // row_bcast:31
+  return lane63(v);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<kX8>(v);
+  v += dpp<kX7>(v);
+  v += dpp<kX2>(v);
+  v += dpp<kX1>(v);
+  v += bcast<0x142, 0xA>(v, 0.0f);
+  v += bcast<0x143, 0xC>(v, 0.0f);
+  return lane63(v);
+}
+
+// gfx950 permlane swaps, emitted through asm (the compiler's builtins fold
+// the two results into one when both are used). swap32(a, b): lanes 0-31
+// end with {own a, a of lane + 32}, lanes 32-63 with {b of lane - 32, own
+// b}; swap16 does the same between even and odd 16-lane rows. a + b after
+// the swap is therefore a's pair sum in the lower half and b's in the upper.
+__device__ __forceinline__ float swap32_sum(float a, float b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+__device__ __forceinline__ float swap16_sum(float a, float b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
 }
 
 // Raw v_exp_f32 (2^x). Softmax weights below 2^-126 are far under the
 // output tolerance, so the denormal-range handling of exp2f is not needed.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// max / sum with the partner lane OFF rows away: OFF 4 is a rotation by 4
-// inside each 16-lane DPP row (after the OFF 8 step every lane has met the
-// other three lanes of its residue class), 8 is lane ^ 8 (row_ror:8), 16 and
-// 32 are lane ^ 16 / lane ^ 32 through the permlane swaps.
-template <int OFF>
-__device__ __forceinline__ float xmax(float x) {
-  if constexpr (OFF == 4) {
-    return fmaxf(x, dpp<0x124>(x));
-  } else if constexpr (OFF == 8) {
-    return fmaxf(x, dpp<0x128>(x));
-  } else {
-    float a, b;
-    swap_pair<OFF>(x, a, b);
-    return fmaxf(a, b);
-  }
+// Raw buffer resources (gfx9 descriptor word 3 = 0x00020000: 32-bit raw
+// data, bounds-checked against num_records bytes; reads past it return 0).
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), bytes,
+                                           0x00020000);
 }
-template <int OFF>
-__device__ __forceinline__ float xsum(float x) {
-  if constexpr (OFF == 4) {
-    return x + dpp<0x124>(x);
-  } else if constexpr (OFF == 8) {
-    return x + dpp<0x128>(x);
-  } else {
-    float a, b;
-    swap_pair<OFF>(x, a, b);
-    return a + b;
-  }
+__device__ __forceinline__ float4 load_b128(rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
-// Reductions over the lane rows of a wave (lanes sharing lane % LPR).
-template <int LPR>
-__device__ __forceinline__ float rows_max(float x) {
-  if constexpr (LPR <= 4) x = xmax<4>(x);
-  if constexpr (LPR <= 8) x = xmax<8>(x);
-  if constexpr (LPR <= 16) x = xmax<16>(x);
-  return xmax<32>(x);
+__device__ __forceinline__ uint2 load_b64(rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
-template <int LPR>
-__device__ __forceinline__ float rows_sum(float x) {
-  if constexpr (LPR <= 4) x = xsum<4>(x);
-  if constexpr (LPR <= 8) x = xsum<8>(x);
-  if constexpr (LPR <= 16) x = xsum<16>(x);
-  return xsum<32>(x);
+__device__ __forceinline__ float load_b32(rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 
-template <int N>
-struct VecLoad;
-template <>
-struct VecLoad<4> {
-  using T = unsigned;
-};
-template <>
-struct VecLoad<8> {
-  using T = uint2;
-};
-template <>
-struct VecLoad<16> {
-  using T = uint4;
-};
-
-// int8 code of byte b of w, biased by +128 (w ^ 0x80808080 per dword), as
-// float: one v_cvt_f32_ubyteN per element.
-__device__ __forceinline__ float u8f(unsigned w, int byte) {
-  return static_cast<float>((w >> (8 * byte)) & 0xFFu);
+// 8 biased int8 codes -> code + 128 as float (one v_cvt_f32_ubyteN each)
+__device__ __forceinline__ void cvt8(const uint2 w, float* f) {
+#pragma unroll
+  for (int b = 0; b < 4; ++b) f[b] = static_cast<float>((w.x >> (8 * b)) & 0xFFu);
+#pragma unroll
+  for (int b = 0; b < 4; ++b) f[4 + b] = static_cast<float>((w.y >> (8 * b)) & 0xFFu);
 }
 
-// Unpacks CH int8 codes to float, biased by +128 (callers subtract 128 times
-// the sum of their multipliers).
-template <int CH>
-__device__ __forceinline__ void unpack_biased(const typename VecLoad<CH>::T& raw, float* f) {
-  constexpr unsigned kFlip = 0x80808080u;
-  if constexpr (CH == 4) {
-    const unsigned w = raw ^ kFlip;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) f[b] = u8f(w, b);
-  } else if constexpr (CH == 8) {
-    const unsigned w0 = raw.x ^ kFlip, w1 = raw.y ^ kFlip;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) f[b] = u8f(w0, b);
-#pragma unroll
-    for (int b = 0; b < 4; ++b) f[4 + b] = u8f(w1, b);
-  } else {
-    const unsigned w[4] = {raw.x ^ kFlip, raw.y ^ kFlip, raw.z ^ kFlip, raw.w ^ kFlip};
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) f[4 * j + b] = u8f(w[j], b);
-  }
-}
-
-template <int HD, int G, int EPL, int KIND>
+template <int HD, int G, int KIND>
 struct Cfg {
   static constexpr bool kInt8 = (KIND == kI8Dense || KIND == kI8Ring);
   static constexpr bool kRing = (KIND == kF32Ring || KIND == kI8Ring);
-  static constexpr int LPR = HD / EPL;         // lanes per position row
-  static constexpr int RPW = 64 / LPR;         // positions per wave load
-  static constexpr int STEPS = kTile / RPW;    // row steps per tile
-  // dims per contiguous chunk: fp32 16 B loads; int8 one load per lane
-  // (dense) or two half-head loads (ring, so d and d + HD/2 share a lane)
-  static constexpr int CH = !kInt8 ? 4 : (kRing ? EPL / 2 : EPL);
-  static constexpr int NCH = EPL / CH;
-  // positions per lane per step, from a VGPR budget: q (or q*ks) and o take
-  // 2*G*EPL, each in-flight position its raw K/V, scales and rope table
-  // (two step buffers are live: the current one and the prefetched next one)
-  static constexpr int kBudget = (kInt8 && G >= 7) ? 150 : 170;
-  static constexpr int PER_POS = !kInt8 ? 2 * EPL + (kRing ? EPL : 0)
-                                        : EPL / 2 + NCH + (kRing ? NCH + EPL : 0);
-  static constexpr int FIXED = 2 * G * EPL + (kInt8 ? EPL : 0) + (KIND == kI8Dense ? 2 * EPL : 0);
-  static constexpr int UFIT = (kBudget - FIXED) / (2 * PER_POS);
-  static constexpr int UMAX = kInt8 ? 4 : 2;
-  static constexpr int UCAP = UFIT < 1 ? 1 : (UFIT > UMAX ? UMAX : UFIT);
-  static constexpr int UPOW = UCAP >= 4 ? 4 : (UCAP >= 2 ? 2 : 1);
-  static constexpr int U = STEPS < UPOW ? STEPS : UPOW;
+  static constexpr int LPR = HD / 8;            // lanes per position row
+  static constexpr int RPW = 64 / LPR;          // rows per load instruction
+  static constexpr int NSG = kGranule / RPW;    // slots per granule
+  // granules per chunk: 2 (32 positions, one int8 K group) for dense int8;
+  // fp32 rows and the ring's rope table need the registers of a second one
+  static constexpr int NGC = KIND == kI8Dense ? 2 : 1;
+  static constexpr int CHUNK = kGranule * NGC;
+  static constexpr int NS = NSG * NGC;          // slots per chunk
+  // wide groups split their heads over two halves of the workgroup (each
+  // half streams the same chunks, the second read hitting L1/L2): a wave
+  // then holds q and o of GW <= 4 heads, which keeps them in registers
+  static constexpr int NHG = (G > 4 && (HD == 128 || KIND == kI8Dense)) ? 2 : 1;
+  static constexpr int GW = (G + NHG - 1) / NHG;  // query heads per wave
+  static constexpr int WPG = kWaves / NHG;        // waves per head group
+  static constexpr int GP = GW <= 4 ? 4 : 8;      // padded heads of an LDS weight row
+  static constexpr int DUP = LPR / NSG;         // lanes holding one position's score
   static constexpr int NB = HD / kBlock;
-  static_assert(LPR * EPL == HD, "lane mapping");
-  static_assert(kTile % RPW == 0 && STEPS % U == 0, "tile mapping");
-  static_assert(!kRing || NCH % 2 == 0, "ring pairs d with d + HD/2 in one lane");
-  __device__ static constexpr int dim(int j, int t, int lr) { return (j * LPR + lr) * CH + t; }
+  static_assert(HD == 64 || HD == 128, "head dim");
+  static_assert(KIND != kI8Dense || CHUNK == kKGroup, "int8 chunk must be one K group");
 };
 
-template <int HD, int G, int EPL, int KIND>
-__global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
-  using C = Cfg<HD, G, EPL, KIND>;
-  constexpr int LPR = C::LPR, RPW = C::RPW, U = C::U, CH = C::CH, NCH = C::NCH;
-  constexpr int NB = C::NB;
-  using VT = typename VecLoad<CH>::T;
-
-  __shared__ float s_q[G][HD];
-  __shared__ float s_o[kWaves][G][HD];
-  __shared__ float s_ml[kWaves][G][2];
-  __shared__ float s_f[G][kWaves];
-  __shared__ float s_M[G];
-  __shared__ float s_L[G];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int lr = lane % LPR;
-  const int rw = lane / LPR;
-  const int split = blockIdx.x;
-  const int kh = blockIdx.y;
-  const int qrow = blockIdx.z;
-
-  const int nkeys = C::kRing ? P.ring_nres : P.pos0 + qrow + 1;
-  const int ntiles = (nkeys + kTile - 1) / kTile;
-  const int t_begin = split * P.tiles_per_split;
-  const int t_end = min(t_begin + P.tiles_per_split, ntiles);
-  const size_t head_rows = static_cast<size_t>(kh) * P.cap;  // first row of this kv head
-
-  // ---- raw loads of one step (U positions per lane row); two buffers so the
-  // next step's loads are in flight while the current one is computed
-  struct StepBuf {
-    VT kraw[U][NCH], vraw[U][NCH];      // int8 codes
-    float4 kf4[U][NCH], vf4[U][NCH];    // fp32 rows
-    float vsc[U][NCH];                  // int8 V block scales
-    float ksc[U][NCH];                  // ring int8 K block scales
-    float2 cs[U][(NCH / 2) * CH + 1];   // ring rope cos/sin of each key
-    float ksv[EPL];                     // dense int8 per-channel K scales of the tile
-    int pu[U];
-    bool valid[U];
-  };
-  StepBuf cur, nxt;
-
-  auto rope_pos = [&](int slot) {
-    if (slot < P.ring_s) return slot;
-    int r = slot - P.ring_s - P.ring_base;
-    r += r < 0 ? P.ring_W : 0;
-    return P.ring_s + r;
-  };
-
-  auto issue = [&](int tile, int st, StepBuf& b) {
-    const int tb = tile * kTile;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int p = tb + (st + u) * RPW + rw;
-      b.valid[u] = p < nkeys && (KIND != kI8Dense || p >= P.n_sink);
-      b.pu[u] = min(p, nkeys - 1);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const size_t row = head_rows + b.pu[u];
-#pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        if constexpr (!C::kInt8) {
-          b.kf4[u][j] = *reinterpret_cast<const float4*>(P.kf + row * HD + C::dim(j, 0, lr));
-          b.vf4[u][j] = *reinterpret_cast<const float4*>(P.vf + row * HD + C::dim(j, 0, lr));
-        } else {
-          b.kraw[u][j] = *reinterpret_cast<const VT*>(P.k8 + row * HD + C::dim(j, 0, lr));
-          b.vraw[u][j] = *reinterpret_cast<const VT*>(P.v8 + row * HD + C::dim(j, 0, lr));
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const size_t row = head_rows + b.pu[u];
-#pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        if constexpr (C::kInt8) b.vsc[u][j] = P.vs[row * NB + C::dim(j, 0, lr) / kBlock];
-        if constexpr (KIND == kI8Ring) b.ksc[u][j] = P.ks[row * NB + C::dim(j, 0, lr) / kBlock];
-      }
-      if constexpr (C::kRing) {
-        const float2* cst = P.rope + static_cast<size_t>(rope_pos(b.pu[u])) * (HD / 2);
-#pragma unroll
-        for (int j = 0; j < NCH / 2; ++j)
-#pragma unroll
-          for (int t = 0; t < CH; ++t) b.cs[u][j * CH + t] = cst[C::dim(j, t, lr)];
-      }
-    }
-    if constexpr (KIND == kI8Dense) {
-      if (st == 0) {
-        // per-channel K scales of group `tile` (model.cpp:627-629)
-        const float* ksr = P.ks + (static_cast<size_t>(kh) * P.ng + tile) * HD;
-#pragma unroll
-        for (int j = 0; j < NCH; ++j)
-#pragma unroll
-          for (int t = 0; t < CH; ++t) b.ksv[j * CH + t] = ksr[C::dim(j, t, lr)];
-      }
-    }
-  };
-
-  // first step's loads go out before the query is staged
-  const int first_tile = t_begin + wave;
-  if (first_tile < t_end) issue(first_tile, 0, cur);
-
-  // ---- stage the query group in LDS: rope (ring), scale to the log2 domain
-  {
-    const float* qb = P.q + (static_cast<size_t>(qrow) * P.n_heads + kh * G) * HD;
-    if constexpr (C::kRing) {
-      const int qpos = P.ring_nres - 1;
-      for (int i = threadIdx.x; i < G * (HD / 2); i += kThreads) {
-        const int g = i / (HD / 2), d = i % (HD / 2);
-        const float2 c = P.rope[static_cast<size_t>(qpos) * (HD / 2) + d];
-        const float a = qb[g * HD + d], b = qb[g * HD + d + HD / 2];
-        s_q[g][d] = (a * c.x - b * c.y) * P.qscale;
-        s_q[g][d + HD / 2] = (b * c.x + a * c.y) * P.qscale;
-      }
-    } else {
-      for (int i = threadIdx.x; i < G * HD; i += kThreads) s_q[i / HD][i % HD] = qb[i] * P.qscale;
-    }
+// Reduces the NSG per-slot partial dots of a lane row to full scores, one
+// position per lane (lane c of the row ends with granule slot kslot_xor(c)).
+template <int HD>
+__device__ __forceinline__ float treduce(const float* a) {
+  float t;
+  if constexpr (HD == 128) {
+    const float s0 = a[0] + dpp<kX8>(a[2]);
+    const float s1 = a[1] + dpp<kX8>(a[3]);
+    t = s0 + dpp<kX7>(s1);
+  } else {
+    t = a[0] + dpp<kX7>(a[1]);
   }
-  __syncthreads();
+  t += dpp<kX2>(t);
+  t += dpp<kX1>(t);
+  return t;
+}
 
-  // q of this lane's elements (dense int8 reads it per tile from LDS instead)
-  float qv[KIND == kI8Dense ? 1 : G][EPL];
-  if constexpr (KIND != kI8Dense) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int j = 0; j < NCH; ++j)
-#pragma unroll
-        for (int t = 0; t < CH; ++t) qv[g][j * CH + t] = s_q[g][C::dim(j, t, lr)];
-  }
-
-  // online-softmax state: m is shared by the whole wave (every lane holds the
-  // wave maximum), l and o are per lane row and summed over rows at the end.
-  // int8 V is unpacked with a +128 bias; corr accumulates the weight each
-  // chunk received, and 128 * corr is taken off o once at the end.
-  constexpr bool kBias = C::kInt8;
-  float m[G], l[G], o[G][EPL];
-  float corr[kBias ? G : 1][kBias ? NCH : 1];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = kMinit;
-    l[g] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) o[g][e] = 0.0f;
-    if constexpr (kBias)
-#pragma unroll
-      for (int j = 0; j < NCH; ++j) corr[g][j] = 0.0f;
-  }
-
-  // one step: scores s[g][u] of U positions per lane row; vrow(u, vx, mul)
-  // yields position u's V elements and per-chunk weight multiplier
-  auto update = [&](float (&s)[G][U], auto&& vrow, auto biased_tag) {
-    constexpr bool kB = decltype(biased_tag)::value;
-    float p[G][U];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mx = s[g][0];
-#pragma unroll
-      for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[g][u]);
-      mx = rows_max<LPR>(mx);
-      const float mn = fmaxf(m[g], mx);
-      const float alpha = fast_exp2(m[g] - mn);
-      m[g] = mn;
-      float psum = 0.0f;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        p[g][u] = fast_exp2(s[g][u] - mn);
-        psum += p[g][u];
-      }
-      l[g] = l[g] * alpha + psum;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) o[g][e] *= alpha;
-      if constexpr (kBias)
-#pragma unroll
-        for (int j = 0; j < NCH; ++j) corr[g][j] *= alpha;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float vx[EPL];
-      float mul[NCH];
-      vrow(u, vx, mul);
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int j = 0; j < NCH; ++j) {
-          const float pw = p[g][u] * mul[j];
-          if constexpr (kB) corr[g][j] += pw;
-#pragma unroll
-          for (int t = 0; t < CH; ++t) o[g][j * CH + t] += pw * vx[j * CH + t];
-        }
-    }
-  };
-  using Unbiased = std::integral_constant<bool, false>;
-  using Biased = std::integral_constant<bool, kBias>;
-
-  // ---- fp32 sinks of the dense int8 cache (model.cpp:623-626, 640-644)
-  if constexpr (KIND == kI8Dense) {
-    if (split == 0 && wave == kWaves - 1) {
-      const int ns = min(P.n_sink, nkeys);
-      for (int p0 = 0; p0 < ns; p0 += RPW) {
-        const int p = p0 + rw;
-        const bool ok = p < ns;
-        const int pl = ok ? p : 0;
-        const float* kr = P.ksink + (static_cast<size_t>(kh) * P.n_sink + pl) * HD;
-        const float* vr = P.vsink + (static_cast<size_t>(kh) * P.n_sink + pl) * HD;
-        float kx[EPL], vx[EPL];
-#pragma unroll
-        for (int j = 0; j < NCH; ++j)
-#pragma unroll
-          for (int t = 0; t < CH; ++t) {
-            kx[j * CH + t] = kr[C::dim(j, t, lr)];
-            vx[j * CH + t] = vr[C::dim(j, t, lr)];
-          }
-        float s[G][U];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float acc = 0.0f;
-#pragma unroll
-          for (int j = 0; j < NCH; ++j)
-#pragma unroll
-            for (int t = 0; t < CH; ++t) acc += s_q[g][C::dim(j, t, lr)] * kx[j * CH + t];
-          acc = row_sum<LPR>(acc);
-          s[g][0] = ok ? acc : -INFINITY;
-#pragma unroll
-          for (int u = 1; u < U; ++u) s[g][u] = -INFINITY;
-        }
-        update(
-            s,
-            [&](int u, float* x, float* mul) {
-#pragma unroll
-              for (int e = 0; e < EPL; ++e) x[e] = u == 0 ? vx[e] : 0.0f;
-#pragma unroll
-              for (int j = 0; j < NCH; ++j) mul[j] = 1.0f;
-            },
-            Unbiased{});
-      }
-    }
-  }
-
-  // ---- main stream over this wave's tiles of the split
-  float qs[KIND == kI8Dense ? G : 1][KIND == kI8Dense ? EPL : 1];
-  float qsum[KIND == kI8Dense ? G : 1];
-  int tile = first_tile, st = 0;
-  while (tile < t_end) {
-    // prefetch the next step of this wave
-    int ntile = tile, nst = st + U;
-    if (nst == C::STEPS) {
-      nst = 0;
-      ntile += kWaves;
-    }
-    if (ntile < t_end) issue(ntile, nst, nxt);
-    if constexpr (KIND == kI8Dense) {
-      if (st == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          qsum[g] = 0.0f;
-#pragma unroll
-          for (int j = 0; j < NCH; ++j)
-#pragma unroll
-            for (int t = 0; t < CH; ++t) {
-              qs[g][j * CH + t] = s_q[g][C::dim(j, t, lr)] * cur.ksv[j * CH + t];
-              qsum[g] += qs[g][j * CH + t];
-            }
-          qsum[g] *= 128.0f;
-        }
-      }
-    }
-    float s[G][U];
-    if constexpr (!C::kInt8) {
-      float kx[U][EPL];
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int j = 0; j < NCH; ++j) {
-          kx[u][j * 4 + 0] = cur.kf4[u][j].x;
-          kx[u][j * 4 + 1] = cur.kf4[u][j].y;
-          kx[u][j * 4 + 2] = cur.kf4[u][j].z;
-          kx[u][j * 4 + 3] = cur.kf4[u][j].w;
-        }
-      if constexpr (C::kRing) {
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-          for (int j = 0; j < NCH / 2; ++j)
-#pragma unroll
-            for (int t = 0; t < CH; ++t) {
-              const float2 c = cur.cs[u][j * CH + t];
-              const float a = kx[u][j * CH + t];
-              const float b = kx[u][(j + NCH / 2) * CH + t];
-              kx[u][j * CH + t] = a * c.x - b * c.y;
-              kx[u][(j + NCH / 2) * CH + t] = b * c.x + a * c.y;
-            }
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          float acc = 0.0f;
-#pragma unroll
-          for (int e = 0; e < EPL; ++e) acc += qv[g][e] * kx[u][e];
-          acc = row_sum<LPR>(acc);
-          s[g][u] = cur.valid[u] ? acc : -INFINITY;
-        }
-      update(
-          s,
-          [&](int u, float* x, float* mul) {
-#pragma unroll
-            for (int j = 0; j < NCH; ++j) {
-              x[j * 4 + 0] = cur.vf4[u][j].x;
-              x[j * 4 + 1] = cur.vf4[u][j].y;
-              x[j * 4 + 2] = cur.vf4[u][j].z;
-              x[j * 4 + 3] = cur.vf4[u][j].w;
-              mul[j] = 1.0f;
-            }
-          },
-          Unbiased{});
-    } else {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float kx[EPL];
-#pragma unroll
-        for (int j = 0; j < NCH; ++j) unpack_biased<CH>(cur.kraw[u][j], kx + j * CH);
-        if constexpr (KIND == kI8Ring) {
-          // dequantize (ks * code, model.cpp:689-690), then rope
-#pragma unroll
-          for (int j = 0; j < NCH; ++j)
-#pragma unroll
-            for (int t = 0; t < CH; ++t) kx[j * CH + t] = cur.ksc[u][j] * (kx[j * CH + t] - 128.0f);
-#pragma unroll
-          for (int j = 0; j < NCH / 2; ++j)
-#pragma unroll
-            for (int t = 0; t < CH; ++t) {
-              const float2 c = cur.cs[u][j * CH + t];
-              const float a = kx[j * CH + t];
-              const float b = kx[(j + NCH / 2) * CH + t];
-              kx[j * CH + t] = a * c.x - b * c.y;
-              kx[(j + NCH / 2) * CH + t] = b * c.x + a * c.y;
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float acc;
-          if constexpr (KIND == kI8Dense) {
-            acc = -qsum[g];
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) acc += qs[g][e] * kx[e];
-          } else {
-            acc = 0.0f;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) acc += qv[g][e] * kx[e];
-          }
-          acc = row_sum<LPR>(acc);
-          s[g][u] = cur.valid[u] ? acc : -INFINITY;
-        }
-      }
-      update(
-          s,
-          [&](int u, float* x, float* mul) {
-#pragma unroll
-            for (int j = 0; j < NCH; ++j) {
-              unpack_biased<CH>(cur.vraw[u][j], x + j * CH);
-              mul[j] = cur.vsc[u][j];
-            }
-          },
-          Biased{});
-    }
-    cur = nxt;
-    tile = ntile;
-    st = nst;
-  }
-
-  // ---- sum the lane rows of this wave (m is already the wave maximum)
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    l[g] = rows_sum<LPR>(l[g]);
-#pragma unroll
-    for (int j = 0; j < NCH; ++j)
-#pragma unroll
-      for (int t = 0; t < CH; ++t) {
-        float x = o[g][j * CH + t];
-        if constexpr (kBias) x -= 128.0f * corr[g][j];
-        o[g][j * CH + t] = rows_sum<LPR>(x);
-      }
-  }
-
-  // ---- merge the waves through LDS
-  if (rw == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int j = 0; j < NCH; ++j)
-#pragma unroll
-        for (int t = 0; t < CH; ++t) s_o[wave][g][C::dim(j, t, lr)] = o[g][j * CH + t];
-    if (lr == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        s_ml[wave][g][0] = m[g];
-        s_ml[wave][g][1] = l[g];
-      }
-    }
-  }
+// Cross-wave combine of (m, l, o) in LDS, then either the final output
+// (single split) or this split's partial record. Head g was handled by the
+// WPG waves of head group g / GW, at their local head index g % GW.
+template <int HD, int G, int GW, int WPG>
+__device__ __forceinline__ void finish(const AttnParams& P, float (&s_o)[kWaves][GW][HD],
+                                       float (&s_ml)[kWaves][GW][2], float (&s_f)[G][WPG],
+                                       float (&s_M)[G], float (&s_L)[G], int split, int kh,
+                                       int qrow) {
   __syncthreads();
   if (static_cast<int>(threadIdx.x) < G) {
-    const int g = threadIdx.x;
+    const int g = threadIdx.x, w0 = (g / GW) * WPG, gl = g % GW;
     float M = kMinit;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[w][g][0]);
+    for (int i = 0; i < WPG; ++i) M = fmaxf(M, s_ml[w0 + i][gl][0]);
     float L = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float f = fast_exp2(s_ml[w][g][0] - M);
-      s_f[g][w] = f;
-      L += s_ml[w][g][1] * f;
+    for (int i = 0; i < WPG; ++i) {
+      const float f = fast_exp2(s_ml[w0 + i][gl][0] - M);
+      s_f[g][i] = f;
+      L += s_ml[w0 + i][gl][1] * f;
     }
     s_M[g] = M;
     s_L[g] = L;
   }
   __syncthreads();
 
+  auto o_of = [&](int g, int d) {
+    const int w0 = (g / GW) * WPG, gl = g % GW;
+    float O = 0.0f;
+#pragma unroll
+    for (int i = 0; i < WPG; ++i) O += s_o[w0 + i][gl][d] * s_f[g][i];
+    return O;
+  };
   const int rec_floats = G * (HD + 2);
   const size_t head_base = static_cast<size_t>(qrow) * P.nkv + kh;
-  float* out_base = P.out + (static_cast<size_t>(qrow) * P.n_heads + kh * G) * HD;
-
-  if (P.nsplit == 1) {
+  if (P.direct) {
+    float* out_base = P.out + (static_cast<size_t>(qrow) * P.n_heads + kh * G) * HD;
     for (int idx = threadIdx.x; idx < G * HD; idx += kThreads) {
       const int g = idx / HD, d = idx % HD;
-      float O = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) O += s_o[w][g][d] * s_f[g][w];
-      out_base[idx] = O / s_L[g];
+      out_base[idx] = o_of(g, d) / s_L[g];
     }
     return;
   }
-
-  // ---- publish this split's (o[G][HD], m[G], l[G]); merge_kernel, the next
-  // launch on the stream, combines the splits (a kernel boundary is the
-  // cheapest release/acquire across this part's per-XCD L2 caches)
   float* rec = P.part + (head_base * P.nsplit + split) * rec_floats;
   for (int idx = threadIdx.x; idx < G * HD + 2 * G; idx += kThreads) {
     float v;
     if (idx < G * HD) {
-      const int g = idx / HD, d = idx % HD;
-      v = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) v += s_o[w][g][d] * s_f[g][w];
+      v = o_of(idx / HD, idx % HD);
     } else {
       const int r = idx - G * HD;
       v = r < G ? s_M[r] : s_L[r - G];
@@ -686,41 +266,485 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
   }
 }
 
-// Combines the split partials of one (row, query head): one thread per
-// output dim; every split's (m, l, o[d]) is loaded in a single round.
+template <int HD, int G, int KIND>
+__global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
+  using C = Cfg<HD, G, KIND>;
+  constexpr int LPR = C::LPR, RPW = C::RPW, NSG = C::NSG, NGC = C::NGC, NS = C::NS;
+  constexpr int CHUNK = C::CHUNK, GP = C::GP, NB = C::NB;
+  constexpr int GW = C::GW, WPG = C::WPG;
+  constexpr bool kInt8 = C::kInt8, kRing = C::kRing;
+
+  __shared__ float s_o[kWaves][GW][HD];
+  __shared__ float s_ml[kWaves][GW][2];
+  __shared__ float s_f[G][WPG];
+  __shared__ float s_M[G];
+  __shared__ float s_L[G];
+  __shared__ __align__(16) float s_w[kWaves][CHUNK][GP];
+
+  const int lane = threadIdx.x & 63;
+  // wave index as a provably uniform value: buffer-load SGPR offsets derive
+  // from it (a divergent one would turn every load into a waterfall loop)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g0 = (wave / WPG) * GW;  // first query head of this wave's head group
+  const int wl = wave % WPG;         // wave index inside the head group
+  const int c = lane % LPR;
+  const int r = lane / LPR;
+  const int split = blockIdx.x;
+  const int kh = blockIdx.y;
+  const int qrow = blockIdx.z;
+  const int nkeys = kRing ? P.ring_nres : P.pos0 + qrow + 1;
+
+  const int nchunks = (nkeys + CHUNK - 1) / CHUNK;
+  const int c_end = min((split + 1) * P.chunks_per_split, nchunks);
+  const size_t head = static_cast<size_t>(kh) * P.capg;  // first row of this kv head
+  const size_t head_el = head * HD;
+  const int kx_slot = kslot_xor(HD, c);  // granule slot of this lane's scores
+
+  // ---- per-chunk register buffers
+  uint2 kq[kInt8 ? NS : 1], vq[kInt8 ? NS : 1];
+  float4 kf[kInt8 ? 1 : NS][2], vf[kInt8 ? 1 : NS][2];
+  float4 ksv[KIND == kI8Dense ? 2 : 1];    // dense int8 channel scales of the group
+  float ksc[KIND == kI8Ring ? NS : 1][2];  // ring int8 K block scales
+  float vsc[kInt8 ? NS : 1];               // int8 V block scales
+  float4 cs[kRing ? NS : 1][2];            // ring rope cos/sin of the lane's 4 pairs
+
+  auto rope_pos = [&](int slot) {
+    if (slot < P.ring_s) return slot;
+    int t = slot - P.ring_s - P.ring_base;
+    t += t < 0 ? P.ring_W : 0;
+    return P.ring_s + t;
+  };
+
+  // Buffer resources of this kv head's arrays: every load is a raw buffer
+  // load with a wave-uniform SGPR offset (chunk and slot) and one per-lane
+  // VGPR offset, so no 64-bit address registers are held per load.
+  constexpr int ES = kInt8 ? 1 : 4;  // bytes per K/V element
+  const int kv_bytes = P.capg * HD * ES;
+  const rsrc_t rk = make_rsrc(kInt8 ? static_cast<const void*>(P.k8 + head_el)
+                                    : static_cast<const void*>(P.kf + head_el), kv_bytes);
+  const rsrc_t rv = make_rsrc(kInt8 ? static_cast<const void*>(P.v8 + head_el)
+                                    : static_cast<const void*>(P.vf + head_el), kv_bytes);
+  // (arrays a layout lacks get an empty resource: every read returns 0)
+  const rsrc_t rks =
+      KIND == kI8Dense ? make_rsrc(P.ks + static_cast<size_t>(kh) * P.ng * HD, P.ng * HD * 4)
+      : KIND == kI8Ring ? make_rsrc(P.ks + head * NB, P.capg * NB * 4)
+                        : make_rsrc(P.q, 0);
+  const rsrc_t rvs = kInt8 ? make_rsrc(P.vs + head * NB, P.capg * NB * 4) : make_rsrc(P.q, 0);
+  const rsrc_t rcs = kRing ? make_rsrc(P.rope, P.rope_rows * (HD / 2) * 8) : make_rsrc(P.q, 0);
+  const int lane_k = lane * 8 * ES;  // this lane's 8 elements inside a slot
+
+  auto issue_k = [&](int ch) {
+    const int p0 = ch * CHUNK;
+#pragma unroll
+    for (int gs = 0; gs < NGC; ++gs)
+#pragma unroll
+      for (int j = 0; j < NSG; ++j) {
+        const int sl = gs * NSG + j;
+        const int so = (p0 + gs * kGranule) * HD * ES + j * 512 * ES;
+        if constexpr (kInt8) {
+          kq[sl] = load_b64(rk, lane_k, so);
+        } else {
+          kf[sl][0] = load_b128(rk, lane * 16, so);
+          kf[sl][1] = load_b128(rk, lane * 16, so + 1024);
+        }
+        if constexpr (kRing) {
+          const int p = min(p0 + gs * kGranule + (j ^ kx_slot) * RPW + r, nkeys - 1);
+          const int co = rope_pos(p) * (HD / 2) * 8 + 32 * c;
+          cs[sl][0] = load_b128(rcs, co, 0);
+          cs[sl][1] = load_b128(rcs, co + 16, 0);
+          if constexpr (KIND == kI8Ring) {
+            ksc[sl][0] = load_b32(rks, (p * NB + (4 * c) / kBlock) * 4, 0);
+            ksc[sl][1] = load_b32(rks, (p * NB + (HD / 2 + 4 * c) / kBlock) * 4, 0);
+          }
+        }
+      }
+    if constexpr (KIND == kI8Dense) {
+      const int so = (p0 / kKGroup) * HD * 4;
+      ksv[0] = load_b128(rks, 16 * c, so);
+      ksv[1] = load_b128(rks, 16 * c + HD * 2, so);
+    }
+  };
+
+  auto issue_v = [&](int ch) {
+    const int p0 = ch * CHUNK;
+#pragma unroll
+    for (int gs = 0; gs < NGC; ++gs)
+#pragma unroll
+      for (int i = 0; i < NSG; ++i) {
+        const int sl = gs * NSG + i;
+        const int pb = p0 + gs * kGranule + i * RPW;  // position of row 0
+        const int so = (p0 + gs * kGranule) * HD * ES + i * 512 * ES;
+        if constexpr (kInt8) {
+          vq[sl] = load_b64(rv, lane_k, so);
+          vsc[sl] = load_b32(rvs, (r * NB + (8 * c) / kBlock) * 4, pb * NB * 4);
+        } else {
+          vf[sl][0] = load_b128(rv, lane * 16, so);
+          vf[sl][1] = load_b128(rv, lane * 16, so + 1024);
+        }
+      }
+  };
+
+  int ch = split * P.chunks_per_split + wl;
+  if (ch < c_end) {
+    issue_k(ch);
+    issue_v(ch);
+  }
+
+  // ---- q of this lane's K dims (4c..4c+3, hd/2+4c..), in the log2 domain;
+  // the ring ropes it at n_res - 1 (model.cpp:669-671)
+  float qv[GW][8];
+  {
+    const float* qb = P.q + (static_cast<size_t>(qrow) * P.n_heads + kh * G) * HD;
+    float4 cq[2];
+    if constexpr (kRing) {
+      const float4* t = reinterpret_cast<const float4*>(
+          P.rope + static_cast<size_t>(P.ring_nres - 1) * (HD / 2) + 4 * c);
+      cq[0] = t[0];
+      cq[1] = t[1];
+    }
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      // a head group's padding head (odd G) gets q = 0 and is never stored
+      const bool hv = g0 + g < G;
+      const float* qg = qb + (hv ? g0 + g : 0) * HD;
+      float4 a = *reinterpret_cast<const float4*>(qg + 4 * c);
+      float4 b = *reinterpret_cast<const float4*>(qg + HD / 2 + 4 * c);
+      if (!hv) a = b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      if constexpr (kRing) {
+        const float cv[4] = {cq[0].x, cq[0].z, cq[1].x, cq[1].z};
+        const float sv[4] = {cq[0].y, cq[0].w, cq[1].y, cq[1].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float u = x[t], w = x[4 + t];
+          x[t] = u * cv[t] - w * sv[t];
+          x[4 + t] = w * cv[t] + u * sv[t];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[g][e] = x[e] * P.qscale;
+    }
+  }
+
+  float M[GW], l[GW], o[GW][8], corr[kInt8 ? GW : 1];
+#pragma unroll
+  for (int g = 0; g < GW; ++g) {
+    M[g] = kMinit;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+    if constexpr (kInt8) corr[g] = 0.0f;
+  }
+
+  while (ch < c_end) {
+    const int nch = ch + WPG;
+    const int p0 = ch * CHUNK;
+
+    // ---- q for this chunk: dense int8 folds the group's channel scales in
+    float qt[GW][8], qb[GW];
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      if constexpr (KIND == kI8Dense) {
+        const float ks8[8] = {ksv[0].x, ksv[0].y, ksv[0].z, ksv[0].w,
+                              ksv[1].x, ksv[1].y, ksv[1].z, ksv[1].w};
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          qt[g][e] = qv[g][e] * ks8[e];
+          sum += qt[g][e];
+        }
+        qb[g] = -128.0f * sum;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qt[g][e] = qv[g][e];
+        qb[g] = 0.0f;
+      }
+    }
+
+    // ---- QK: per granule, NSG slot partials -> one score per lane
+    float sc[NGC][GW];
+#pragma unroll
+    for (int gs = 0; gs < NGC; ++gs) {
+      float acc[GW][NSG];
+#pragma unroll
+      for (int j = 0; j < NSG; ++j) {
+        const int sl = gs * NSG + j;
+        float kx[8];
+        if constexpr (kInt8) {
+          cvt8(kq[sl], kx);
+          if constexpr (KIND == kI8Ring) {
+            // dequantize (code * block scale, model.cpp:689-690)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kx[e] = ksc[sl][e >> 2] * (kx[e] - 128.0f);
+          }
+        } else {
+          kx[0] = kf[sl][0].x; kx[1] = kf[sl][0].y; kx[2] = kf[sl][0].z; kx[3] = kf[sl][0].w;
+          kx[4] = kf[sl][1].x; kx[5] = kf[sl][1].y; kx[6] = kf[sl][1].z; kx[7] = kf[sl][1].w;
+        }
+        if constexpr (kRing) {
+          const float cv[4] = {cs[sl][0].x, cs[sl][0].z, cs[sl][1].x, cs[sl][1].z};
+          const float sv[4] = {cs[sl][0].y, cs[sl][0].w, cs[sl][1].y, cs[sl][1].w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float a = kx[t], b = kx[4 + t];
+            kx[t] = a * cv[t] - b * sv[t];
+            kx[4 + t] = b * cv[t] + a * sv[t];
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < GW; ++g) {
+          float a = qb[g];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a += qt[g][e] * kx[e];
+          acc[g][j] = a;
+        }
+      }
+      const int p = p0 + gs * kGranule + kx_slot * RPW + r;
+      const bool valid = p < nkeys && (KIND != kI8Dense || p >= P.n_sink);
+#pragma unroll
+      for (int g = 0; g < GW; ++g) {
+        const float s = treduce<HD>(acc[g]);
+        sc[gs][g] = valid ? s : -INFINITY;
+      }
+    }
+    // the scheduler must not hoist the next chunk's loads above the use of
+    // this chunk's registers (that doubles the live buffers)
+    __builtin_amdgcn_sched_barrier(0);
+    if (nch < c_end) issue_k(nch);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- online softmax with a wave-uniform running max
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      float mx = sc[0][g];
+#pragma unroll
+      for (int gs = 1; gs < NGC; ++gs) mx = fmaxf(mx, sc[gs][g]);
+      const float mn = fmaxf(M[g], wave_max(mx));
+      const float alpha = fast_exp2(M[g] - mn);
+      M[g] = mn;
+      float ls = l[g] * alpha;
+#pragma unroll
+      for (int gs = 0; gs < NGC; ++gs) {
+        const float w = fast_exp2(sc[gs][g] - mn);
+        sc[gs][g] = w;
+        ls += w;
+      }
+      l[g] = ls;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
+      if constexpr (kInt8) corr[g] *= alpha;
+    }
+
+    // ---- weights to the PV mapping through this wave's LDS rows
+    if ((c & 3) == 0) {
+#pragma unroll
+      for (int gs = 0; gs < NGC; ++gs) {
+        float* wr = &s_w[wave][gs * kGranule + kx_slot * RPW + r][0];
+#pragma unroll
+        for (int gq = 0; gq < GP; gq += 4) {
+          float4 w4;
+          w4.x = gq + 0 < GW ? sc[gs][gq + 0 < GW ? gq + 0 : 0] : 0.0f;
+          w4.y = gq + 1 < GW ? sc[gs][gq + 1 < GW ? gq + 1 : 0] : 0.0f;
+          w4.z = gq + 2 < GW ? sc[gs][gq + 2 < GW ? gq + 2 : 0] : 0.0f;
+          w4.w = gq + 3 < GW ? sc[gs][gq + 3 < GW ? gq + 3 : 0] : 0.0f;
+          *reinterpret_cast<float4*>(wr + gq) = w4;
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- PV: lane (row r, dims 8c..8c+7), slot i -> position i*RPW + r.
+    // Rows past the last key have weight 0; in the final partial chunk their
+    // (stale) V and scales are zeroed as well, so nothing non-finite enters.
+    const bool full = p0 + CHUNK <= nkeys;  // uniform
+#pragma unroll
+    for (int gs = 0; gs < NGC; ++gs)
+#pragma unroll
+      for (int i = 0; i < NSG; ++i) {
+        const int sl = gs * NSG + i;
+        const float* wr = &s_w[wave][gs * kGranule + i * RPW + r][0];
+        float wv[GP];
+#pragma unroll
+        for (int gq = 0; gq < GP; gq += 4) {
+          const float4 w4 = *reinterpret_cast<const float4*>(wr + gq);
+          wv[gq] = w4.x;
+          wv[gq + 1] = w4.y;
+          wv[gq + 2] = w4.z;
+          wv[gq + 3] = w4.w;
+        }
+        float vx[8];
+        float vsl = 0.0f;
+        if constexpr (kInt8) {
+          cvt8(vq[sl], vx);
+          vsl = vsc[sl];
+        } else {
+          vx[0] = vf[sl][0].x; vx[1] = vf[sl][0].y; vx[2] = vf[sl][0].z; vx[3] = vf[sl][0].w;
+          vx[4] = vf[sl][1].x; vx[5] = vf[sl][1].y; vx[6] = vf[sl][1].z; vx[7] = vf[sl][1].w;
+        }
+        if (!full) {
+          const bool ok = p0 + gs * kGranule + i * RPW + r < nkeys;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vx[e] = ok ? vx[e] : 0.0f;
+          vsl = ok ? vsl : 0.0f;
+        }
+        if constexpr (kInt8) {
+#pragma unroll
+          for (int g = 0; g < GW; ++g) {
+            wv[g] *= vsl;
+            corr[g] += wv[g];
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < GW; ++g)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[g][e] += wv[g] * vx[e];
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    if (nch < c_end) issue_v(nch);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_wave_barrier();
+    ch = nch;
+  }
+
+  // ---- wave epilogue: l over lanes, o over the RPW lane rows (transposing
+  // permlane swaps: lane ends with values K = k + 2GW * (lane / 16), k < 2GW)
+#pragma unroll
+  for (int g = 0; g < GW; ++g) {
+    l[g] = wave_sum(l[g]) * (1.0f / C::DUP);
+    if constexpr (kInt8)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] -= 128.0f * corr[g];
+  }
+  float v1[4 * GW], v2[2 * GW];
+#pragma unroll
+  for (int k = 0; k < 4 * GW; ++k)
+    v1[k] = swap32_sum(o[k / 8][k % 8], o[(k + 4 * GW) / 8][(k + 4 * GW) % 8]);
+#pragma unroll
+  for (int k = 0; k < 2 * GW; ++k) v2[k] = swap16_sum(v1[k], v1[k + 2 * GW]);
+  if constexpr (HD == 64) {
+#pragma unroll
+    for (int k = 0; k < 2 * GW; ++k) v2[k] += dpp<kX8>(v2[k]);
+  }
+  if (HD == 128 || (lane & 8) == 0) {
+    const int q4 = lane >> 4;
+#pragma unroll
+    for (int k = 0; k < 2 * GW; ++k) {
+      const int K = k + 2 * GW * q4;
+      s_o[wave][K / 8][8 * c + K % 8] = v2[k];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      s_ml[wave][g][0] = M[g];
+      s_ml[wave][g][1] = l[g];
+    }
+  }
+  finish<HD, G, GW, WPG>(P, s_o, s_ml, s_f, s_M, s_L, split, kh, qrow);
+}
+
+// fp32 sinks of the dense int8 cache (model.cpp:623-626, 640-644), folded
+// into the merge as one more split.
+struct SinkArgs {
+  const float* q;      // [rows][n_heads][hd]
+  const float* ksink;  // this layer's [nkv][n_sink][hd]
+  const float* vsink;
+  int n_sink;          // 0: no sinks
+  int pos0;            // row r attends keys [0, pos0 + r]
+  float qscale;
+};
+
+constexpr int kSinkBatch = 8;
+
+// Combines the split partials of one (row, query head), one thread per
+// output dim. All loads go out in one round: every thread's o[d] of each
+// split (indices clamped, surplus splits weighted 0), wave 0's lanes the
+// (m, l) of one split each, and the first sink rows. Wave 0 turns the
+// (m, l) into split weights (DPP max / sum); the sink positions, when the
+// layout has them, are attended here in batches as further entries.
 template <int HD>
 __global__ __launch_bounds__(HD) void merge_kernel(const float* __restrict__ part,
                                                    float* __restrict__ out, int nkv, int G,
-                                                   int nsplit, int n_heads) {
+                                                   int nsplit, int n_heads, SinkArgs sa) {
+  constexpr int NW = HD / 64;
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_dot[kSinkBatch][NW];
+  __shared__ float s_M, s_L;
   const int h = blockIdx.x;
   const int row = blockIdx.y;
   const int kh = h / G, g = h % G;
   const int d = threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rec_floats = G * (HD + 2);
   const float* recs = part + ((static_cast<size_t>(row) * nkv + kh) * nsplit) * rec_floats;
-  float mv[kMaxSplits], lv[kMaxSplits], ov[kMaxSplits];
+  float ov[kMaxSplits];
 #pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp) {
-    if (sp < nsplit) {
-      const float* r = recs + static_cast<size_t>(sp) * rec_floats;
-      mv[sp] = r[G * HD + g];
-      lv[sp] = r[G * HD + G + g];
-      ov[sp] = r[g * HD + d];
-    } else {
-      mv[sp] = kMinit;
-      lv[sp] = 0.0f;
-      ov[sp] = 0.0f;
+  for (int sp = 0; sp < kMaxSplits; ++sp)
+    ov[sp] = recs[static_cast<size_t>(min(sp, nsplit - 1)) * rec_floats + g * HD + d];
+  const int ns = min(sa.n_sink, sa.pos0 + row + 1);
+  const float qd =
+      ns > 0 ? sa.q[(static_cast<size_t>(row) * n_heads + h) * HD + d] * sa.qscale : 0.0f;
+  float kd[kSinkBatch], vd[kSinkBatch];
+  auto load_sinks = [&](int p0) {
+#pragma unroll
+    for (int b = 0; b < kSinkBatch; ++b) {
+      const size_t at = (static_cast<size_t>(kh) * sa.n_sink + min(p0 + b, ns - 1)) * HD + d;
+      kd[b] = sa.ksink[at];
+      vd[b] = sa.vsink[at];
+    }
+  };
+  if (ns > 0) load_sinks(0);
+
+  if (wave == 0) {
+    const bool on = lane < nsplit;
+    const float* r = recs + static_cast<size_t>(min(lane, nsplit - 1)) * rec_floats;
+    const float m = on ? r[G * HD + g] : kMinit;
+    const float l = on ? r[G * HD + G + g] : 0.0f;
+    const float M = wave_max(m);
+    const float w = on ? fast_exp2(m - M) : 0.0f;
+    const float L = wave_sum(l * w);
+    if (lane < kMaxSplits) s_w[lane] = w;
+    if (lane == 0) {
+      s_M = M;
+      s_L = L;
     }
   }
-  float M = kMinit;
+  __syncthreads();
+  float M = s_M, L = s_L, O = 0.0f;
 #pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp) M = fmaxf(M, mv[sp]);
-  float L = 0.0f, O = 0.0f;
+  for (int sp = 0; sp < kMaxSplits; ++sp) O += s_w[sp] * ov[sp];
+
+  for (int p0 = 0; p0 < ns; p0 += kSinkBatch) {
+    if (p0 > 0) load_sinks(p0);
 #pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp) {
-    const float w = fast_exp2(mv[sp] - M);
-    L += lv[sp] * w;
-    O += ov[sp] * w;
+    for (int b = 0; b < kSinkBatch; ++b) {
+      const float t = wave_sum(qd * kd[b]);
+      if (lane == 0) s_dot[b][wave] = t;
+    }
+    __syncthreads();
+    float sc[kSinkBatch];
+    float bm = M;
+#pragma unroll
+    for (int b = 0; b < kSinkBatch; ++b) {
+      float t = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) t += s_dot[b][w];
+      sc[b] = p0 + b < ns ? t : -INFINITY;
+      bm = fmaxf(bm, sc[b]);
+    }
+    const float scale = fast_exp2(M - bm);
+    M = bm;
+    L *= scale;
+    O *= scale;
+#pragma unroll
+    for (int b = 0; b < kSinkBatch; ++b) {
+      const float w = fast_exp2(sc[b] - M);
+      L += w;
+      O += w * vd[b];
+    }
+    __syncthreads();
   }
   out[(static_cast<size_t>(row) * n_heads + h) * HD + d] = O / L;
 }
@@ -728,21 +752,9 @@ __global__ __launch_bounds__(HD) void merge_kernel(const float* __restrict__ par
 // ---------------------------------------------------------------------------
 // dispatch
 
-// Elements per lane: 16 keeps the lane-row count (and the end-of-wave row
-// merge) small; 8 halves the q / o registers where G is large or int8 wants
-// more positions in flight.
-template <int HD, int G, int KIND>
-constexpr int epl_for() {
-#ifdef DBI_EPL_RULE
-  return DBI_EPL_RULE;
-#else
-  return (KIND == kI8Dense || KIND == kI8Ring) ? 8 : (G <= 2 ? 16 : 8);
-#endif
-}
-
 template <int HD, int G, int KIND>
 void* kernel_for() {
-  return reinterpret_cast<void*>(&attn_kernel<HD, G, epl_for<HD, G, KIND>(), KIND>);
+  return reinterpret_cast<void*>(&attn_kernel<HD, G, KIND>);
 }
 
 template <int HD, int KIND>
@@ -779,6 +791,9 @@ void* pick_kernel(int hd, int kind, int G) {
 
 int kind_of(const KvGeom& g) { return (g.ring ? 2 : 0) + (g.int8 ? 1 : 0); }
 
+// positions per chunk of the kernel instance (Cfg::CHUNK)
+int chunk_of(const KvGeom& g) { return g.int8 && !g.ring ? 2 * kGranule : kGranule; }
+
 // Workgroups one launch aims for (split-K fan-out: one 8-wave workgroup per
 // CU); DBI_ATTN_TARGET_BLOCKS overrides it for tuning sweeps.
 int target_blocks() {
@@ -790,63 +805,77 @@ int target_blocks() {
   return v;
 }
 
-void plan(const KvGeom& g, const AttnCall& c, int* nsplit, int* tiles_per_split) {
+struct Plan {
+  int nsplit, chunks_per_split;
+  bool merge;  // a merge launch follows (several splits, or fp32 sinks)
+};
+
+Plan plan(const KvGeom& g, const AttnCall& c) {
+  const int G = c.n_heads / g.nkv;
+  const int chunk = chunk_of(g);
   const int nkeys_max = g.ring ? c.ring.n_res : c.pos0 + c.rows;
-  const int ntiles = (nkeys_max + kTile - 1) / kTile;
+  const int nchunks = (nkeys_max + chunk - 1) / chunk;
+  const bool sinks = g.int8 && !g.ring && g.n_sink > 0;
   const int units = g.nkv * c.rows;
-  int want = (target_blocks() + units - 1) / units;
-  const int max_by_tiles = (ntiles + kWaves - 1) / kWaves;  // >= one tile per wave
-  if (want > max_by_tiles) want = max_by_tiles;
+  // whole waves of workgroups only: a launch of target + a few would run a
+  // second, nearly empty round on the CUs
+  int want = target_blocks() / units;
+  const int wpg = (G > 4 && (g.hd == 128 || (g.int8 && !g.ring))) ? kWaves / 2 : kWaves;
+  const int max_by_chunks = (nchunks + wpg - 1) / wpg;  // >= one chunk per wave
+  if (want > max_by_chunks) want = max_by_chunks;
   if (want > kMaxSplits) want = kMaxSplits;
   if (want < 1) want = 1;
-  const int tps = (ntiles + want - 1) / want;
-  *tiles_per_split = tps;
-  *nsplit = (ntiles + tps - 1) / tps;
+  Plan p;
+  p.chunks_per_split = (nchunks + want - 1) / want;
+  p.nsplit = (nchunks + p.chunks_per_split - 1) / p.chunks_per_split;
+  p.merge = p.nsplit > 1 || sinks;
+  return p;
 }
 
 }  // namespace
 
 bool attention_supported(const KvGeom& g, int n_heads) {
-  if (n_heads <= 0 || n_heads % g.nkv != 0) return false;
+  if (n_heads <= 0 || n_heads % g.nkv != 0 || !g.tiled) return false;
   return pick_kernel(g.hd, kind_of(g), n_heads / g.nkv) != nullptr;
 }
 
 size_t attention_workspace_need(const KvGeom& g, const AttnCall& c) {
-  int nsplit = 1, tps = 1;
-  plan(g, c, &nsplit, &tps);
+  const Plan p = plan(g, c);
   const int G = c.n_heads / g.nkv;
-  return nsplit > 1 ? static_cast<size_t>(c.rows) * g.nkv * nsplit * G * (g.hd + 2) : 0;
+  return p.merge ? static_cast<size_t>(c.rows) * g.nkv * p.nsplit * G * (g.hd + 2) : 0;
 }
 
 hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, const AttnCall& c,
                             hipStream_t st) {
   const int G = c.n_heads / g.nkv;
   void* fn = pick_kernel(g.hd, kind_of(g), G);
-  if (fn == nullptr) return hipErrorNotSupported;
+  if (fn == nullptr || !g.tiled) return hipErrorNotSupported;
   AttnParams p{};
-  const size_t layer_rows = static_cast<size_t>(c.layer) * g.nkv * g.cap;
+  const size_t layer_heads = static_cast<size_t>(c.layer) * g.nkv;
+  const size_t layer_el = layer_heads * head_elems(g);
   if (!g.int8) {
-    p.kf = s.k + layer_rows * g.hd;
-    p.vf = s.v + layer_rows * g.hd;
+    p.kf = s.k + layer_el;
+    p.vf = s.v + layer_el;
   } else {
-    p.k8 = s.k8 + layer_rows * g.hd;
-    p.v8 = s.v8 + layer_rows * g.hd;
-    p.vs = s.v_scale + layer_rows * g.nb;
+    p.k8 = reinterpret_cast<const uint8_t*>(s.k8) + layer_el;
+    p.v8 = reinterpret_cast<const uint8_t*>(s.v8) + layer_el;
+    p.vs = s.v_scale + layer_heads * g.capg * g.nb;
     if (g.ring) {
-      p.ks = s.k_scale + layer_rows * g.nb;
+      p.ks = s.k_scale + layer_heads * g.capg * g.nb;
     } else {
-      p.ks = s.k_scale + static_cast<size_t>(c.layer) * g.nkv * g.ngroups * g.hd;
+      p.ks = s.k_scale + layer_heads * g.ngroups * g.hd;
       if (g.n_sink > 0) {
-        p.ksink = s.k_sink + static_cast<size_t>(c.layer) * g.nkv * g.n_sink * g.hd;
-        p.vsink = s.v_sink + static_cast<size_t>(c.layer) * g.nkv * g.n_sink * g.hd;
+        p.ksink = s.k_sink + layer_heads * g.n_sink * g.hd;
+        p.vsink = s.v_sink + layer_heads * g.n_sink * g.hd;
       }
     }
   }
   p.rope = s.rope_cs;
+  p.rope_rows = g.ring ? g.cap : 0;
   p.q = c.q;
   p.out = c.out;
   p.part = ws.part;
-  p.cap = g.cap;
+  p.capg = g.capg;
   p.ng = g.ngroups;
   p.n_sink = g.int8 && !g.ring ? g.n_sink : 0;
   p.nkv = g.nkv;
@@ -857,17 +886,21 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
   p.ring_s = c.ring.s;
   p.ring_W = c.ring.W > 0 ? c.ring.W : 1;
   p.ring_base = c.ring.base;
-  plan(g, c, &p.nsplit, &p.tiles_per_split);
+  const Plan pl = plan(g, c);
+  p.nsplit = pl.nsplit;
+  p.direct = pl.merge ? 0 : 1;
+  p.chunks_per_split = pl.chunks_per_split;
   p.qscale = c.scale * kLog2e;
   void* args[] = {&p};
   hipError_t e = hipLaunchKernel(fn, dim3(p.nsplit, g.nkv, c.rows), dim3(kThreads), args, 0, st);
-  if (e != hipSuccess || p.nsplit == 1) return e;
+  if (e != hipSuccess || !pl.merge) return e;
+  SinkArgs sa{c.q, p.ksink, p.vsink, p.ksink != nullptr ? g.n_sink : 0, c.pos0, p.qscale};
   if (g.hd == 64)
     hipLaunchKernelGGL(merge_kernel<64>, dim3(c.n_heads, c.rows), dim3(64), 0, st, ws.part, c.out,
-                       g.nkv, G, p.nsplit, c.n_heads);
+                       g.nkv, G, p.nsplit, c.n_heads, sa);
   else
     hipLaunchKernelGGL(merge_kernel<128>, dim3(c.n_heads, c.rows), dim3(128), 0, st, ws.part,
-                       c.out, g.nkv, G, p.nsplit, c.n_heads);
+                       c.out, g.nkv, G, p.nsplit, c.n_heads, sa);
   return hipGetLastError();
 }
 

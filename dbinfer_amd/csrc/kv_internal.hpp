@@ -4,14 +4,26 @@
 // Device storage is head-major, so the keys of one kv head are one contiguous
 // stream for decode attention (the reference stores [slot][kv_head][hd],
 // model.hpp:108-214; dbi_kv_export converts back):
-//   fp32 (dense, ring)  k, v          [L][nkv][cap][hd]   fp32
-//   int8                k8, v8        [L][nkv][cap][hd]   int8
-//                       v_scale       [L][nkv][cap][nb]   fp32
-//   ring int8           k_scale       [L][nkv][cap][nb]   fp32 (per 32-block)
+//   fp32 (dense, ring)  k, v          [L][nkv][capg*hd]   fp32, granule layout
+//   int8                k8, v8        [L][nkv][capg*hd]   uint8 code+128, granule layout
+//                       v_scale       [L][nkv][capg][nb]  fp32
+//   ring int8           k_scale       [L][nkv][capg][nb]  fp32 (per 32-block)
 //   dense int8          k_scale       [L][nkv][ng][hd]    fp32 (per channel, per 32-token group)
 //                       k_raw         [L][32][nkv*hd]     fp32 (reference order)
 //                       k_sink,v_sink [L][nkv][ns][hd]    fp32
 //   ring                rope_cs       [cap][hd/2]         float2 (cos, sin)
+// capg is the capacity rounded up to whole 32-position chunks (two granules).
+//
+// Granule layout (head dims 64 and 128; other head dims are stored row-major
+// [pos][hd]): 16 positions per granule, 16*hd elements. A wave reads one
+// "slot" of a granule per load instruction, 64 lanes x 8 elements,
+// contiguous: int8 [slot][lane][8], fp32 [slot][half][lane][4]. Lane
+// l = r*LPR + c, LPR = hd/8 lanes per position row, RPW = 64/LPR rows; slot j
+// of row r holds granule position i*RPW + r, with i = j for V and
+// i = j ^ kslot_xor(c) for K (the permutation that lets the attention kernel
+// reduce 16 lanes' partial dots with one DPP add per position, see
+// attention.hip). K lane c holds dims 4c..4c+3 and hd/2+4c..hd/2+4c+3 (rope
+// pairs d, d+hd/2 in one lane); V lane c holds dims 8c..8c+7.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -29,8 +41,45 @@ constexpr int kKGroup = 32;  // kKvKGroup, model.hpp:87
 
 struct KvGeom {
   int n_layers, cap, nkv, hd, nb, n_sink, window, ngroups;
+  int capg;    // cap rounded up to a multiple of kCapAlign (rows per kv head)
   bool int8, ring;
+  bool tiled;  // granule layout (hd 64 / 128); row-major otherwise
 };
+
+constexpr int kGranule = 16;
+constexpr int kCapAlign = 32;  // the attention kernels read whole 32-position chunks
+
+__host__ __device__ inline int kslot_xor(int hd, int c) {
+  return hd == 128 ? ((((c >> 3) & 1) << 1) ^ ((c >> 2) & 1)) : ((c >> 2) & 1);
+}
+
+__host__ __device__ inline size_t granule_off(int hd, bool int8, int pos, int j, int l, int e) {
+  const size_t base = static_cast<size_t>(pos >> 4) * kGranule * hd + static_cast<size_t>(j) * 512;
+  return int8 ? base + l * 8 + e : base + (e >> 2) * 256 + l * 4 + (e & 3);
+}
+
+// Offset of element (pos, d) inside one (layer, kv head) K array.
+__host__ __device__ inline size_t k_off(const KvGeom& g, int pos, int d) {
+  if (!g.tiled) return static_cast<size_t>(pos) * g.hd + d;
+  const int LPR = g.hd >> 3, RPW = 64 / LPR, pp = pos & 15, r = pp % RPW, i = pp / RPW;
+  const int half = g.hd >> 1;
+  const bool hi = d >= half;
+  const int dd = hi ? d - half : d;
+  const int c = dd >> 2, e = (dd & 3) + (hi ? 4 : 0);
+  return granule_off(g.hd, g.int8, pos, i ^ kslot_xor(g.hd, c), r * LPR + c, e);
+}
+
+// Offset of element (pos, d) inside one (layer, kv head) V array.
+__host__ __device__ inline size_t v_off(const KvGeom& g, int pos, int d) {
+  if (!g.tiled) return static_cast<size_t>(pos) * g.hd + d;
+  const int LPR = g.hd >> 3, RPW = 64 / LPR, pp = pos & 15, r = pp % RPW, i = pp / RPW;
+  return granule_off(g.hd, g.int8, pos, i, r * LPR + (d >> 3), d & 7);
+}
+
+// Elements of one (layer, kv head) K or V array.
+__host__ __device__ inline size_t head_elems(const KvGeom& g) {
+  return static_cast<size_t>(g.capg) * g.hd;
+}
 
 struct KvStore {
   float* k = nullptr;
@@ -83,10 +132,11 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws,
 size_t attention_workspace_need(const KvGeom& g, const AttnCall& c);
 bool attention_supported(const KvGeom& g, int n_heads);
 
-// Prefix pack/unpack between [L][len][nkv][hd] and the head-major store.
+// Prefix pack/unpack between [L][len][nkv][hd] and the head-major store
+// (is_k selects the K or the V granule layout).
 hipError_t launch_prefix_pack(const KvGeom& g, const float* src_store, float* dst, int len,
-                              hipStream_t st);
+                              bool is_k, hipStream_t st);
 hipError_t launch_prefix_unpack(const KvGeom& g, const float* src, float* dst_store, int len,
-                                hipStream_t st);
+                                bool is_k, hipStream_t st);
 
 }  // namespace dbi
