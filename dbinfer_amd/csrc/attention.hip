@@ -153,8 +153,10 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
 __device__ __forceinline__ float4 load_b128(rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
-__device__ __forceinline__ uint2 load_b64(rsrc_t r, int voff, int soff) {
-  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+// K/V rows are read once per call: non-temporal (gfx940+ cache policy NT)
+constexpr int kNT = 2;
+__device__ __forceinline__ float4 stream_b128(rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kNT));
 }
 __device__ __forceinline__ float load_b32(rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
@@ -331,7 +333,6 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
                         : make_rsrc(P.q, 0);
   const rsrc_t rvs = kInt8 ? make_rsrc(P.vs + head * NB, P.capg * NB * 4) : make_rsrc(P.q, 0);
   const rsrc_t rcs = kRing ? make_rsrc(P.rope, P.rope_rows * (HD / 2) * 8) : make_rsrc(P.q, 0);
-  const int lane_k = lane * 8 * ES;  // this lane's 8 elements inside a slot
 
   auto issue_k = [&](int ch) {
     const int p0 = ch * CHUNK;
@@ -342,10 +343,14 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
         const int sl = gs * NSG + j;
         const int so = (p0 + gs * kGranule) * HD * ES + j * 512 * ES;
         if constexpr (kInt8) {
-          kq[sl] = load_b64(rk, lane_k, so);
+          if ((j & 1) == 0) {  // one 16-byte load per lane covers slots j, j + 1
+            const uint4 t = __builtin_bit_cast(uint4, stream_b128(rk, lane * 16, so));
+            kq[sl] = make_uint2(t.x, t.y);
+            kq[sl + 1] = make_uint2(t.z, t.w);
+          }
         } else {
-          kf[sl][0] = load_b128(rk, lane * 16, so);
-          kf[sl][1] = load_b128(rk, lane * 16, so + 1024);
+          kf[sl][0] = stream_b128(rk, lane * 16, so);
+          kf[sl][1] = stream_b128(rk, lane * 16, so + 1024);
         }
         if constexpr (kRing) {
           const int p = min(p0 + gs * kGranule + (j ^ kx_slot) * RPW + r, nkeys - 1);
@@ -375,27 +380,26 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
         const int pb = p0 + gs * kGranule + i * RPW;  // position of row 0
         const int so = (p0 + gs * kGranule) * HD * ES + i * 512 * ES;
         if constexpr (kInt8) {
-          vq[sl] = load_b64(rv, lane_k, so);
+          if ((i & 1) == 0) {
+            const uint4 t = __builtin_bit_cast(uint4, stream_b128(rv, lane * 16, so));
+            vq[sl] = make_uint2(t.x, t.y);
+            vq[sl + 1] = make_uint2(t.z, t.w);
+          }
           vsc[sl] = load_b32(rvs, (r * NB + (8 * c) / kBlock) * 4, pb * NB * 4);
         } else {
-          vf[sl][0] = load_b128(rv, lane * 16, so);
-          vf[sl][1] = load_b128(rv, lane * 16, so + 1024);
+          vf[sl][0] = stream_b128(rv, lane * 16, so);
+          vf[sl][1] = stream_b128(rv, lane * 16, so + 1024);
         }
       }
   };
 
-  int ch = split * P.chunks_per_split + wl;
-  if (ch < c_end) {
-    issue_k(ch);
-    issue_v(ch);
-  }
-
   // ---- q of this lane's K dims (4c..4c+3, hd/2+4c..), in the log2 domain;
-  // the ring ropes it at n_res - 1 (model.cpp:669-671)
-  float qv[GW][8];
+  // the ring ropes it at n_res - 1 (model.cpp:669-671). Its loads go out
+  // before the first chunk's: vector loads return in order, so q issued last
+  // would hold QK back until the whole chunk (V included) had arrived.
+  float4 qa[GW], qc[GW], cq[2];
   {
     const float* qb = P.q + (static_cast<size_t>(qrow) * P.n_heads + kh * G) * HD;
-    float4 cq[2];
     if constexpr (kRing) {
       const float4* t = reinterpret_cast<const float4*>(
           P.rope + static_cast<size_t>(P.ring_nres - 1) * (HD / 2) + 4 * c);
@@ -404,26 +408,36 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
     }
 #pragma unroll
     for (int g = 0; g < GW; ++g) {
-      // a head group's padding head (odd G) gets q = 0 and is never stored
-      const bool hv = g0 + g < G;
-      const float* qg = qb + (hv ? g0 + g : 0) * HD;
-      float4 a = *reinterpret_cast<const float4*>(qg + 4 * c);
-      float4 b = *reinterpret_cast<const float4*>(qg + HD / 2 + 4 * c);
-      if (!hv) a = b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      if constexpr (kRing) {
-        const float cv[4] = {cq[0].x, cq[0].z, cq[1].x, cq[1].z};
-        const float sv[4] = {cq[0].y, cq[0].w, cq[1].y, cq[1].w};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float u = x[t], w = x[4 + t];
-          x[t] = u * cv[t] - w * sv[t];
-          x[4 + t] = w * cv[t] + u * sv[t];
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qv[g][e] = x[e] * P.qscale;
+      const float* qg = qb + min(g0 + g, G - 1) * HD;
+      qa[g] = *reinterpret_cast<const float4*>(qg + 4 * c);
+      qc[g] = *reinterpret_cast<const float4*>(qg + HD / 2 + 4 * c);
     }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  int ch = split * P.chunks_per_split + wl;
+  if (ch < c_end) {
+    issue_k(ch);
+    issue_v(ch);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float qv[GW][8];
+#pragma unroll
+  for (int g = 0; g < GW; ++g) {
+    // a head group's padding head (odd G) gets q = 0 and is never stored
+    const bool hv = g0 + g < G;
+    float x[8] = {qa[g].x, qa[g].y, qa[g].z, qa[g].w, qc[g].x, qc[g].y, qc[g].z, qc[g].w};
+    if constexpr (kRing) {
+      const float cv[4] = {cq[0].x, cq[0].z, cq[1].x, cq[1].z};
+      const float sv[4] = {cq[0].y, cq[0].w, cq[1].y, cq[1].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float u = x[t], w = x[4 + t];
+        x[t] = u * cv[t] - w * sv[t];
+        x[4 + t] = w * cv[t] + u * sv[t];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[g][e] = hv ? x[e] * P.qscale : 0.0f;
   }
 
   float M[GW], l[GW], o[GW][8], corr[kInt8 ? GW : 1];

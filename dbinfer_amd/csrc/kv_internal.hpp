@@ -16,8 +16,9 @@
 //
 // Granule layout (head dims 64 and 128; other head dims are stored row-major
 // [pos][hd]): 16 positions per granule, 16*hd elements. A wave reads one
-// "slot" of a granule per load instruction, 64 lanes x 8 elements,
-// contiguous: int8 [slot][lane][8], fp32 [slot][half][lane][4]. Lane
+// "slot" of a granule per 64 lanes x 8 elements, each load instruction one
+// contiguous KiB: int8 [slot pair][lane][2 slots][8] (one 16-byte load per
+// lane covers two slots), fp32 [slot][half][lane][4]. Lane
 // l = r*LPR + c, LPR = hd/8 lanes per position row, RPW = 64/LPR rows; slot j
 // of row r holds granule position i*RPW + r, with i = j for V and
 // i = j ^ kslot_xor(c) for K (the permutation that lets the attention kernel
@@ -55,7 +56,8 @@ __host__ __device__ inline int kslot_xor(int hd, int c) {
 
 __host__ __device__ inline size_t granule_off(int hd, bool int8, int pos, int j, int l, int e) {
   const size_t base = static_cast<size_t>(pos >> 4) * kGranule * hd + static_cast<size_t>(j) * 512;
-  return int8 ? base + l * 8 + e : base + (e >> 2) * 256 + l * 4 + (e & 3);
+  return int8 ? base - (j & 1) * 512 + l * 16 + (j & 1) * 8 + e
+              : base + (e >> 2) * 256 + l * 4 + (e & 3);
 }
 
 // Offset of element (pos, d) inside one (layer, kv head) K array.
