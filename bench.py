@@ -6,8 +6,9 @@ attention shape of config 3 -- 28 layers, 24 query / 8 kv heads, head_dim
 per-block V, 4 fp32 sinks) holding 8192 positions of synthetic N(0,1) keys
 and values with 1% outlier channels x8. One step decodes one token through
 all 28 layers: per layer, quantize-on-append at position 8191 then GQA decode
-attention over the 8192 resident keys. Inputs (q, k, v) are resident in HBM
-before the timed region; the step is replayed from a HIP graph.
+attention over the 8192 resident keys (dbi_kv_decode: one fused kernel plus
+its split merge). Inputs (q, k, v) are resident in HBM before the timed
+region; the step is replayed from a HIP graph.
 
 The same step over the fp32 cache of that shape (the reference point of
 BASELINE.md) is reported beside it. The working sets (529 MB int8, 1.9 GB
@@ -73,11 +74,15 @@ def build_cache(torch, HipKV, dtype_code, K, V):
 
 
 def step(kv, K, V, q, out, scale, attention_only=False):
-    """One decode token through all layers: append at POS then attend."""
+    """One decode token through all layers: per layer the fused decode step
+    (quantize-on-append at POS + attention, one kernel and its split merge);
+    attention_only leaves the cache as it is and times the attention call."""
     for layer in range(L):
-        if not attention_only:
-            kv.append_async(layer, POS, 1, K[layer, POS].data_ptr(), V[layer, POS].data_ptr())
-        kv.attend_async(layer, POS, NH, scale, q[layer].data_ptr(), out[layer].data_ptr())
+        if attention_only:
+            kv.attend_async(layer, POS, NH, scale, q[layer].data_ptr(), out[layer].data_ptr())
+        else:
+            kv.decode_async(layer, POS, K[layer, POS].data_ptr(), V[layer, POS].data_ptr(), NH,
+                            scale, q[layer].data_ptr(), out[layer].data_ptr())
 
 
 def capture(torch, fn):
@@ -292,7 +297,7 @@ def main():
         "config": {
             "workload": "config 3: Llama-3.2-3B attention shape, dense int8 KV (per-channel K, "
                         "per-block V, 4 fp32 sinks), decode step at ctx 8192 over 28 layers "
-                        "(append + GQA decode attention per layer, HIP-graph replay)",
+                        "(fused append + GQA decode attention per layer, HIP-graph replay)",
             "n_layers": L, "n_heads": NH, "n_kv_heads": NKV, "head_dim": HD, "ctx": CTX,
             "parallelism": "single GPU",
         },

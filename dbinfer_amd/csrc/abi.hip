@@ -128,10 +128,31 @@ dbi_status check_attend(const dbi_kv* kv, uint32_t layer, uint32_t n_heads, cons
   return DBI_OK;
 }
 
+dbi_status append_impl(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, const float* k_dev,
+                       const float* v_dev);
+
 dbi_status decode_impl(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads, float scale,
-                       const float* q_dev, float* out_dev) {
+                       const float* q_dev, float* out_dev, const float* k_dev = nullptr,
+                       const float* v_dev = nullptr) {
   if (dbi_status st = check_rows(kv, pos, 1)) return st;
+  // the fused kernel reads the new rows 16 bytes per lane; rows that are not
+  // 16-byte aligned go through the append kernel first
+  if (k_dev != nullptr &&
+      ((reinterpret_cast<uintptr_t>(k_dev) | reinterpret_cast<uintptr_t>(v_dev)) & 15) != 0) {
+    if (dbi_status st = append_impl(kv, layer, pos, 1, k_dev, v_dev)) return st;
+    k_dev = v_dev = nullptr;
+  }
   dbi::AttnCall c{};
+  if (k_dev != nullptr) {
+    const dbi::KvGeom& g = kv->geom;
+    c.app_k = k_dev;
+    c.app_v = v_dev;
+    c.app_pos = static_cast<int>(pos);
+    c.app_slot = g.ring ? (static_cast<int>(pos) < g.n_sink
+                               ? static_cast<int>(pos)
+                               : g.n_sink + static_cast<int>((pos - g.n_sink) % g.window))
+                        : static_cast<int>(pos);
+  }
   c.layer = static_cast<int>(layer);
   c.rows = 1;
   c.pos0 = static_cast<int>(pos);
@@ -142,6 +163,7 @@ dbi_status decode_impl(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_head
   if (kv->geom.ring) c.ring = ring_view(kv, pos + 1);
   if (dbi_status st = ensure_workspace(kv, c)) return st;
   HIP_TRY(dbi::launch_attention(kv->geom, kv->store, kv->ws, c, kv->stream), "attention launch");
+  if (k_dev != nullptr) kv->n_seen = pos + 1;
   return DBI_OK;
 }
 
@@ -397,6 +419,37 @@ dbi_status dbi_attn_decode_async(dbi_kv* kv, uint32_t layer, uint32_t pos, uint3
   if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
   if (dbi_status st = check_attend(kv, layer, n_heads, q_dev, out_dev)) return st;
   return decode_impl(kv, layer, pos, n_heads, scale, q_dev, out_dev);
+}
+
+dbi_status dbi_kv_decode(dbi_kv* kv, uint32_t layer, uint32_t pos, const float* k,
+                         const float* v, uint32_t n_heads, float scale, const float* q,
+                         float* out) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (dbi_status st = append_check(kv, layer, pos, 1, k, v)) return st;
+  if (dbi_status st = check_attend(kv, layer, n_heads, q, out)) return st;
+  const size_t P = size_t(kv->cfg.n_kv_heads) * kv->cfg.head_dim;
+  const size_t qn = size_t(n_heads) * kv->cfg.head_dim;
+  if (dbi_status st = need_staging(kv, 2 * P + 2 * qn)) return st;
+  float* kd = kv->ws.staging;
+  float* vd = kd + P;
+  float* qd = vd + P;
+  float* od = qd + qn;
+  HIP_TRY(hipMemcpyAsync(kd, k, P * 4, hipMemcpyHostToDevice, kv->stream), "k upload");
+  HIP_TRY(hipMemcpyAsync(vd, v, P * 4, hipMemcpyHostToDevice, kv->stream), "v upload");
+  HIP_TRY(hipMemcpyAsync(qd, q, qn * 4, hipMemcpyHostToDevice, kv->stream), "q upload");
+  if (dbi_status st = decode_impl(kv, layer, pos, n_heads, scale, qd, od, kd, vd)) return st;
+  HIP_TRY(hipMemcpyAsync(out, od, qn * 4, hipMemcpyDeviceToHost, kv->stream), "out readback");
+  HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+  return DBI_OK;
+}
+
+dbi_status dbi_kv_decode_async(dbi_kv* kv, uint32_t layer, uint32_t pos, const float* k_dev,
+                               const float* v_dev, uint32_t n_heads, float scale,
+                               const float* q_dev, float* out_dev) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (dbi_status st = append_check(kv, layer, pos, 1, k_dev, v_dev)) return st;
+  if (dbi_status st = check_attend(kv, layer, n_heads, q_dev, out_dev)) return st;
+  return decode_impl(kv, layer, pos, n_heads, scale, q_dev, out_dev, k_dev, v_dev);
 }
 
 dbi_status dbi_attn_chunk(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,

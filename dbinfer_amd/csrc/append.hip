@@ -2,48 +2,16 @@
 // leaves the storage exactly as n sequential KVCache::append calls would
 // (model.cpp:357-404).
 //
-// Bit-exactness of the int8 paths rests on three facts: max|x| is
-// order-free, x / 127.0f and 1.0f / s are IEEE correctly rounded divisions
-// (HIP's default, never fast-math), and the code is round-half-away of one
-// fp32 product, clamped to [-127, 127] (quant_code below). Codes are stored
-// biased, as the byte code + 128, in the granule layout of kv_internal.hpp.
+// The int8 arithmetic (quant.hpp) is bit-exact with the reference; codes are
+// stored biased, as the byte code + 128, in the granule layout of
+// kv_internal.hpp.
 #include "kv_internal.hpp"
+#include "quant.hpp"
 
 namespace dbi {
 namespace {
 
 constexpr int kThreads = 256;
-
-__device__ __forceinline__ float max_f(float a, float b) { return (a < b) ? b : a; }
-
-// clamp(lround(x * inv), -127, 127) as glibc computes it on x86-64: lround of a
-// NaN, an infinity or |x| >= 2^63 yields LONG_MIN, which clamps to -127.
-__device__ __forceinline__ int8_t quant_code(float x, float inv) {
-  const float r = x * inv;
-  if (!(fabsf(r) < 9223372036854775808.0f)) return -127;
-  const float t = roundf(r);
-  return static_cast<int8_t>(t > 127.0f ? 127 : (t < -127.0f ? -127 : static_cast<int>(t)));
-}
-
-// quant_head (model.cpp:303-317) of one block with one lane per element: lanes of an aligned
-// 32-lane group hold the block's elements (inactive tail lanes pass 0), the
-// block max comes from xor shuffles inside the group. Every lane returns its
-// code; the block scale is returned through *scale.
-__device__ __forceinline__ int8_t quant_lane(float x, float* scale) {
-  float m = fabsf(x);
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) m = max_f(m, __shfl_xor(m, off, 32));
-  const float s = m / 127.0f;
-  *scale = s;
-  const float inv = s > 0.0f ? 1.0f / s : 0.0f;
-  return quant_code(x, inv);
-}
-
-__device__ __forceinline__ int8_t biased(int8_t code) { return static_cast<int8_t>(code ^ 0x80); }
-
-__device__ __forceinline__ int slot_for(int pos, int s, int W) {
-  return pos < s ? pos : s + (pos - s) % W;
-}
 
 // In a batch, a ring row is overwritten by row p + W when that row is in the
 // same batch; only the last writer of each slot stores (sequential result).

@@ -42,8 +42,10 @@
 //    and d + hd/2 together, so the rotation is lane-local.
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 #include "kv_internal.hpp"
+#include "quant.hpp"
 
 namespace dbi {
 namespace {
@@ -153,13 +155,13 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
 __device__ __forceinline__ float4 load_b128(rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
+__device__ __forceinline__ float load_b32(rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
 // K/V rows are read once per call: non-temporal (gfx940+ cache policy NT)
 constexpr int kNT = 2;
 __device__ __forceinline__ float4 stream_b128(rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kNT));
-}
-__device__ __forceinline__ float load_b32(rsrc_t r, int voff, int soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 
 // 8 biased int8 codes -> code + 128 as float (one v_cvt_f32_ubyteN each)
@@ -268,8 +270,278 @@ __device__ __forceinline__ void finish(const AttnParams& P, float (&s_o)[kWaves]
   }
 }
 
+// Fused decode step (Model::decode_layer's kv.append then attend,
+// model.cpp:759-771): the row of one position, written by the workgroup
+// whose split holds its storage chunk, before that chunk is read.
+struct AppendArgs {
+  const float* k;  // new row, device [nkv][hd]; nullptr: no append
+  const float* v;
+  int slot;        // storage row (dense: pos; ring: slot_for(pos)); -1: no append
+  int pos;
+  int nkv, n_sink, capg, ng;
+  float* kf;       // this layer's arrays, writable
+  float* vf;
+  uint8_t* k8;
+  uint8_t* v8;
+  float* ks;
+  float* vs;
+  float* k_raw;    // dense int8 staging [32][nkv*hd]
+  float* ksink;
+  float* vsink;
+};
+
+// LDS stage of a fused step's new values, in the layouts the attention
+// reads them in, for the wave that processes the appended chunk.
+struct AppStage {
+  float ks[4];                       // ring int8: the new row's K block scales
+  float vs[4];                       // int8: the new row's V block scales
+  float krow[128];                   // fp32: the new K row
+  float vrow[128];                   // fp32: the new V row
+  uint32_t k8row[32];                // ring int8: the new K codes (biased bytes)
+  uint32_t v8row[32];                // int8: the new V codes (biased bytes)
+};
+
+// Dense int8: the requantized 32-token group of the fused step, shared by
+// the head groups of the workgroup.
+struct KGroupStage {
+  uint4 kchunk[kKGroup * 128 / 16];  // the group's codes, granule layout
+  float ks[128];                     // its channel scales
+  unsigned done;                     // requantizing waves done (zeroed at launch)
+};
+
+// One kv head's part of KVCache::append (model.cpp:357-404) inside the
+// attention kernel, with the arithmetic of the append kernels (quant.hpp):
+// fp32 rows are copied; int8 ring rows are block-quantized (a 32-element
+// block spans 16 lanes, two elements per lane); dense int8 stages the raw K
+// row and requantizes its 32-token group per channel, and block-quantizes
+// V, or stores both as fp32 sinks when pos < n_sink. New values go to LDS
+// stages in the layouts the attention reads, and to global memory only
+// after the writing wave's last load (a store in flight would hold back its
+// next wait on loads).
+//
+// Work split: the wave (of each head group) that attends the new row's
+// chunk, the owner, stages the row itself. The dense int8 group
+// requantization (32 codes per channel, far too long for one wave's
+// critical path) is shared by the first RW waves of the workgroup, CPW
+// channels each, before their own chunk: their loads go out first, so the
+// shares are done by the time the owner (usually a later wave) reaches the
+// new row's chunk. They publish through an LDS counter that only the owners
+// wait on; no other wave waits.
+//
+// Loads are LDS-direct (16 bytes per lane, no registers held): the new K
+// and V rows into `row` ([0, HD) and [HD, 2 HD) of 256 floats; k_dev and
+// v_dev are 16-byte aligned) and a wave's channels of the group's 32 staged
+// raw rows into its `raw` share ([32][CPW]). The compiler does not track
+// these loads: the consumers wait for them explicitly.
+template <int HD, int KIND>
+struct FusedAppend {
+  static constexpr bool kInt8 = (KIND == kI8Dense || KIND == kI8Ring);
+  static constexpr int NB = HD / kBlock;
+  static constexpr int RW = kWaves / 2;       // dense int8: requantizing waves
+  static constexpr int CPW = HD / RW;         // channels per requantizing wave
+  static constexpr int RPL = kKGroup * CPW / 64;  // raw rows per lane of a share
+
+  __device__ __forceinline__ static void wait_loads() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  __device__ __forceinline__ static void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  __device__ __forceinline__ static void load_row(const AppendArgs& A, int kh, int lane,
+                                                  float* row) {
+    constexpr int Q = HD / 4;         // lanes per row
+    const int hl = lane % (2 * Q);    // lanes past 2Q (hd 64) repeat into row[2 HD, 4 HD)
+    const float* src = (hl < Q ? A.k : A.v) + kh * HD + (hl % Q) * 4;
+    __builtin_amdgcn_global_load_lds(src, row, 16, 0, 0);
+  }
+
+  // dense int8, wave < RW: its raw share (LDS-direct) and its channels of
+  // the new K row (returned; lane l holds channel l % CPW of the share)
+  __device__ __forceinline__ static float load_share(const AppendArgs& A, int kh, int wave,
+                                                     int lane, float* raw) {
+    constexpr int LPRW = CPW / 4, RPI = 64 / LPRW;  // lanes per share row, rows per load
+    const size_t P_ = static_cast<size_t>(A.nkv) * HD;
+    const float* src = A.k_raw + static_cast<size_t>(lane / LPRW) * P_ + kh * HD + wave * CPW +
+                       (lane % LPRW) * 4;
+#pragma unroll
+    for (int m = 0; m < kKGroup / RPI; ++m)
+      __builtin_amdgcn_global_load_lds(src + m * RPI * P_, raw + m * RPI * CPW, 16, 0, 0);
+    return A.k[kh * HD + wave * CPW + lane % CPW];
+  }
+
+  // dense int8, wave < RW, after wait_loads(): requantize_kgroup
+  // (model.cpp:329-355) of the wave's CPW channels over raw rows
+  // [0, within] that are not sinks (row `within` is the new one). Lane l
+  // takes channel l % CPW over RPL rows; the channel max combines its lanes
+  // by xor shuffles. Rows outside the range count |x| * 0 (0, or a NaN that
+  // max_f skips as it skips NaN inputs) and their codes are neither
+  // attended (masked positions) nor flushed.
+  __device__ __forceinline__ static void requant_share(const AppendArgs& A, int wave, int lane,
+                                                       float knew, float* raw,
+                                                       KGroupStage& kg) {
+    const int within = A.pos % kKGroup, first = A.pos - within;
+    const int c = lane % CPW, rb = lane / CPW;
+    if (lane < CPW) raw[within * CPW + c] = knew;
+    wave_sync();
+    float x[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) x[i] = raw[(rb * RPL + i) * CPW + c];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) {
+      const int w = rb * RPL + i;
+      m = max_f(m, fabsf(x[i]) * ((w <= within && first + w >= A.n_sink) ? 1.0f : 0.0f));
+    }
+#pragma unroll
+    for (int off = CPW; off < 64; off <<= 1) m = max_f(m, __shfl_xor(m, off));
+    const float sc = m / 127.0f;
+    const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
+    uint8_t* kc = reinterpret_cast<uint8_t*>(kg.kchunk);
+    const int d = wave * CPW + c;
+#pragma unroll
+    for (int i = 0; i < RPL; ++i)
+      kc[k_off_tiled(HD, true, rb * RPL + i, d)] = static_cast<uint8_t>(biased(quant_code(x[i], inv)));
+    if (lane < CPW) kg.ks[d] = sc;
+    // publish (the release orders the stage writes before the count)
+    if (lane == 0) __hip_atomic_fetch_add(&kg.done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+
+  // dense int8 owner: wait until all RW shares are published
+  __device__ __forceinline__ static void await_shares(const KGroupStage& kg) {
+    while (__hip_atomic_load(&kg.done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+           static_cast<unsigned>(RW))
+      __builtin_amdgcn_s_sleep(1);
+  }
+
+  // quant_head of a 32-element block held two per lane by 16 lanes
+  __device__ __forceinline__ static float block_scale(float2 x) {
+    float m = max_f(fabsf(x.x), fabsf(x.y));
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) m = max_f(m, __shfl_xor(m, off, 16));
+    return m / 127.0f;
+  }
+  __device__ __forceinline__ static uint32_t codes2(float2 x, float s) {
+    const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+    const uint32_t a = static_cast<uint8_t>(biased(quant_code(x.x, inv)));
+    const uint32_t b = static_cast<uint8_t>(biased(quant_code(x.y, inv)));
+    return a | (b << 8);
+  }
+
+  // owner wave, after wait_loads(): the row's own values into its stage
+  // (dense int8: V only; the K group is requant_share's)
+  __device__ __forceinline__ static void stage_row(const AppendArgs& A, int lane, AppStage& st,
+                                                   const float* row) {
+    const bool on = 2 * lane < HD;
+    const int d = 2 * lane;
+    const float2 kx = on ? *reinterpret_cast<const float2*>(row + d) : float2{};
+    const float2 vx = on ? *reinterpret_cast<const float2*>(row + HD + d) : float2{};
+    uint16_t* k8s = reinterpret_cast<uint16_t*>(st.k8row);
+    uint16_t* v8s = reinterpret_cast<uint16_t*>(st.v8row);
+    if constexpr (!kInt8) {
+      if (on) {
+        *reinterpret_cast<float2*>(&st.krow[d]) = kx;
+        *reinterpret_cast<float2*>(&st.vrow[d]) = vx;
+      }
+    } else if constexpr (KIND == kI8Ring) {
+      const float sk = block_scale(kx), sv = block_scale(vx);
+      if (on) {
+        k8s[lane] = static_cast<uint16_t>(codes2(kx, sk));
+        v8s[lane] = static_cast<uint16_t>(codes2(vx, sv));
+        if (d % kBlock == 0) {
+          st.ks[d / kBlock] = sk;
+          st.vs[d / kBlock] = sv;
+        }
+      }
+    } else if (A.pos < A.n_sink) {
+      if (on) {
+        v8s[lane] = 0x8080;  // a sink position is masked in the stream; keep the stage finite
+        if (d % kBlock == 0) st.vs[d / kBlock] = 0.0f;
+      }
+    } else {
+      const float sv = block_scale(vx);
+      if (on) {
+        v8s[lane] = static_cast<uint16_t>(codes2(vx, sv));
+        if (d % kBlock == 0) st.vs[d / kBlock] = sv;
+      }
+    }
+    wave_sync();
+  }
+
+  // The stages to global memory in whole contiguous pieces, by one wave per
+  // kv head, after its last load.
+  __device__ __forceinline__ static void flush(const AppendArgs& A, int kh, int lane,
+                                               const AppStage& st, const KGroupStage& kg,
+                                               const float* row) {
+    const bool on = 2 * lane < HD;
+    const int d = 2 * lane;
+    const size_t hel = static_cast<size_t>(kh) * A.capg * HD;
+    constexpr int LPR = HD / 8, RPW = 64 / LPR;
+    const int pg = A.slot & 15, rr = pg % RPW, ii = pg / RPW;  // the row's granule slot
+    if constexpr (KIND == kI8Dense) {
+      const int pos = A.pos, grp = pos / kKGroup, within = pos % kKGroup, first = pos - within;
+#pragma unroll 4
+      for (int m = 0; m < kKGroup * HD / 8 / 64; ++m) {  // one 8-byte piece per lane each
+        const int o = (m * 64 + lane) * 8, gs = o / (kGranule * HD), og = o % (kGranule * HD);
+        const int l = (og % 1024) / 16, j = 2 * (og / 1024) + (og % 16) / 8;
+        const int r = l / LPR, c = l % LPR;
+        const int w = gs * kGranule + (j ^ kslot_xor(HD, c)) * RPW + r;
+        if (w <= within && first + w >= A.n_sink)  // later rows and sinks keep their memory
+          *reinterpret_cast<uint2*>(A.k8 + hel + static_cast<size_t>(first) * HD + o) =
+              *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(kg.kchunk) + o);
+      }
+      if (on) {
+        const float2 kx = *reinterpret_cast<const float2*>(row + d);
+        *reinterpret_cast<float2*>(A.ks + (static_cast<size_t>(kh) * A.ng + grp) * HD + d) =
+            *reinterpret_cast<const float2*>(&kg.ks[d]);
+        *reinterpret_cast<float2*>(A.k_raw + static_cast<size_t>(within) * A.nkv * HD + kh * HD +
+                                   d) = kx;
+        if (pos < A.n_sink) {
+          const size_t at = (static_cast<size_t>(kh) * A.n_sink + pos) * HD + d;
+          *reinterpret_cast<float2*>(A.ksink + at) = kx;
+          *reinterpret_cast<float2*>(A.vsink + at) = *reinterpret_cast<const float2*>(row + HD + d);
+        }
+      }
+      if (pos >= A.n_sink) {
+        if (lane < LPR)  // V row: dims 8c..8c+7 of lane (rr, c)
+          *reinterpret_cast<uint2*>(A.v8 + hel +
+                                    granule_off(HD, true, pos, ii, rr * LPR + lane, 0)) =
+              make_uint2(st.v8row[2 * lane], st.v8row[2 * lane + 1]);
+        if (lane < NB) A.vs[(static_cast<size_t>(kh) * A.capg + pos) * NB + lane] = st.vs[lane];
+      }
+    } else if constexpr (KIND == kI8Ring) {
+      if (lane < LPR) {
+        const int c = lane, j = ii ^ kslot_xor(HD, c);
+        *reinterpret_cast<uint2*>(A.k8 + hel + granule_off(HD, true, A.slot, j, rr * LPR + c, 0)) =
+            make_uint2(st.k8row[c], st.k8row[HD / 8 + c]);
+        *reinterpret_cast<uint2*>(A.v8 + hel + granule_off(HD, true, A.slot, ii, rr * LPR + c, 0)) =
+            make_uint2(st.v8row[2 * c], st.v8row[2 * c + 1]);
+      }
+      if (lane < NB) {
+        const size_t srow = static_cast<size_t>(kh) * A.capg + A.slot;
+        A.ks[srow * NB + lane] = st.ks[lane];
+        A.vs[srow * NB + lane] = st.vs[lane];
+      }
+    } else {
+      if (lane < LPR) {
+        const int c = lane, j = ii ^ kslot_xor(HD, c);
+        float* kdst = A.kf + hel + granule_off(HD, false, A.slot, j, rr * LPR + c, 0);
+        *reinterpret_cast<float4*>(kdst) = *reinterpret_cast<const float4*>(&row[4 * c]);
+        *reinterpret_cast<float4*>(kdst + 256) =
+            *reinterpret_cast<const float4*>(&row[HD / 2 + 4 * c]);
+        float* vdst = A.vf + hel + granule_off(HD, false, A.slot, ii, rr * LPR + c, 0);
+        *reinterpret_cast<float4*>(vdst) = *reinterpret_cast<const float4*>(&row[HD + 8 * c]);
+        *reinterpret_cast<float4*>(vdst + 256) =
+            *reinterpret_cast<const float4*>(&row[HD + 8 * c + 4]);
+      }
+    }
+  }
+};
+
 template <int HD, int G, int KIND>
-__global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
+__global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, const AppendArgs A) {
   using C = Cfg<HD, G, KIND>;
   constexpr int LPR = C::LPR, RPW = C::RPW, NSG = C::NSG, NGC = C::NGC, NS = C::NS;
   constexpr int CHUNK = C::CHUNK, GP = C::GP, NB = C::NB;
@@ -282,6 +554,17 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
   __shared__ float s_M[G];
   __shared__ float s_L[G];
   __shared__ __align__(16) float s_w[kWaves][CHUNK][GP];
+  __shared__ __align__(16) AppStage s_stage[C::NHG];
+  // dense int8 keeps each wave's scaled q in LDS, not registers, between
+  // chunks (it is re-scaled by every group's channel scales anyway)
+  __shared__ __align__(16) float s_qw[KIND == kI8Dense ? kWaves : 1][GW][HD];
+  // dense int8 fused step: each head group's copy of the group's raw K rows
+  // fused step inputs, per head group: the new K and V rows, and (dense
+  // int8) the group's raw K rows
+  __shared__ __align__(16) float s_row[C::NHG][256];
+  __shared__ __align__(16) float s_raw[KIND == kI8Dense ? kWaves / 2 : 1][KIND == kI8Dense ? kKGroup * HD / (kWaves / 2) : 1];
+  __shared__ __align__(16) uint8_t s_kgbuf[KIND == kI8Dense ? sizeof(KGroupStage) : 16];
+  KGroupStage& s_kg = *reinterpret_cast<KGroupStage*>(s_kgbuf);
 
   const int lane = threadIdx.x & 63;
   // wave index as a provably uniform value: buffer-load SGPR offsets derive
@@ -301,6 +584,9 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
   const size_t head = static_cast<size_t>(kh) * P.capg;  // first row of this kv head
   const size_t head_el = head * HD;
   const int kx_slot = kslot_xor(HD, c);  // granule slot of this lane's scores
+  const int app_chunk = A.slot >= 0 ? A.slot / CHUNK : -1;
+  const bool app_here =
+      app_chunk >= split * P.chunks_per_split && app_chunk < c_end;  // workgroup-uniform
 
   // ---- per-chunk register buffers
   uint2 kq[kInt8 ? NS : 1], vq[kInt8 ? NS : 1];
@@ -335,7 +621,9 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
   const rsrc_t rcs = kRing ? make_rsrc(P.rope, P.rope_rows * (HD / 2) * 8) : make_rsrc(P.q, 0);
 
   auto issue_k = [&](int ch) {
-    const int p0 = ch * CHUNK;
+    const int p0 = __builtin_amdgcn_readfirstlane(ch * CHUNK);  // uniform: SGPR offsets
+    // the group a fused step requantized comes from LDS (patch_k)
+    if (KIND == kI8Dense && ch == app_chunk) return;
 #pragma unroll
     for (int gs = 0; gs < NGC; ++gs)
 #pragma unroll
@@ -371,7 +659,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
   };
 
   auto issue_v = [&](int ch) {
-    const int p0 = ch * CHUNK;
+    const int p0 = __builtin_amdgcn_readfirstlane(ch * CHUNK);  // uniform: SGPR offsets
 #pragma unroll
     for (int gs = 0; gs < NGC; ++gs)
 #pragma unroll
@@ -413,6 +701,32 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
       qc[g] = *reinterpret_cast<const float4*>(qg + HD / 2 + 4 * c);
     }
   }
+  // fused decode step (FusedAppend): the owner wave of each head group
+  // stages the new row and takes its values from the stage for that chunk,
+  // so no global read-after-write happens inside the kernel. The row's
+  // inputs load ahead of the owner's first chunk when that chunk is the new
+  // row's, else right behind it (vector loads return in order, so they then
+  // hold back nothing before that chunk), and are staged on reaching the
+  // chunk. Dense int8: waves [0, RW) requantize the row's group before their
+  // own chunk and count themselves done in LDS (zeroed here first).
+  AppStage& s_app = s_stage[wave / WPG];
+  const int app_rel = app_chunk - split * P.chunks_per_split;
+  const bool app_owner = app_here && wl == app_rel % WPG;  // wave-uniform
+  const bool app_first = app_rel / WPG == 0;
+  using App = FusedAppend<HD, KIND>;
+  float* app_row = s_row[wave / WPG];
+  constexpr bool kShare = KIND == kI8Dense;
+  const bool app_share = kShare && app_here && wave < App::RW;  // wave-uniform
+  float* app_raw = s_raw[kShare && wave < App::RW ? wave : 0];
+  if constexpr (kShare) {
+    if (app_here) {  // workgroup-uniform
+      if (threadIdx.x == 0) s_kg.done = 0;
+      __syncthreads();
+    }
+  }
+  float app_knew = 0.0f;
+  if (app_share) app_knew = App::load_share(A, kh, wave, lane, app_raw);
+  if (app_owner && app_first) App::load_row(A, kh, lane, app_row);
   __builtin_amdgcn_sched_barrier(0);
   int ch = split * P.chunks_per_split + wl;
   if (ch < c_end) {
@@ -420,6 +734,12 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
     issue_v(ch);
   }
   __builtin_amdgcn_sched_barrier(0);
+  if (app_owner && !app_first) App::load_row(A, kh, lane, app_row);
+  __builtin_amdgcn_sched_barrier(0);
+  if (app_share) {
+    App::wait_loads();
+    App::requant_share(A, wave, lane, app_knew, app_raw, s_kg);
+  }
   float qv[GW][8];
 #pragma unroll
   for (int g = 0; g < GW; ++g) {
@@ -439,6 +759,20 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) qv[g][e] = hv ? x[e] * P.qscale : 0.0f;
   }
+  if constexpr (KIND == kI8Dense) {
+    if (r == 0) {
+#pragma unroll
+      for (int g = 0; g < GW; ++g) {
+        *reinterpret_cast<float4*>(&s_qw[wave][g][4 * c]) =
+            make_float4(qv[g][0], qv[g][1], qv[g][2], qv[g][3]);
+        *reinterpret_cast<float4*>(&s_qw[wave][g][HD / 2 + 4 * c]) =
+            make_float4(qv[g][4], qv[g][5], qv[g][6], qv[g][7]);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
 
   float M[GW], l[GW], o[GW][8], corr[kInt8 ? GW : 1];
 #pragma unroll
@@ -454,6 +788,46 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
     const int nch = ch + WPG;
     const int p0 = ch * CHUNK;
 
+    // ---- the appended row (fused step): take its new values from the stage
+    const bool app_now = ch == app_chunk;  // uniform
+    const int app_pc = A.slot - p0;        // its position inside the chunk
+    const int app_r = (app_pc & 15) % RPW, app_i = (app_pc & 15) / RPW, app_gs = app_pc >> 4;
+    if (app_now) {
+      App::wait_loads();
+      App::stage_row(A, lane, s_app, app_row);
+      if constexpr (kShare) App::await_shares(s_kg);
+      if constexpr (KIND == kI8Dense) {
+#pragma unroll
+        for (int gs = 0; gs < NGC; ++gs)
+#pragma unroll
+          for (int j = 0; j < NSG; j += 2) {
+            const uint4 t = s_kg.kchunk[(gs * kGranule * HD + j * 512) / 16 + lane];
+            kq[gs * NSG + j] = make_uint2(t.x, t.y);
+            kq[gs * NSG + j + 1] = make_uint2(t.z, t.w);
+          }
+        ksv[0] = *reinterpret_cast<const float4*>(&s_kg.ks[4 * c]);
+        ksv[1] = *reinterpret_cast<const float4*>(&s_kg.ks[HD / 2 + 4 * c]);
+      } else {
+        const bool mine = r == app_r;
+#pragma unroll
+        for (int gs = 0; gs < NGC; ++gs)
+#pragma unroll
+          for (int j = 0; j < NSG; ++j) {
+            const int sl = gs * NSG + j;
+            if (mine && gs == app_gs && (j ^ kx_slot) == app_i) {
+              if constexpr (kInt8) {
+                kq[sl] = make_uint2(s_app.k8row[c], s_app.k8row[HD / 8 + c]);
+                ksc[sl][0] = s_app.ks[(4 * c) / kBlock];
+                ksc[sl][1] = s_app.ks[(HD / 2 + 4 * c) / kBlock];
+              } else {
+                kf[sl][0] = *reinterpret_cast<const float4*>(&s_app.krow[4 * c]);
+                kf[sl][1] = *reinterpret_cast<const float4*>(&s_app.krow[HD / 2 + 4 * c]);
+              }
+            }
+          }
+      }
+    }
+
     // ---- q for this chunk: dense int8 folds the group's channel scales in
     float qt[GW][8], qb[GW];
 #pragma unroll
@@ -461,10 +835,13 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
       if constexpr (KIND == kI8Dense) {
         const float ks8[8] = {ksv[0].x, ksv[0].y, ksv[0].z, ksv[0].w,
                               ksv[1].x, ksv[1].y, ksv[1].z, ksv[1].w};
+        const float4 qa4 = *reinterpret_cast<const float4*>(&s_qw[wave][g][4 * c]);
+        const float4 qb4 = *reinterpret_cast<const float4*>(&s_qw[wave][g][HD / 2 + 4 * c]);
+        const float q8[8] = {qa4.x, qa4.y, qa4.z, qa4.w, qb4.x, qb4.y, qb4.z, qb4.w};
         float sum = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          qt[g][e] = qv[g][e] * ks8[e];
+          qt[g][e] = q8[e] * ks8[e];
           sum += qt[g][e];
         }
         qb[g] = -128.0f * sum;
@@ -569,6 +946,24 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+    if (app_now && r == app_r) {
+#pragma unroll
+      for (int gs = 0; gs < NGC; ++gs)
+#pragma unroll
+        for (int i = 0; i < NSG; ++i) {
+          const int sl = gs * NSG + i;
+          if (gs == app_gs && i == app_i) {
+            if constexpr (kInt8) {
+              vq[sl] = make_uint2(s_app.v8row[2 * c], s_app.v8row[2 * c + 1]);
+              vsc[sl] = s_app.vs[(8 * c) / kBlock];
+            } else {
+              vf[sl][0] = *reinterpret_cast<const float4*>(&s_app.vrow[8 * c]);
+              vf[sl][1] = *reinterpret_cast<const float4*>(&s_app.vrow[8 * c + 4]);
+            }
+          }
+        }
+    }
+
     // ---- PV: lane (row r, dims 8c..8c+7), slot i -> position i*RPW + r.
     // Rows past the last key have weight 0; in the final partial chunk their
     // (stale) V and scales are zeroed as well, so nothing non-finite enters.
@@ -657,6 +1052,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P) {
     }
   }
   finish<HD, G, GW, WPG>(P, s_o, s_ml, s_f, s_M, s_L, split, kh, qrow);
+  if (app_owner && g0 == 0) App::flush(A, kh, lane, s_app, s_kg, app_row);
 }
 
 // fp32 sinks of the dense int8 cache (model.cpp:623-626, 640-644), folded
@@ -905,7 +1301,37 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
   p.direct = pl.merge ? 0 : 1;
   p.chunks_per_split = pl.chunks_per_split;
   p.qscale = c.scale * kLog2e;
-  void* args[] = {&p};
+  AppendArgs a{};
+  a.slot = -1;
+  if (c.app_slot >= 0 && c.app_k != nullptr && c.app_v != nullptr && c.rows == 1) {
+    a.k = c.app_k;
+    a.v = c.app_v;
+    a.slot = c.app_slot;
+    a.pos = c.app_pos;
+    a.nkv = g.nkv;
+    a.n_sink = g.n_sink;
+    a.capg = g.capg;
+    a.ng = g.ngroups;
+    if (!g.int8) {
+      a.kf = s.k + layer_el;
+      a.vf = s.v + layer_el;
+    } else {
+      a.k8 = reinterpret_cast<uint8_t*>(s.k8) + layer_el;
+      a.v8 = reinterpret_cast<uint8_t*>(s.v8) + layer_el;
+      a.vs = s.v_scale + layer_heads * g.capg * g.nb;
+      if (g.ring) {
+        a.ks = s.k_scale + layer_heads * g.capg * g.nb;
+      } else {
+        a.ks = s.k_scale + layer_heads * g.ngroups * g.hd;
+        a.k_raw = s.k_raw + static_cast<size_t>(c.layer) * kKGroup * g.nkv * g.hd;
+        if (g.n_sink > 0) {
+          a.ksink = s.k_sink + layer_heads * g.n_sink * g.hd;
+          a.vsink = s.v_sink + layer_heads * g.n_sink * g.hd;
+        }
+      }
+    }
+  }
+  void* args[] = {&p, &a};
   hipError_t e = hipLaunchKernel(fn, dim3(p.nsplit, g.nkv, c.rows), dim3(kThreads), args, 0, st);
   if (e != hipSuccess || !pl.merge) return e;
   SinkArgs sa{c.q, p.ksink, p.vsink, p.ksink != nullptr ? g.n_sink : 0, c.pos0, p.qscale};

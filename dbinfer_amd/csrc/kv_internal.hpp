@@ -60,22 +60,29 @@ __host__ __device__ inline size_t granule_off(int hd, bool int8, int pos, int j,
               : base + (e >> 2) * 256 + l * 4 + (e & 3);
 }
 
-// Offset of element (pos, d) inside one (layer, kv head) K array.
-__host__ __device__ inline size_t k_off(const KvGeom& g, int pos, int d) {
-  if (!g.tiled) return static_cast<size_t>(pos) * g.hd + d;
-  const int LPR = g.hd >> 3, RPW = 64 / LPR, pp = pos & 15, r = pp % RPW, i = pp / RPW;
-  const int half = g.hd >> 1;
+// Offset of element (pos, d) inside one (layer, kv head) K / V array of the
+// granule layout (hd 64 or 128).
+__host__ __device__ inline size_t k_off_tiled(int hd, bool int8, int pos, int d) {
+  const int LPR = hd >> 3, RPW = 64 / LPR, pp = pos & 15, r = pp % RPW, i = pp / RPW;
+  const int half = hd >> 1;
   const bool hi = d >= half;
   const int dd = hi ? d - half : d;
   const int c = dd >> 2, e = (dd & 3) + (hi ? 4 : 0);
-  return granule_off(g.hd, g.int8, pos, i ^ kslot_xor(g.hd, c), r * LPR + c, e);
+  return granule_off(hd, int8, pos, i ^ kslot_xor(hd, c), r * LPR + c, e);
+}
+__host__ __device__ inline size_t v_off_tiled(int hd, bool int8, int pos, int d) {
+  const int LPR = hd >> 3, RPW = 64 / LPR, pp = pos & 15, r = pp % RPW, i = pp / RPW;
+  return granule_off(hd, int8, pos, i, r * LPR + (d >> 3), d & 7);
+}
+
+// Offset of element (pos, d) inside one (layer, kv head) K array.
+__host__ __device__ inline size_t k_off(const KvGeom& g, int pos, int d) {
+  return g.tiled ? k_off_tiled(g.hd, g.int8, pos, d) : static_cast<size_t>(pos) * g.hd + d;
 }
 
 // Offset of element (pos, d) inside one (layer, kv head) V array.
 __host__ __device__ inline size_t v_off(const KvGeom& g, int pos, int d) {
-  if (!g.tiled) return static_cast<size_t>(pos) * g.hd + d;
-  const int LPR = g.hd >> 3, RPW = 64 / LPR, pp = pos & 15, r = pp % RPW, i = pp / RPW;
-  return granule_off(g.hd, g.int8, pos, i, r * LPR + (d >> 3), d & 7);
+  return g.tiled ? v_off_tiled(g.hd, g.int8, pos, d) : static_cast<size_t>(pos) * g.hd + d;
 }
 
 // Elements of one (layer, kv head) K or V array.
@@ -122,6 +129,12 @@ struct AttnCall {
   const float* q;  // device [rows][n_heads][hd]
   float* out;      // device [rows][n_heads][hd]
   RingView ring;
+  // fused decode step: append this row (device [nkv*hd] each) at position
+  // app_pos, storage row app_slot, before attending; app_slot < 0: none
+  const float* app_k = nullptr;
+  const float* app_v = nullptr;
+  int app_slot = -1;
+  int app_pos = 0;
 };
 
 // Launchers (return a hipError_t of the launch).

@@ -41,10 +41,10 @@ bool decode_attention(KVCache& kv, const Config& cfg, std::size_t layer, std::in
     rope(q, &pos, cfg.rope_theta, cfg.n_heads, 1, cfg.head_dim);
     rope(k, &pos, cfg.rope_theta, cfg.n_kv_heads, 1, cfg.head_dim);
   }
-  kv.append(layer, p, k, v);
   if (!kv.ok()) return false;
-  return kv.check(dbi_attn_decode(kv.handle(), l, p, static_cast<std::uint32_t>(cfg.n_heads),
-                                  attn_scale(cfg), q, attn_out));
+  // kv.append + attend in one launch (dbi_kv_decode)
+  return kv.check(dbi_kv_decode(kv.handle(), l, p, k, v, static_cast<std::uint32_t>(cfg.n_heads),
+                                attn_scale(cfg), q, attn_out));
 }
 
 bool chunk_attention(KVCache& kv, const Config& cfg, std::size_t layer, std::int32_t pos0,

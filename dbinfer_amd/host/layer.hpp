@@ -55,9 +55,10 @@ void rope(float* x, const std::int32_t* positions, float theta, std::size_t n_he
 
 // The attention half of decode_layer (model.cpp:757-771): dense caches rope q
 // and k at pos, append, then attend; a ring appends un-roped k and the device
-// ropes q and every resident key (attend_ring, model.cpp:662-700). q and k
-// are modified in place for dense caches like the reference's q_/k_.
-// attn_out is [n_heads*head_dim]. Returns false on a device error.
+// ropes q and every resident key (attend_ring, model.cpp:662-700). The append
+// and the attention run as one fused launch (dbi_kv_decode). q and k are
+// modified in place for dense caches like the reference's q_/k_. attn_out is
+// [n_heads*head_dim]. Returns false on a device error.
 bool decode_attention(KVCache& kv, const Config& cfg, std::size_t layer, std::int32_t pos,
                       float* q, float* k, const float* v, float* attn_out);
 

@@ -153,6 +153,21 @@ class HipKV:
         _check(self._lib, self._lib.dbi_attn_decode_async(self._h, layer, pos, n_heads, scale,
                                                           q_dev, out_dev))
 
+    def decode(self, layer: int, pos: int, k, v, q, n_heads: int, scale: float) -> np.ndarray:
+        """Fused append of (k, v) at pos + attention of q at pos (one launch)."""
+        k, v, q = _f32(k), _f32(v), _f32(q)
+        assert k.size == self.pos_stride and v.size == self.pos_stride
+        assert q.size == n_heads * self.head_dim
+        out = np.empty(n_heads * self.head_dim, np.float32)
+        _check(self._lib, self._lib.dbi_kv_decode(self._h, layer, pos, _ptr(k), _ptr(v), n_heads,
+                                                  scale, _ptr(q), _ptr(out)))
+        return out
+
+    def decode_async(self, layer: int, pos: int, k_dev: int, v_dev: int, n_heads: int,
+                     scale: float, q_dev: int, out_dev: int) -> None:
+        _check(self._lib, self._lib.dbi_kv_decode_async(self._h, layer, pos, k_dev, v_dev, n_heads,
+                                                        scale, q_dev, out_dev))
+
     def attend_chunk(self, layer: int, pos0: int, q, n_heads: int, scale: float) -> np.ndarray:
         q = _f32(q)
         n = q.size // (n_heads * self.head_dim)

@@ -123,6 +123,19 @@ dbi_status dbi_attn_decode(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_
 dbi_status dbi_attn_decode_async(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
                                  float scale, const float* q_dev, float* out_dev);
 
+/* One decode step of a layer, fused: KVCache::append of position pos then
+ * the single-query attention at pos, exactly as dbi_kv_append followed by
+ * dbi_attn_decode (the attention half of Model::decode_layer,
+ * model.cpp:759-771). k, v host [n_kv_heads*head_dim] (for dense layouts
+ * already roped, as the reference's k_), q, out host [n_heads*head_dim]. One
+ * kernel launch writes the row and attends; sets n_seen = pos + 1. */
+dbi_status dbi_kv_decode(dbi_kv* kv, uint32_t layer, uint32_t pos, const float* k,
+                         const float* v, uint32_t n_heads, float scale, const float* q,
+                         float* out);
+dbi_status dbi_kv_decode_async(dbi_kv* kv, uint32_t layer, uint32_t pos, const float* k_dev,
+                               const float* v_dev, uint32_t n_heads, float scale,
+                               const float* q_dev, float* out_dev);
+
 /* Causal chunk attention of decode_layer_chunk (model.cpp:956-981): row c of
  * q [n][n_heads][head_dim] attends [0, pos0 + c] and writes row c of out.
  * Every row must have been appended first (model.cpp:933-954). Dense fp32

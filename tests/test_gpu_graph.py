@@ -56,3 +56,69 @@ def test_graph_replay_matches_eager(dtype, n_sink, window):
             kv.attend_async(0, pos, nh, scale, q[1].data_ptr(), other[0].data_ptr())
             torch.cuda.synchronize()
         kv.close()
+
+
+@pytest.mark.parametrize("dtype,n_sink,window,misalign", [
+    (INT8, 4, 0, 0), (F32, 0, 0, 0), (INT8, 4, 64, 0), (F32, 4, 64, 0),
+    (INT8, 4, 0, 1),  # rows 4 bytes off 16-byte alignment: append kernel, then attention
+    (F32, 4, 64, 1),
+])
+def test_fused_step_graph_matches_separate(dtype, n_sink, window, misalign):
+    """The fused decode step (dbi_kv_decode_async, device rows) against the
+    separate append + attention calls bit for bit, eager and over graph
+    replays (the step is idempotent at a fixed position), and the stored
+    arrays equal afterwards."""
+    torch = pytest.importorskip("torch")
+    L, nh, nkv, hd, ctx = 2, 24, 8, 128, 1500
+    P, pos = nkv * hd, ctx - 1
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(11)
+        kflat = torch.randn(L * ctx * P + 1, device="cuda", generator=g)
+        vflat = torch.randn(L * ctx * P + 1, device="cuda", generator=g)
+        K = kflat[misalign:misalign + L * ctx * P].view(L, ctx, P)
+        V = vflat[misalign:misalign + L * ctx * P].view(L, ctx, P)
+        q = torch.randn(L, nh * hd, device="cuda", generator=g)
+        kv = HipKV(L, ctx, nkv, hd, n_sink, window, dtype, 1e6)
+        sep = HipKV(L, ctx, nkv, hd, n_sink, window, dtype, 1e6)
+        for h in (kv, sep):
+            h.set_stream(stream.cuda_stream)
+            for l in range(L):
+                h.append_async(l, 0, pos, K[l].data_ptr(), V[l].data_ptr())
+        out = torch.zeros(L, nh * hd, device="cuda")
+        ref = torch.zeros(L, nh * hd, device="cuda")
+        for l in range(L):
+            sep.append_async(l, pos, 1, K[l, pos].data_ptr(), V[l, pos].data_ptr())
+            sep.attend_async(l, pos, nh, scale, q[l].data_ptr(), ref[l].data_ptr())
+
+        def step():
+            for l in range(L):
+                kv.decode_async(l, pos, K[l, pos].data_ptr(), V[l, pos].data_ptr(), nh, scale,
+                                q[l].data_ptr(), out[l].data_ptr())
+
+        step()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), "eager fused step vs separate calls"
+        graph = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(stream)
+        with torch.cuda.graph(graph, stream=cap):
+            kv.set_stream(cap.cuda_stream)
+            step()
+        kv.set_stream(stream.cuda_stream)
+        torch.cuda.synchronize()
+        for r in range(3):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"replay {r}"
+        names = (["k8", "v8", "k_scale", "v_scale"] + ([] if window else ["k_raw"])
+                 if dtype == INT8 else ["k", "v"])
+        for l in range(L):
+            for n in names:
+                a, b = kv.export(n, l), sep.export(n, l)
+                assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{n} layer {l}"
+        kv.close()
+        sep.close()

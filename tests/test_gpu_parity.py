@@ -183,6 +183,72 @@ def test_decode_ring_stream(dtype, nh, nkv, hd, n_sink, window):
         assert_close(got, want, what=f"ring step {t}")
 
 
+# ---------------------------------------------------------------- fused decode step
+
+
+FUSED_CASES = [
+    # dtype, nh, nkv, hd, n_sink, window, steps
+    (F32, 24, 8, 128, 0, 0, 70),
+    (INT8, 24, 8, 128, 4, 0, 70),     # config 3 shape: sinks, then groups
+    (INT8, 32, 8, 64, 0, 0, 40),
+    (INT8, 28, 4, 128, 37, 0, 45),    # sinks spanning a whole group and more
+    (F32, 32, 4, 64, 0, 0, 33),       # config 1 shape (gqa 8, head groups)
+    (F32, 28, 4, 128, 4, 24, 70),     # config 4 shape ring, wraps twice
+    (INT8, 28, 4, 128, 4, 24, 70),
+    (INT8, 8, 2, 64, 0, 20, 50),
+]
+
+
+@pytest.mark.parametrize("dtype,nh,nkv,hd,n_sink,window,steps", FUSED_CASES)
+def test_fused_decode_step(dtype, nh, nkv, hd, n_sink, window, steps):
+    """dbi_kv_decode (append + attend in one launch) against the oracle's
+    append + attend every step, the separate C-ABI path bit for bit, and the
+    stored arrays bit-exact at the end."""
+    cap = 0 if window else steps + 3
+    g, o = pair(1, cap, nkv, hd, n_sink, window, dtype, 1e6)
+    sep = HipKV(1, cap, nkv, hd, n_sink, window, dtype, 1e6)
+    K = normal(400, steps, nkv * hd)
+    V = normal(401, steps, nkv * hd)
+    if dtype == INT8:
+        K[:, 5] *= 8.0
+    sc = scale_of(hd)
+    for t in range(steps):
+        q = normal(500 + t, nh * hd)
+        got = g.decode(0, t, K[t], V[t], q, nh, sc)
+        sep.append(0, t, K[t], V[t])
+        ref = sep.attend(0, t, q, nh, sc)
+        if window:
+            want = o.attend_ring(0, t, q, K[t], V[t], nh, sc)
+        else:
+            o.append(0, t, K[t], V[t])
+            want = o.attend(0, t, q, nh, sc)
+        assert_close(got, want, what=f"fused step {t}")
+        same_bits(got, ref, f"fused vs separate step {t}")
+    assert g.n_seen == steps
+    if dtype == INT8:
+        names = ["k8", "v8", "k_scale", "v_scale"]
+        if not window:
+            names += ["k_raw"] + (["k_sink", "v_sink"] if n_sink else [])
+    else:
+        names = ["k", "v"]
+    for n in names:
+        same_bits(g.export(n, 0), sep.export(n, 0), f"fused store {n} vs separate")
+    compare_store(g, o, [0], names)
+    sep.close()
+
+
+def test_fused_decode_rejects_bad_input():
+    g = HipKV(1, 16, 2, 64)
+    k = np.zeros(128, np.float32)
+    q = np.zeros(8 * 64, np.float32)
+    with pytest.raises(DbiError):
+        g.decode(0, 16, k, k, q, 8, 0.125)  # past capacity
+    with pytest.raises(DbiError):
+        g.decode(0, 0, k, k, q[: 7 * 64], 7, 0.125)  # n_heads not a multiple of n_kv_heads
+    assert g.n_seen == 0
+    g.close()
+
+
 # ---------------------------------------------------------------- chunk
 
 
