@@ -58,6 +58,7 @@ void free_store(dbi::KvStore& s) {
 
 void free_ws(dbi::Workspace& w) {
   if (w.part) (void)hipFree(w.part);
+  if (w.counters) (void)hipFree(w.counters);
   if (w.staging) (void)hipFree(w.staging);
   w = dbi::Workspace{};
 }
@@ -110,6 +111,21 @@ dbi_status ensure_workspace(dbi_kv* kv, const dbi::AttnCall& c) {
     if (hipMalloc(reinterpret_cast<void**>(&kv->ws.part), part * sizeof(float)) != hipSuccess)
       return fail(DBI_ERR_NOMEM, "attention workspace allocation failed");
     kv->ws.part_floats = part;
+  }
+  // the kernels leave the counters at zero; a fresh array starts there
+  const size_t cnt = dbi::attention_counters_need(kv->geom, c);
+  if (cnt > kv->ws.counters_n) {
+    HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+    if (kv->ws.counters) (void)hipFree(kv->ws.counters);
+    kv->ws.counters = nullptr;
+    kv->ws.counters_n = 0;
+    if (hipMalloc(reinterpret_cast<void**>(&kv->ws.counters), cnt * sizeof(unsigned)) !=
+        hipSuccess)
+      return fail(DBI_ERR_NOMEM, "attention counter allocation failed");
+    HIP_TRY(hipMemsetAsync(kv->ws.counters, 0, cnt * sizeof(unsigned), kv->stream),
+            "counter clear");
+    HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+    kv->ws.counters_n = cnt;
   }
   return DBI_OK;
 }

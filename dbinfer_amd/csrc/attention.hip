@@ -53,6 +53,9 @@ namespace {
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxSplits = 32;
+// split-arrival counters sit 256 bytes apart: the atomics of different
+// (row, kv head) pairs never share a cache line
+constexpr int kCounterStride = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMinit = -1.0e30f;  // finite: exp2(kMinit - kMinit) == 1, no NaN
 
@@ -72,11 +75,13 @@ struct AttnParams {
   const float* q;
   float* out;
   float* part;
+  unsigned* cnt;  // split arrivals per (row, kv head), zero between launches
   int capg, ng, n_sink, nkv, n_heads;
   int rows, pos0;
   int ring_nres, ring_s, ring_W, ring_base;
   int nsplit;  // splits (partial records) per (row, kv head)
-  int direct;  // 1: single split and no sinks, write the output directly
+  int direct;  // 1: single split and no sinks, write the output directly;
+               // 0: write a partial record, the last split to arrive merges
   int chunks_per_split;
   float qscale;
 };
@@ -214,6 +219,26 @@ __device__ __forceinline__ float treduce(const float* a) {
   return t;
 }
 
+// Fused decode step (Model::decode_layer's kv.append then attend,
+// model.cpp:759-771): the row of one position, appended by the workgroup
+// whose split holds its storage chunk (FusedAppend below).
+struct AppendArgs {
+  const float* k;  // new row, device [nkv][hd]; nullptr: no append
+  const float* v;
+  int slot;        // storage row (dense: pos; ring: slot_for(pos)); -1: no append
+  int pos;
+  int nkv, n_sink, capg, ng;
+  float* kf;       // this layer's arrays, writable
+  float* vf;
+  uint8_t* k8;
+  uint8_t* v8;
+  float* ks;
+  float* vs;
+  float* k_raw;    // dense int8 staging [32][nkv*hd]
+  float* ksink;
+  float* vsink;
+};
+
 // Cross-wave combine of (m, l, o) in LDS, then either the final output
 // (single split) or this split's partial record. Head g was handled by the
 // WPG waves of head group g / GW, at their local head index g % GW.
@@ -266,29 +291,115 @@ __device__ __forceinline__ void finish(const AttnParams& P, float (&s_o)[kWaves]
       const int r = idx - G * HD;
       v = r < G ? s_M[r] : s_L[r - G];
     }
-    rec[idx] = v;
+    // written through to the device coherence point (the merging
+    // workgroup may run on another XCD, behind another L2)
+    __hip_atomic_store(rec + idx, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
-// Fused decode step (Model::decode_layer's kv.append then attend,
-// model.cpp:759-771): the row of one position, written by the workgroup
-// whose split holds its storage chunk, before that chunk is read.
-struct AppendArgs {
-  const float* k;  // new row, device [nkv][hd]; nullptr: no append
-  const float* v;
-  int slot;        // storage row (dense: pos; ring: slot_for(pos)); -1: no append
-  int pos;
-  int nkv, n_sink, capg, ng;
-  float* kf;       // this layer's arrays, writable
-  float* vf;
-  uint8_t* k8;
-  uint8_t* v8;
-  float* ks;
-  float* vs;
-  float* k_raw;    // dense int8 staging [32][nkv*hd]
-  float* ksink;
-  float* vsink;
-};
+// The split merge of one (row, kv head), run by the workgroup whose split
+// arrived last (each split counts itself in P.cnt after its record stores
+// completed; the last one resets the count for the next launch). Wave g
+// merges query head g: the (m, l) of split s in lane s gives the split
+// weights (DPP max / sum), every lane combines its HD/64 dims of the split
+// records, then the fp32 sink positions, when the layout has them
+// (model.cpp:612-614), are attended as further entries with a running max.
+// Records are read at device coherence.
+template <int HD, int G>
+__device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs& A, int kh,
+                                           int qrow, int wave, int lane) {
+  constexpr int DPL = HD / 64;
+  constexpr int kSinkBatch = 8;
+  constexpr int kSC1 = 16;  // cache policy: agent-coherent load
+  if (wave >= G) return;
+  const int g = wave;
+  const int rec_floats = G * (HD + 2);
+  const size_t head_base = static_cast<size_t>(qrow) * P.nkv + kh;
+  const rsrc_t rr = make_rsrc(P.part + head_base * P.nsplit * rec_floats,
+                              P.nsplit * rec_floats * 4);
+  auto ld = [&](int idx) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, idx * 4, 0, kSC1));
+  };
+  // every load of the merge in one round: (m, l) of split `lane`, this
+  // lane's dims of every split (clamped, surplus splits weighted 0), q and
+  // the first sink rows
+  const bool on = lane < P.nsplit;
+  const int r0 = min(lane, P.nsplit - 1) * rec_floats;
+  const float m = ld(r0 + G * HD + g);
+  const float l = ld(r0 + G * HD + G + g);
+  float ov[kMaxSplits][DPL];
+#pragma unroll
+  for (int sp = 0; sp < kMaxSplits; ++sp)
+#pragma unroll
+    for (int e = 0; e < DPL; ++e)
+      ov[sp][e] = ld(min(sp, P.nsplit - 1) * rec_floats + g * HD + lane * DPL + e);
+  const int ns = min(P.n_sink, P.pos0 + qrow + 1);
+  const size_t h = static_cast<size_t>(qrow) * P.n_heads + kh * G + g;
+  float qd[DPL], kd[kSinkBatch][DPL], vd[kSinkBatch][DPL];
+  // sink row p; a fused step's own sink row is flushed after this merge,
+  // so that one comes from the step's inputs
+  auto sink_rows = [&](int p0) {
+#pragma unroll
+    for (int b = 0; b < kSinkBatch; ++b) {
+      const int p = min(p0 + b, ns - 1);
+      const bool fresh = A.slot >= 0 && p == A.pos;
+      const size_t at = (static_cast<size_t>(kh) * P.n_sink + p) * HD + lane * DPL;
+      const float* kr = fresh ? A.k + kh * HD + lane * DPL : P.ksink + at;
+      const float* vr = fresh ? A.v + kh * HD + lane * DPL : P.vsink + at;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        kd[b][e] = kr[e];
+        vd[b][e] = vr[e];
+      }
+    }
+  };
+  if (ns > 0) {
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) qd[e] = P.q[h * HD + lane * DPL + e] * P.qscale;
+    sink_rows(0);
+  }
+
+  float M = wave_max(on ? m : kMinit);
+  const float w = on ? fast_exp2(m - M) : 0.0f;
+  float L = wave_sum(on ? l * w : 0.0f);
+  float O[DPL] = {};
+#pragma unroll
+  for (int sp = 0; sp < kMaxSplits; ++sp) {
+    const float ws =
+        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), sp));
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) O[e] += ws * ov[sp][e];
+  }
+  // sinks as further entries, a batch at a time with a running max
+  for (int p0 = 0; p0 < ns; p0 += kSinkBatch) {
+    if (p0 > 0) sink_rows(p0);
+    float sc[kSinkBatch];
+    float bm = M;
+#pragma unroll
+    for (int b = 0; b < kSinkBatch; ++b) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) dot += qd[e] * kd[b][e];
+      sc[b] = p0 + b < ns ? wave_sum(dot) : -INFINITY;
+      bm = fmaxf(bm, sc[b]);
+    }
+    const float f = fast_exp2(M - bm);
+    M = bm;
+    L *= f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) O[e] *= f;
+#pragma unroll
+    for (int b = 0; b < kSinkBatch; ++b) {
+      const float ws = fast_exp2(sc[b] - M);
+      L += ws;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) O[e] += ws * vd[b][e];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) P.out[h * HD + lane * DPL + e] = O[e] / L;
+}
+
 
 // LDS stage of a fused step's new values, in the layouts the attention
 // reads them in, for the wave that processes the appended chunk.
@@ -553,6 +664,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
   __shared__ float s_f[G][WPG];
   __shared__ float s_M[G];
   __shared__ float s_L[G];
+  __shared__ int s_last;
   __shared__ __align__(16) float s_w[kWaves][CHUNK][GP];
   __shared__ __align__(16) AppStage s_stage[C::NHG];
   // dense int8 keeps each wave's scaled q in LDS, not registers, between
@@ -1052,111 +1164,22 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
     }
   }
   finish<HD, G, GW, WPG>(P, s_o, s_ml, s_f, s_M, s_L, split, kh, qrow);
+  if (!P.direct) {
+    // this thread's record stores have reached the coherence point
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned* cnt = P.cnt + (static_cast<size_t>(qrow) * P.nkv + kh) * kCounterStride;
+      const unsigned before =
+          __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = before == static_cast<unsigned>(P.nsplit - 1);
+      if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (s_last) merge_last<HD, G>(P, A, kh, qrow, wave, lane);
+  }
   if (app_owner && g0 == 0) App::flush(A, kh, lane, s_app, s_kg, app_row);
-}
-
-// fp32 sinks of the dense int8 cache (model.cpp:623-626, 640-644), folded
-// into the merge as one more split.
-struct SinkArgs {
-  const float* q;      // [rows][n_heads][hd]
-  const float* ksink;  // this layer's [nkv][n_sink][hd]
-  const float* vsink;
-  int n_sink;          // 0: no sinks
-  int pos0;            // row r attends keys [0, pos0 + r]
-  float qscale;
-};
-
-constexpr int kSinkBatch = 8;
-
-// Combines the split partials of one (row, query head), one thread per
-// output dim. All loads go out in one round: every thread's o[d] of each
-// split (indices clamped, surplus splits weighted 0), wave 0's lanes the
-// (m, l) of one split each, and the first sink rows. Wave 0 turns the
-// (m, l) into split weights (DPP max / sum); the sink positions, when the
-// layout has them, are attended here in batches as further entries.
-template <int HD>
-__global__ __launch_bounds__(HD) void merge_kernel(const float* __restrict__ part,
-                                                   float* __restrict__ out, int nkv, int G,
-                                                   int nsplit, int n_heads, SinkArgs sa) {
-  constexpr int NW = HD / 64;
-  __shared__ float s_w[kMaxSplits];
-  __shared__ float s_dot[kSinkBatch][NW];
-  __shared__ float s_M, s_L;
-  const int h = blockIdx.x;
-  const int row = blockIdx.y;
-  const int kh = h / G, g = h % G;
-  const int d = threadIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int rec_floats = G * (HD + 2);
-  const float* recs = part + ((static_cast<size_t>(row) * nkv + kh) * nsplit) * rec_floats;
-  float ov[kMaxSplits];
-#pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp)
-    ov[sp] = recs[static_cast<size_t>(min(sp, nsplit - 1)) * rec_floats + g * HD + d];
-  const int ns = min(sa.n_sink, sa.pos0 + row + 1);
-  const float qd =
-      ns > 0 ? sa.q[(static_cast<size_t>(row) * n_heads + h) * HD + d] * sa.qscale : 0.0f;
-  float kd[kSinkBatch], vd[kSinkBatch];
-  auto load_sinks = [&](int p0) {
-#pragma unroll
-    for (int b = 0; b < kSinkBatch; ++b) {
-      const size_t at = (static_cast<size_t>(kh) * sa.n_sink + min(p0 + b, ns - 1)) * HD + d;
-      kd[b] = sa.ksink[at];
-      vd[b] = sa.vsink[at];
-    }
-  };
-  if (ns > 0) load_sinks(0);
-
-  if (wave == 0) {
-    const bool on = lane < nsplit;
-    const float* r = recs + static_cast<size_t>(min(lane, nsplit - 1)) * rec_floats;
-    const float m = on ? r[G * HD + g] : kMinit;
-    const float l = on ? r[G * HD + G + g] : 0.0f;
-    const float M = wave_max(m);
-    const float w = on ? fast_exp2(m - M) : 0.0f;
-    const float L = wave_sum(l * w);
-    if (lane < kMaxSplits) s_w[lane] = w;
-    if (lane == 0) {
-      s_M = M;
-      s_L = L;
-    }
-  }
-  __syncthreads();
-  float M = s_M, L = s_L, O = 0.0f;
-#pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp) O += s_w[sp] * ov[sp];
-
-  for (int p0 = 0; p0 < ns; p0 += kSinkBatch) {
-    if (p0 > 0) load_sinks(p0);
-#pragma unroll
-    for (int b = 0; b < kSinkBatch; ++b) {
-      const float t = wave_sum(qd * kd[b]);
-      if (lane == 0) s_dot[b][wave] = t;
-    }
-    __syncthreads();
-    float sc[kSinkBatch];
-    float bm = M;
-#pragma unroll
-    for (int b = 0; b < kSinkBatch; ++b) {
-      float t = 0.0f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) t += s_dot[b][w];
-      sc[b] = p0 + b < ns ? t : -INFINITY;
-      bm = fmaxf(bm, sc[b]);
-    }
-    const float scale = fast_exp2(M - bm);
-    M = bm;
-    L *= scale;
-    O *= scale;
-#pragma unroll
-    for (int b = 0; b < kSinkBatch; ++b) {
-      const float w = fast_exp2(sc[b] - M);
-      L += w;
-      O += w * vd[b];
-    }
-    __syncthreads();
-  }
-  out[(static_cast<size_t>(row) * n_heads + h) * HD + d] = O / L;
 }
 
 // ---------------------------------------------------------------------------
@@ -1249,6 +1272,10 @@ bool attention_supported(const KvGeom& g, int n_heads) {
   return pick_kernel(g.hd, kind_of(g), n_heads / g.nkv) != nullptr;
 }
 
+size_t attention_counters_need(const KvGeom& g, const AttnCall& c) {
+  return plan(g, c).merge ? static_cast<size_t>(c.rows) * g.nkv * kCounterStride : 0;
+}
+
 size_t attention_workspace_need(const KvGeom& g, const AttnCall& c) {
   const Plan p = plan(g, c);
   const int G = c.n_heads / g.nkv;
@@ -1285,6 +1312,7 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
   p.q = c.q;
   p.out = c.out;
   p.part = ws.part;
+  p.cnt = ws.counters;
   p.capg = g.capg;
   p.ng = g.ngroups;
   p.n_sink = g.int8 && !g.ring ? g.n_sink : 0;
@@ -1332,16 +1360,7 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
     }
   }
   void* args[] = {&p, &a};
-  hipError_t e = hipLaunchKernel(fn, dim3(p.nsplit, g.nkv, c.rows), dim3(kThreads), args, 0, st);
-  if (e != hipSuccess || !pl.merge) return e;
-  SinkArgs sa{c.q, p.ksink, p.vsink, p.ksink != nullptr ? g.n_sink : 0, c.pos0, p.qscale};
-  if (g.hd == 64)
-    hipLaunchKernelGGL(merge_kernel<64>, dim3(c.n_heads, c.rows), dim3(64), 0, st, ws.part, c.out,
-                       g.nkv, G, p.nsplit, c.n_heads, sa);
-  else
-    hipLaunchKernelGGL(merge_kernel<128>, dim3(c.n_heads, c.rows), dim3(128), 0, st, ws.part,
-                       c.out, g.nkv, G, p.nsplit, c.n_heads, sa);
-  return hipGetLastError();
+  return hipLaunchKernel(fn, dim3(p.nsplit, g.nkv, c.rows), dim3(kThreads), args, 0, st);
 }
 
 }  // namespace dbi

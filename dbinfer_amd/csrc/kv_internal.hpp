@@ -107,6 +107,8 @@ struct KvStore {
 struct Workspace {
   float* part = nullptr;
   size_t part_floats = 0;
+  unsigned* counters = nullptr;  // split arrivals per (row, kv head); zero between launches
+  size_t counters_n = 0;
   float* staging = nullptr;  // device staging for host-pointer calls
   size_t staging_floats = 0;
 };
@@ -145,6 +147,7 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws,
                             const AttnCall& c, hipStream_t st);
 // Number of partial floats one call needs (for workspace sizing).
 size_t attention_workspace_need(const KvGeom& g, const AttnCall& c);
+size_t attention_counters_need(const KvGeom& g, const AttnCall& c);
 bool attention_supported(const KvGeom& g, int n_heads);
 
 // Prefix pack/unpack between [L][len][nkv][hd] and the head-major store
