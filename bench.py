@@ -6,9 +6,10 @@ attention shape of config 3 -- 28 layers, 24 query / 8 kv heads, head_dim
 per-block V, 4 fp32 sinks) holding 8192 positions of synthetic N(0,1) keys
 and values with 1% outlier channels x8. One step decodes one token through
 all 28 layers: per layer, quantize-on-append at position 8191 then GQA decode
-attention over the 8192 resident keys (dbi_kv_decode: one fused kernel plus
-its split merge). Inputs (q, k, v) are resident in HBM before the timed
-region; the step is replayed from a HIP graph.
+attention over the 8192 resident keys (dbi_kv_decode: one kernel, split-K
+over the keys, the last split to finish merges). Inputs (q, k, v) are
+resident in HBM before the timed region; the step is replayed from a HIP
+graph.
 
 The same step over the fp32 cache of that shape (the reference point of
 BASELINE.md) is reported beside it. The working sets (529 MB int8, 1.9 GB
@@ -75,7 +76,7 @@ def build_cache(torch, HipKV, dtype_code, K, V):
 
 def step(kv, K, V, q, out, scale, attention_only=False):
     """One decode token through all layers: per layer the fused decode step
-    (quantize-on-append at POS + attention, one kernel and its split merge);
+    (quantize-on-append at POS + attention, one kernel);
     attention_only leaves the cache as it is and times the attention call."""
     for layer in range(L):
         if attention_only:
@@ -315,7 +316,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_kernel<HD=128,G=3,EPL=8,int8 dense> + merge_kernel<128> "
+            "kernel": "attn_kernel<hd 128, gqa 3, int8 dense> "
                       "(one decode-attention call)",
             "achieved": round(achieved, 2),
             "peak": PEAK_GBS,
