@@ -298,6 +298,9 @@ dbi_status dbi_kv_create(const dbi_kv_config* cfg, dbi_kv** out) {
     if (e == hipSuccess)
       e = hipMemcpy(s.rope_cs, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice);
   }
+  // the fills above run on the null stream, which a non-blocking stream does
+  // not wait for: finish them before any work can reach the arrays
+  if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&kv->own_stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     free_store(s);

@@ -122,3 +122,38 @@ def test_fused_step_graph_matches_separate(dtype, n_sink, window, misalign):
                 assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{n} layer {l}"
         kv.close()
         sep.close()
+
+
+@pytest.mark.parametrize("dtype", [INT8, F32])
+def test_split_merge_is_stable_under_load(dtype):
+    """The split merge runs in the last workgroup to arrive, reading the other
+    splits' records at device coherence. The merge order is fixed, so every
+    call must give the same bits whichever workgroup merges: 60 back-to-back
+    rounds over 28 layers at the config-3 shape (256 workgroups per call, the
+    full-load case) all equal the first round."""
+    torch = pytest.importorskip("torch")
+    L, nh, nkv, hd, ctx = 28, 24, 8, 128, 4096
+    pos = ctx - 1
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(21)
+        K = torch.randn(ctx, nkv * hd, device="cuda", generator=g)
+        V = torch.randn(ctx, nkv * hd, device="cuda", generator=g)
+        q = torch.randn(L, nh * hd, device="cuda", generator=g)
+        kv = HipKV(L, ctx, nkv, hd, 4 if dtype == INT8 else 0, 0, dtype, 1e6)
+        kv.set_stream(stream.cuda_stream)
+        for l in range(L):
+            kv.append_async(l, 0, ctx, K.data_ptr(), V.data_ptr())
+        rounds = 60
+        out = torch.zeros(rounds, L, nh * hd, device="cuda")
+        for r in range(rounds):
+            for l in range(L):
+                kv.attend_async(l, pos, nh, scale, q[l].data_ptr(), out[r, l].data_ptr())
+        torch.cuda.synchronize()
+        first = out[0]
+        assert torch.isfinite(first).all()
+        bad = [r for r in range(1, rounds) if not torch.equal(out[r], first)]
+        assert not bad, f"rounds differing from the first: {bad[:10]}"
+        kv.close()
