@@ -24,18 +24,21 @@
 //    of one position row).
 //  - Loads: K of the next chunk is issued right after QK, V of the next
 //    chunk right after PV, so one of them is always in flight.
-//  - Split-K: each split writes (o[G][HD], m[G], l[G]) of its range; a small
-//    merge kernel, the next launch on the stream, combines the splits of every
-//    (row, query head) and writes out = o / l. The kernel boundary is the
-//    release/acquire: inside one kernel, making one workgroup's stores visible
-//    to another across the per-XCD L2 caches takes an agent-scope fence (a
-//    whole-L2 writeback) per workgroup.
+//  - Split-K: each split writes (o[G][HD], m[G], l[G]) of its range with
+//    agent-coherent stores, waits for them, and counts itself in a per
+//    (row, kv head) counter with one device-scope atomic. The split that
+//    arrives last merges every split (and the sinks) and resets the counter,
+//    so no second launch, no fence (an agent-scope fence is a whole-L2
+//    writeback on this multi-XCD part) and no memset between launches.
 //  - int8 dense: a 32-position chunk is exactly one K group, so the
 //    per-channel K scale folds into q once per chunk (the reference's
 //    (q_i * ks_i) * k8_i); codes are stored biased (+128) and converted with
 //    one v_cvt_f32_ubyteN each, the bias removed through -128 * sum(q*ks) (K)
 //    and -128 * sum(w*vs) (V). The fp32 sinks (pos < n_sink) are attended
-//    by the merge kernel as one more split.
+//    in the merge as further entries.
+//  - Fused decode step (dbi_kv_decode): the append of the new row runs
+//    inside the launch (FusedAppend), staged in LDS for the wave that
+//    attends its chunk.
 //  - ring: keys are stored un-roped; each resident key is dequantized (int8:
 //    per-block scale) and roped at its cache-relative position from an fp32
 //    cos/sin table, q at n_res - 1 (model.cpp:662-700). K lanes hold dims d
