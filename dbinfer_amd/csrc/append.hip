@@ -80,56 +80,71 @@ __global__ __launch_bounds__(kThreads) void append_i8_ring_kernel(KvGeom g, KvSt
   }
 }
 
-// Dense int8 (model.cpp:358-384). Blocks [0, n_kblocks) run the key side, one
-// thread per channel c of [0, n_kv*hd): for every 32-token group the batch
-// touches, in order, stage the group's new rows into k_raw[pos % 32] and
-// requantize the group over raw rows [0, within] that are not sinks
-// (requantize_kgroup, model.cpp:329-355). Each channel only ever reads and
-// writes its own column of k_raw, k_scale and k8, so threads never interact.
-// The remaining blocks run the value side, one lane per element, 32 lanes per
-// (row, kv head, block): fp32 sink copy for pos < n_sink, else quant_head of V.
-__global__ __launch_bounds__(kThreads) void append_i8_dense_kernel(KvGeom g, KvStore s, int layer,
-                                                                   int pos0, int n, int n_kblocks,
-                                                                   const float* __restrict__ k,
-                                                                   const float* __restrict__ v) {
+// Dense int8 key side (model.cpp:358-384, requantize_kgroup :329-355) of a
+// batch [pos0, pos0 + n): one thread per (32-token group, channel). The
+// result is that of n sequential appends: a group ends requantized over its
+// raw rows [0, within] that are not sinks, with within the batch's last row
+// in the group. Those rows come from the batch, or, before pos0 in the first
+// group, from the staging rows k_raw left by earlier appends (which keeps the
+// reference's staging-row aliasing after a rollback). Groups are
+// independent; the staging rows are rewritten afterwards
+// (append_i8_kraw_kernel), so every reader here sees them as they were.
+__global__ __launch_bounds__(kThreads) void append_i8_kgroup_kernel(KvGeom g, KvStore s, int layer,
+                                                                    int pos0, int n,
+                                                                    const float* __restrict__ k) {
   const int P = g.nkv * g.hd;
-  if (static_cast<int>(blockIdx.x) < n_kblocks) {
-    const int c = blockIdx.x * kThreads + threadIdx.x;
-    if (c >= P) return;
-    const int kh = c / g.hd, i = c % g.hd;
-    float* raw = s.k_raw + static_cast<size_t>(layer) * kKGroup * P + c;
-    const size_t head = static_cast<size_t>(layer) * g.nkv + kh;
-    const int end = pos0 + n;
-    int p = pos0;
-    while (p < end) {
-      const int grp = p / kKGroup;
-      const int first = grp * kKGroup;
-      const int hi = min(end - 1, first + kKGroup - 1);
-      for (int q = p; q <= hi; ++q)
-        raw[static_cast<size_t>(q % kKGroup) * P] = k[static_cast<size_t>(q - pos0) * P + c];
-      const int within = hi - first;
-      // all 32 staging rows in flight at once (rows past `within` are unused)
-      float rv[kKGroup];
+  const int c = blockIdx.x * kThreads + threadIdx.x;
+  if (c >= P) return;
+  const int kh = c / g.hd, i = c % g.hd;
+  const int grp = pos0 / kKGroup + static_cast<int>(blockIdx.y);
+  const int first = grp * kKGroup, end = pos0 + n;
+  const int within = min(end - 1, first + kKGroup - 1) - first;
+  const float* raw = s.k_raw + static_cast<size_t>(layer) * kKGroup * P + c;
+  const size_t head = static_cast<size_t>(layer) * g.nkv + kh;
+  float x[kKGroup];
+  float mx = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kKGroup; ++w) rv[w] = raw[static_cast<size_t>(w) * P];
-      float mx = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kKGroup; ++w)
-        if (w <= within && first + w >= g.n_sink) mx = max_f(mx, fabsf(rv[w]));
-      const float sc = mx / 127.0f;
-      s.k_scale[(head * g.ngroups + grp) * g.hd + i] = sc;
-      const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
-#pragma unroll
-      for (int w = 0; w < kKGroup; ++w)
-        if (w <= within && first + w >= g.n_sink)
-          s.k8[head * head_elems(g) + k_off(g, first + w, i)] = biased(quant_code(rv[w], inv));
-      p = hi + 1;
-    }
-    return;
+  for (int w = 0; w < kKGroup; ++w) {
+    const int p = first + w;  // uniform over the block
+    x[w] = w > within ? 0.0f
+                      : (p >= pos0 ? k[static_cast<size_t>(p - pos0) * P + c]
+                                   : raw[static_cast<size_t>(w) * P]);
+    if (w <= within && p >= g.n_sink) mx = max_f(mx, fabsf(x[w]));
   }
+  const float sc = mx / 127.0f;
+  s.k_scale[(head * g.ngroups + grp) * g.hd + i] = sc;
+  const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
+#pragma unroll
+  for (int w = 0; w < kKGroup; ++w)
+    if (w <= within && first + w >= g.n_sink)
+      s.k8[head * head_elems(g) + k_off(g, first + w, i)] = biased(quant_code(x[w], inv));
+}
+
+// The staging rows after the batch: k_raw[w] holds the batch's last row p
+// with p % 32 == w (n sequential appends each copy k into k_raw[p % 32]).
+__global__ __launch_bounds__(kThreads) void append_i8_kraw_kernel(KvGeom g, KvStore s, int layer,
+                                                                  int pos0, int n,
+                                                                  const float* __restrict__ k) {
+  const int P = g.nkv * g.hd;
+  const size_t idx = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x;
+  if (idx >= static_cast<size_t>(kKGroup) * P) return;
+  const int w = static_cast<int>(idx / P), c = static_cast<int>(idx % P);
+  const int last = pos0 + n - 1;
+  const int p = last - (((last - w) % kKGroup) + kKGroup) % kKGroup;
+  if (p >= pos0)
+    s.k_raw[static_cast<size_t>(layer) * kKGroup * P + idx] = k[static_cast<size_t>(p - pos0) * P + c];
+}
+
+// Dense int8 value side (model.cpp:366-384), one lane per element, 32 lanes
+// per (row, kv head, block): fp32 sink copy of K and V for pos < n_sink, else
+// quant_head of V.
+__global__ __launch_bounds__(kThreads) void append_i8_dense_v_kernel(KvGeom g, KvStore s, int layer,
+                                                                     int pos0, int n,
+                                                                     const float* __restrict__ k,
+                                                                     const float* __restrict__ v) {
+  const int P = g.nkv * g.hd;
   const size_t blocks = static_cast<size_t>(n) * g.nkv * g.nb;
-  const size_t bidx =
-      ((blockIdx.x - n_kblocks) * static_cast<size_t>(kThreads) + threadIdx.x) / kBlock;
+  const size_t bidx = (blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x) / kBlock;
   const int t = threadIdx.x % kBlock;
   if (bidx >= blocks) return;  // whole 32-lane groups leave together
   const int b = static_cast<int>(bidx % g.nb);
@@ -197,11 +212,16 @@ hipError_t launch_append(const KvGeom& g, const KvStore& s, int layer, int pos0,
     hipLaunchKernelGGL(append_i8_ring_kernel, dim3((lanes + kThreads - 1) / kThreads),
                        dim3(kThreads), 0, st, g, s, layer, pos0, n, k, v);
   } else {
-    const int n_kblocks = static_cast<int>((P + kThreads - 1) / kThreads);
+    const int n_groups = (pos0 + n - 1) / kKGroup - pos0 / kKGroup + 1;
+    if (n_groups > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(append_i8_kgroup_kernel,
+                       dim3(static_cast<unsigned>((P + kThreads - 1) / kThreads), n_groups),
+                       dim3(kThreads), 0, st, g, s, layer, pos0, n, k);
+    hipLaunchKernelGGL(append_i8_kraw_kernel, dim3(grid_for(kKGroup * P)), dim3(kThreads), 0, st, g,
+                       s, layer, pos0, n, k);
     const size_t vwork = static_cast<size_t>(n) * g.nkv * g.nb * kBlock;
-    const int n_vblocks = static_cast<int>((vwork + kThreads - 1) / kThreads);
-    hipLaunchKernelGGL(append_i8_dense_kernel, dim3(n_kblocks + n_vblocks), dim3(kThreads), 0, st,
-                       g, s, layer, pos0, n, n_kblocks, k, v);
+    hipLaunchKernelGGL(append_i8_dense_v_kernel, dim3((vwork + kThreads - 1) / kThreads),
+                       dim3(kThreads), 0, st, g, s, layer, pos0, n, k, v);
   }
   return hipGetLastError();
 }

@@ -80,10 +80,13 @@ def test_append_int8_dense_bit_exact(hd, nkv, n_sink):
         compare_store(g, o, [l], names)
 
 
-def test_int8_rollback_across_group_boundary():
+@pytest.mark.parametrize("n_new", [5, 50, 97])
+def test_int8_rollback_across_group_boundary(n_new):
     """Rollback then re-append: the staging-row aliasing of the reference
-    (k_raw indexed by pos % 32) is reproduced bit for bit."""
-    L, cap, nkv, hd = 1, 96, 2, 64
+    (k_raw indexed by pos % 32) is reproduced bit for bit. A batch longer
+    than a group also overwrites staging rows that its first group still
+    reads as they were."""
+    L, cap, nkv, hd = 1, 160, 2, 64
     g, o = pair(L, cap, nkv, hd, n_sink=4, dtype=INT8)
     P = nkv * hd
     K, V = normal(5, 80, P), normal(6, 80, P)
@@ -93,11 +96,29 @@ def test_int8_rollback_across_group_boundary():
     for kv in (g, o):
         kv.truncate(30)
     assert g.n_seen == o.n_seen == 30
-    knew, vnew = normal(7, 5, P), normal(8, 5, P)
+    knew, vnew = normal(7, n_new, P), normal(8, n_new, P)
     g.append_n(0, 30, knew, vnew)  # crosses back into group 1
-    for r in range(5):
+    for r in range(n_new):
         o.append(0, 30 + r, knew[r], vnew[r])
     compare_store(g, o, [0], INT8_DENSE + ["k_sink", "v_sink"])
+
+
+def test_int8_bulk_append_matches_sequential():
+    """One batch of 1000 rows from a group boundary and one from mid-group
+    against the oracle's row-by-row appends (31 groups requantized at once)."""
+    L, cap, nkv, hd = 1, 2100, 4, 128
+    P = nkv * hd
+    K, V = normal(9, 2048, P), normal(10, 2048, P)
+    K[:, 11] *= 8.0
+    for start in (0, 1037):
+        g, o = pair(L, cap, nkv, hd, n_sink=4, dtype=INT8)
+        if start:
+            g.append_n(0, 0, K[:start], V[:start])
+            o.append_n(0, 0, K[:start], V[:start])
+        g.append_n(0, start, K[start:start + 1000], V[start:start + 1000])
+        for r in range(start, start + 1000):
+            o.append(0, r, K[r], V[r])
+        compare_store(g, o, [0], INT8_DENSE + ["k_sink", "v_sink"])
 
 
 @pytest.mark.parametrize("dtype", [F32, INT8])
