@@ -230,6 +230,104 @@ def _profiled_traffic():
     return None
 
 
+# SURVEY 8(d) workloads, one decode step (and, where the config has them, the
+# prefill chunk / verify round) per config; bench.py --configs
+CONFIGS = [
+    # name, layers, nh, nkv, hd, dtype, n_sink, window, position decoded, chunk rows
+    ("C1 TinyLlama", 22, 32, 4, 64, "f32", 0, 0, 1024, 0),
+    ("C2 Llama-3.2-1B", 16, 32, 8, 64, "f32", 0, 0, 4095, 256),
+    ("C3 Llama-3.2-3B int8", 28, 24, 8, 128, "int8", 4, 0, 8191, 0),
+    ("C3 Llama-3.2-3B fp32", 28, 24, 8, 128, "f32", 0, 0, 8191, 0),
+    ("C4 Qwen2.5-7B ring fp32", 28, 28, 4, 128, "f32", 4, 4096, 32767, 0),
+    ("C4 Qwen2.5-7B ring int8", 28, 28, 4, 128, "int8", 4, 4096, 32767, 0),
+    ("C5 Qwen3-8B fp32", 36, 32, 8, 128, "f32", 0, 0, 16383, 5),
+    ("C5 Qwen3-8B int8", 36, 32, 8, 128, "int8", 4, 0, 16383, 5),
+]
+
+
+def config_bytes(dtype, nkv, hd, n, s, ring):
+    """Algorithmic HBM bytes of one decode-attention call (n keys or
+    residents, s fp32 sinks of the dense int8 layout)."""
+    P = nkv * hd
+    nb = (hd + 31) // 32
+    if dtype == "f32":
+        return 2 * n * P * 4
+    if ring:
+        return 2 * n * P + 2 * n * nkv * nb * 4
+    return 2 * (n - s) * P + -(-n // 32) * P * 4 + (n - s) * nkv * nb * 4 + 2 * s * P * 4
+
+
+def run_configs(torch, HipKV, F32, INT8, args):
+    """One JSON line per config: the fused decode step per layer (graph
+    replay), its algorithmic GB/s, and the chunk rows of C2 (the last 256-row
+    prefill chunk of the 2048-token prompt) and C5 (a 5-row verify round)."""
+    for (name, L_, nh, nkv, hd, dt, ns, win, pos, rows) in CONFIGS:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+        P = nkv * hd
+        n_fill = pos + 1 if not win else pos + 1
+        stream = torch.cuda.Stream()
+        res = {"config": name, "layers": L_, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd,
+               "kv": dt + (" ring %d+%d" % (ns, win) if win else (" dense, %d sinks" % ns if ns
+                                                                   else " dense"))}
+        with torch.cuda.stream(stream):
+            g = torch.Generator(device="cuda")
+            g.manual_seed(77)
+            K = torch.randn(n_fill, P, device="cuda", generator=g)
+            V = torch.randn(n_fill, P, device="cuda", generator=g)
+            q = torch.randn(L_, max(rows, 1) * nh * hd, device="cuda", generator=g)
+            out = torch.empty_like(q)
+            kv = HipKV(L_, pos + 1 if not win else 1, nkv, hd, ns, win,
+                       INT8 if dt == "int8" else F32, 1e6)
+            kv.set_stream(stream.cuda_stream)
+            for layer in range(L_):
+                kv.append_async(layer, 0, pos, K.data_ptr(), V.data_ptr())
+            torch.cuda.synchronize()
+
+            def step(s_):
+                kv.set_stream(s_.cuda_stream)
+                for layer in range(L_):
+                    kv.decode_async(layer, pos, K[pos].data_ptr(), V[pos].data_ptr(), nh, scale,
+                                    q[layer].data_ptr(), out[layer].data_ptr())
+
+            gr = capture(torch, step)
+            for _ in range(5):
+                gr.replay()
+            ms = time_graph(torch, gr, args.config_steps)
+            n_keys = min(pos + 1, ns + win) if win else pos + 1
+            byts = config_bytes(dt, nkv, hd, n_keys, 0 if win else ns, bool(win))
+            us = 1000.0 * ms / L_
+            res.update({"decode_pos": pos, "keys": n_keys, "us_per_token_layer": round(us, 3),
+                        "bytes_per_call": byts, "GBs": round(byts / (us * 1e-6) / 1e9, 1),
+                        "frac_of_peak": round(byts / (us * 1e-6) / 1e9 / PEAK_GBS, 4),
+                        "working_set_MB": round(L_ * byts / 1e6, 1)})
+            del gr
+            if rows:
+                pos0 = 1792 if rows == 256 else pos + 1 - rows
+                kv.truncate(pos0 + rows)
+
+                def chunk(s_):
+                    kv.set_stream(s_.cuda_stream)
+                    for layer in range(L_):
+                        kv.attend_chunk_async(layer, pos0, rows, nh, scale, q[layer].data_ptr(),
+                                              out[layer].data_ptr())
+
+                gc = capture(torch, chunk)
+                for _ in range(3):
+                    gc.replay()
+                msc = time_graph(torch, gc, max(3, args.config_steps // 4))
+                usc = 1000.0 * msc / L_
+                flops = sum((pos0 + c + 1) * nh * hd * 4 for c in range(rows))
+                res.update({"chunk_rows": rows, "chunk_pos0": pos0,
+                            "chunk_us_per_layer": round(usc, 2),
+                            "chunk_us_per_token_layer": round(usc / rows, 3),
+                            "chunk_TFLOPs": round(flops / (usc * 1e-6) / 1e12, 3)})
+                del gc
+            kv.close()
+            del K, V, q, out
+        torch.cuda.synchronize()
+        print(json.dumps(res), flush=True)
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -247,6 +345,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--configs", action="store_true",
+                    help="instead of the bench line, one JSON line per SURVEY config (C1-C5)")
+    ap.add_argument("--config-steps", type=int, default=30)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (PMC calibration)")
     args = ap.parse_args()
@@ -268,6 +369,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibration_copy_bytes": n * 4, "launches": 5}))
+        return
+    if args.configs:
+        run_configs(torch, HipKV, F32, INT8, args)
         return
     scale = float(np.float32(1.0) / np.sqrt(np.float32(HD)))
     # every launch and event goes on one non-default stream (the kernels'

@@ -101,6 +101,19 @@ dbi::RingView ring_view(const dbi_kv* kv, uint32_t n_seen) {
   return r;
 }
 
+dbi_status ensure_part(dbi_kv* kv, size_t part) {
+  if (part > kv->ws.part_floats) {
+    HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+    if (kv->ws.part) (void)hipFree(kv->ws.part);
+    kv->ws.part = nullptr;
+    kv->ws.part_floats = 0;
+    if (hipMalloc(reinterpret_cast<void**>(&kv->ws.part), part * sizeof(float)) != hipSuccess)
+      return fail(DBI_ERR_NOMEM, "attention workspace allocation failed");
+    kv->ws.part_floats = part;
+  }
+  return DBI_OK;
+}
+
 dbi_status ensure_workspace(dbi_kv* kv, const dbi::AttnCall& c) {
   const size_t part = dbi::attention_workspace_need(kv->geom, c);
   if (part > kv->ws.part_floats) {
@@ -198,6 +211,11 @@ dbi_status chunk_impl(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, uin
   c.q = q_dev;
   c.out = out_dev;
   if (n > 65535) return fail(DBI_ERR_INVALID, "chunk longer than 65535 rows");
+  if (dbi::prefill_supported(kv->geom, static_cast<int>(n_heads), static_cast<int>(n))) {
+    if (dbi_status st = ensure_part(kv, dbi::prefill_workspace_need(kv->geom, c))) return st;
+    HIP_TRY(dbi::launch_prefill(kv->geom, kv->store, kv->ws, c, kv->stream), "prefill launch");
+    return DBI_OK;
+  }
   if (dbi_status st = ensure_workspace(kv, c)) return st;
   HIP_TRY(dbi::launch_attention(kv->geom, kv->store, kv->ws, c, kv->stream), "attention launch");
   return DBI_OK;

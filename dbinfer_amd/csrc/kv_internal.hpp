@@ -12,7 +12,8 @@
 //                       k_raw         [L][32][nkv*hd]     fp32 (reference order)
 //                       k_sink,v_sink [L][nkv][ns][hd]    fp32
 //   ring                rope_cs       [cap][hd/2]         float2 (cos, sin)
-// capg is the capacity rounded up to whole 32-position chunks (two granules).
+// capg is the capacity rounded up to a multiple of 64 positions (the reads of
+// the attention and prefill kernels are whole 32- / 64-position pieces).
 //
 // Granule layout (head dims 64 and 128; other head dims are stored row-major
 // [pos][hd]): 16 positions per granule, 16*hd elements. A wave reads one
@@ -48,7 +49,9 @@ struct KvGeom {
 };
 
 constexpr int kGranule = 16;
-constexpr int kCapAlign = 32;  // the attention kernels read whole 32-position chunks
+// the attention kernels read whole 32-position chunks, the prefill kernel
+// whole 64-position stages
+constexpr int kCapAlign = 64;
 
 __host__ __device__ inline int kslot_xor(int hd, int c) {
   return hd == 128 ? ((((c >> 3) & 1) << 1) ^ ((c >> 2) & 1)) : ((c >> 2) & 1);
@@ -147,6 +150,15 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws,
                             const AttnCall& c, hipStream_t st);
 // Number of partial floats one call needs (for workspace sizing).
 size_t attention_workspace_need(const KvGeom& g, const AttnCall& c);
+
+// Causal chunks of at least this many rows over the dense fp32 cache run on
+// the matrix cores (prefill.hip); shorter ones through launch_attention.
+constexpr int kPrefillMinRows = 64;
+constexpr int kPrefillMaxSplits = 4;  // key splits of one chunk (workspace records)
+bool prefill_supported(const KvGeom& g, int n_heads, int rows);
+size_t prefill_workspace_need(const KvGeom& g, const AttnCall& c);
+hipError_t launch_prefill(const KvGeom& g, const KvStore& s, Workspace& ws, const AttnCall& c,
+                          hipStream_t st);
 size_t attention_counters_need(const KvGeom& g, const AttnCall& c);
 bool attention_supported(const KvGeom& g, int n_heads);
 

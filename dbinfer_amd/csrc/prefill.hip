@@ -1,0 +1,342 @@
+// Causal chunk attention of the dense fp32 cache on the matrix cores: the
+// attention loop of decode_layer_chunk (model.cpp:956-981), rows c of a
+// chunk at pos0 attending keys [0, pos0 + c], for chunks long enough to
+// make QK^T and PV real matrix products (the prefill chunks of config 2).
+//
+// Design (CDNA4 v_mfma_f32_16x16x4_f32, fp32 in and out, so the result stays
+// within the fp32 tolerance of the CPU path):
+//  - A workgroup of 4 waves owns 64 query vectors of one kv head: each wave
+//    16 vectors (16/G rows x the G query heads sharing the kv head). The
+//    workgroup walks its keys in stages of SK keys: the stage's K and V are
+//    copied into LDS once, by LDS-direct loads (no registers), and every
+//    wave reads its MFMA operands from there. Stages are double-buffered:
+//    the next stage's copy is in flight while the current one computes.
+//  - Keys can be split over KS workgroups (grid z) to fill the GPU on short
+//    chunks; a split writes its unnormalized (o, m, l) and prefill_merge
+//    combines them.
+//  - S^T = K Q^T: A = K (16 keys x 4 dims), B = Q^T (4 dims x 16 vectors),
+//    one instruction per 4 dims, in four independent accumulator chains.
+//    Dims are permuted per lane group so that every lane's operands are 16
+//    contiguous floats: in instruction (h, s), k-index kk stands for dim
+//    16 kk + 64 h + s. The result holds S[vector l % 16][key 4 (l / 16) + v]
+//    in lane l.
+//  - O^T += V^T P^T: A = V^T (16 dims x 4 keys), B = P^T straight from the S
+//    registers (instruction j uses key 4 kk + j, the score lane l already
+//    holds). Output tile tt row i stands for dim (hd/16) i + tt, so a lane's
+//    V operands are hd/16 contiguous floats per key and its output is hd/4
+//    contiguous floats of its vector.
+//  - Online softmax per vector (= per lane % 16); the four lane groups
+//    holding one vector combine through two xor shuffles.
+//  - LDS holds the stage in the cache's own granule layout (kv_internal.hpp),
+//    so the copy is a straight contiguous one and the operand offsets are
+//    the layout's offsets relative to the stage.
+#include <cmath>
+
+#include "kv_internal.hpp"
+
+namespace dbi {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPWaves = 4;
+constexpr int kPThreads = 64 * kPWaves;
+constexpr float kLog2eP = 1.4426950408889634f;
+constexpr float kMinitP = -1.0e30f;  // finite: exp2(kMinit - kMinit) == 1
+
+struct PrefillParams {
+  const float* kf;  // this layer's K, V: [nkv][capg * hd], granule layout
+  const float* vf;
+  const float* q;   // [rows][n_heads][hd]
+  float* out;       // [rows][n_heads][hd]
+  float* part;      // KS > 1: [KS][rows][n_heads][hd + 2] (o unnormalized, m, l)
+  int capg, n_heads, rows, pos0, ks;
+  float qscale;     // scale * log2(e)
+};
+
+// one 16-byte LDS-direct copy per lane (dst is the wave's base; lane l lands
+// at dst + 4 l). Kept out of line of the kernel body: used on a __shared__
+// array there, the builtin stops the host pass from emitting the kernel.
+__device__ __forceinline__ void lds_copy16(const float* src, float* dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
+
+__device__ __forceinline__ float4 lds4(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+
+template <int HD>
+struct Stage {
+  static constexpr int SK = HD == 64 ? 64 : 32;                // keys per stage
+  static constexpr int FL = SK * HD;                           // floats of K (or V)
+  static constexpr int NDMA = FL * 4 / (kPThreads * 16);       // 16-byte copies per thread
+};
+
+template <int HD, int G>
+__global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams P) {
+  using S = Stage<HD>;
+  constexpr int SK = S::SK, FL = S::FL, NDMA = S::NDMA;
+  constexpr int RPV = 16 / G;    // rows per wave
+  constexpr int NQ = HD / 4;     // QK instructions per 16-key tile
+  constexpr int NH = HD / 64;    // 16-dim runs per lane group
+  constexpr int VD = HD / 16;    // V dims per lane per key = output tiles
+  constexpr int NT = HD / 16;
+  __shared__ __align__(16) float s_kv[2][2][FL];  // [buffer][K, V][stage]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kh = blockIdx.y;
+  const int gq = lane >> 4;      // lane group
+  const int vec = lane & 15;     // query vector of this lane
+  const int rowb = blockIdx.x * (kPWaves * RPV);     // first row of the workgroup
+  const int row0 = rowb + wave * RPV;                 // first row of the wave
+  const bool wave_live = row0 < P.rows;               // wave-uniform
+  const int row = min(row0 + vec / G, P.rows - 1);
+  const int head = kh * G + vec % G;
+  const int limit = P.pos0 + row;  // last key of this vector
+  // the workgroup's keys [0, last_key], in stages; split z takes its share
+  const int last_key = P.pos0 + min(rowb + kPWaves * RPV - 1, P.rows - 1);
+  const int n_stages = last_key / SK + 1;
+  const int st_begin = n_stages * static_cast<int>(blockIdx.z) / P.ks;
+  const int st_end = n_stages * (static_cast<int>(blockIdx.z) + 1) / P.ks;
+  const int wave_last = P.pos0 + min(row0 + RPV - 1, P.rows - 1);  // wave-uniform
+
+  const size_t head_el = static_cast<size_t>(kh) * P.capg * HD;
+  const float* kbase = P.kf + head_el;
+  const float* vbase = P.vf + head_el;
+
+  // stage copy: K then V, contiguous, 16 bytes per lane per instruction
+  auto copy_stage = [&](int st, int buf) {
+    const size_t off = static_cast<size_t>(st) * FL;
+#pragma unroll
+    for (int m = 0; m < NDMA; ++m) {
+      const int e = (m * kPThreads + wave * 64) * 4;  // this wave's KiB of the copy
+      lds_copy16(kbase + off + e + lane * 4, &s_kv[buf][0][e]);
+      lds_copy16(vbase + off + e + lane * 4, &s_kv[buf][1][e]);
+    }
+  };
+
+  // Q^T operands: dims 16 gq + 64 h + s, pre-scaled into the log2 domain
+  float qv[NQ];
+  {
+    const float* qp = P.q + (static_cast<size_t>(row) * P.n_heads + head) * HD + 16 * gq;
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const float4 t = *reinterpret_cast<const float4*>(qp + 64 * h + 4 * s4);
+        qv[16 * h + 4 * s4 + 0] = t.x * P.qscale;
+        qv[16 * h + 4 * s4 + 1] = t.y * P.qscale;
+        qv[16 * h + 4 * s4 + 2] = t.z * P.qscale;
+        qv[16 * h + 4 * s4 + 3] = t.w * P.qscale;
+      }
+  }
+
+  f4 acc[NT];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) acc[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = kMinitP, l_run = 0.0f;
+
+  if (st_begin < st_end) copy_stage(st_begin, 0);
+  for (int st = st_begin; st < st_end; ++st) {
+    const int buf = (st - st_begin) & 1;
+    if (st + 1 < st_end) {
+      copy_stage(st + 1, buf ^ 1);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");  // stage st landed
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+    const float* sk = s_kv[buf][0];
+    const float* sv = s_kv[buf][1];
+#pragma unroll
+    for (int t = 0; t < SK / 16; ++t) {
+      const int kb = st * SK + 16 * t;  // first key of the tile (wave-uniform)
+      if (!wave_live || kb > wave_last) continue;  // tile past every row of the wave
+      // S^T tile in four independent chains
+      f4 sc[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sc[c] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        const float* kp = sk + k_off_tiled(HD, false, 16 * t + vec, 16 * gq + 64 * h);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const float4 x = lds4(kp + 4 * s4);
+          const int i = 16 * h + 4 * s4;
+          sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, qv[i + 0], sc[0], 0, 0, 0);
+          sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, qv[i + 1], sc[1], 0, 0, 0);
+          sc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, qv[i + 2], sc[2], 0, 0, 0);
+          sc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, qv[i + 3], sc[3], 0, 0, 0);
+        }
+      }
+      const f4 s = (sc[0] + sc[1]) + (sc[2] + sc[3]);
+
+      // online softmax per vector
+      float sv4[4];
+      float mx = kMinitP;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int key = kb + 4 * gq + v;
+        sv4[v] = key <= limit ? s[v] : -INFINITY;
+        mx = fmaxf(mx, sv4[v]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+      float pv[4], ls = 0.0f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        pv[v] = __builtin_amdgcn_exp2f(sv4[v] - mn);
+        ls += pv[v];
+      }
+      ls += __shfl_xor(ls, 16);
+      ls += __shfl_xor(ls, 32);
+      l_run = l_run * alpha + ls;
+      m_run = mn;
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) acc[tt] *= alpha;
+
+      // O^T += V^T P^T: output tile tt row i is dim VD i + tt. Keys past the
+      // workgroup's last row are never weighted and read as 0.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = kb + 4 * gq + j;
+        const float* vp = sv + v_off_tiled(HD, false, 16 * t + 4 * gq + j, VD * vec);
+        float vd[VD];
+#pragma unroll
+        for (int u = 0; u < VD / 4; ++u) {
+          const float4 x = lds4(vp + 256 * u);
+          vd[4 * u + 0] = key <= last_key ? x.x : 0.0f;
+          vd[4 * u + 1] = key <= last_key ? x.y : 0.0f;
+          vd[4 * u + 2] = key <= last_key ? x.z : 0.0f;
+          vd[4 * u + 3] = key <= last_key ? x.w : 0.0f;
+        }
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[tt], pv[j], acc[tt], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // every wave is done with this buffer before it is refilled
+  }
+
+  // lane holds O^T[dim VD (4 gq + v) + tt][vec]: dims 4 VD gq .. 4 VD gq + 4 VD - 1
+  if (!wave_live || row0 + vec / G >= P.rows) return;
+  const size_t rh = static_cast<size_t>(row) * P.n_heads + head;
+  if (P.ks == 1) {
+    const float inv = 1.0f / l_run;
+    float* op = P.out + rh * HD + 4 * VD * gq;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+      for (int tt = 0; tt < NT; tt += 4)
+        *reinterpret_cast<float4*>(op + VD * v + tt) =
+            make_float4(acc[tt][v] * inv, acc[tt + 1][v] * inv, acc[tt + 2][v] * inv,
+                        acc[tt + 3][v] * inv);
+    return;
+  }
+  float* rec = P.part + (static_cast<size_t>(blockIdx.z) * P.rows * P.n_heads + rh) * (HD + 2);
+  float* op = rec + 4 * VD * gq;
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+#pragma unroll
+    for (int tt = 0; tt < NT; tt += 4)
+      *reinterpret_cast<float4*>(op + VD * v + tt) =
+          make_float4(acc[tt][v], acc[tt + 1][v], acc[tt + 2][v], acc[tt + 3][v]);
+  if (gq == 0) {
+    rec[HD] = m_run;
+    rec[HD + 1] = l_run;
+  }
+}
+
+// Combines the KS key splits of every (row, query head): one thread per dim.
+template <int HD>
+__global__ __launch_bounds__(HD) void prefill_merge(const float* __restrict__ part,
+                                                    float* __restrict__ out, int n_vec, int ks) {
+  const int rh = blockIdx.x;
+  const int d = threadIdx.x;
+  float M = kMinitP;
+  for (int z = 0; z < ks; ++z) M = fmaxf(M, part[(static_cast<size_t>(z) * n_vec + rh) * (HD + 2) + HD]);
+  float L = 0.0f, O = 0.0f;
+  for (int z = 0; z < ks; ++z) {
+    const float* r = part + (static_cast<size_t>(z) * n_vec + rh) * (HD + 2);
+    const float w = __builtin_amdgcn_exp2f(r[HD] - M);
+    L += r[HD + 1] * w;
+    O += r[d] * w;
+  }
+  out[static_cast<size_t>(rh) * HD + d] = O / L;
+}
+
+template <int HD>
+void* prefill_for(int G) {
+  switch (G) {
+    case 1: return reinterpret_cast<void*>(&prefill_kernel<HD, 1>);
+    case 2: return reinterpret_cast<void*>(&prefill_kernel<HD, 2>);
+    case 4: return reinterpret_cast<void*>(&prefill_kernel<HD, 4>);
+    case 8: return reinterpret_cast<void*>(&prefill_kernel<HD, 8>);
+    default: return nullptr;
+  }
+}
+
+// key splits: enough workgroups for every CU, at least two stages each
+int prefill_splits(const KvGeom& g, const AttnCall& c) {
+  const int G = c.n_heads / g.nkv;
+  const int rows_per_block = kPWaves * (16 / G);
+  const int blocks = (c.rows + rows_per_block - 1) / rows_per_block * g.nkv;
+  const int sk = g.hd == 64 ? Stage<64>::SK : Stage<128>::SK;
+  const int stages = (c.pos0 + c.rows - 1) / sk + 1;
+  int ks = 1;
+  while (ks < kPrefillMaxSplits && blocks * ks < 256 && stages / (2 * ks) >= 2) ks *= 2;
+  return ks;
+}
+
+}  // namespace
+
+bool prefill_supported(const KvGeom& g, int n_heads, int rows) {
+  if (g.int8 || g.ring || !g.tiled || rows < kPrefillMinRows || n_heads % g.nkv != 0)
+    return false;
+  const int G = n_heads / g.nkv;
+  return (g.hd == 64 ? prefill_for<64>(G) : prefill_for<128>(G)) != nullptr;
+}
+
+size_t prefill_workspace_need(const KvGeom& g, const AttnCall& c) {
+  const int ks = prefill_splits(g, c);
+  return ks > 1 ? static_cast<size_t>(ks) * c.rows * c.n_heads * (g.hd + 2) : 0;
+}
+
+hipError_t launch_prefill(const KvGeom& g, const KvStore& s, Workspace& ws, const AttnCall& c,
+                          hipStream_t st) {
+  const int G = c.n_heads / g.nkv;
+  void* fn = g.hd == 64 ? prefill_for<64>(G) : prefill_for<128>(G);
+  if (fn == nullptr) return hipErrorNotSupported;
+  const int ks = prefill_splits(g, c);
+  if (ks > 1 && ws.part_floats < prefill_workspace_need(g, c)) return hipErrorInvalidValue;
+  PrefillParams p{};
+  const size_t layer_el = static_cast<size_t>(c.layer) * g.nkv * head_elems(g);
+  p.kf = s.k + layer_el;
+  p.vf = s.v + layer_el;
+  p.q = c.q;
+  p.out = c.out;
+  p.part = ws.part;
+  p.capg = g.capg;
+  p.n_heads = c.n_heads;
+  p.rows = c.rows;
+  p.pos0 = c.pos0;
+  p.ks = ks;
+  p.qscale = c.scale * kLog2eP;
+  const int rows_per_block = kPWaves * (16 / G);
+  void* args[] = {&p};
+  hipError_t e = hipLaunchKernel(fn, dim3((c.rows + rows_per_block - 1) / rows_per_block, g.nkv, ks),
+                                 dim3(kPThreads), args, 0, st);
+  if (e != hipSuccess || ks == 1) return e;
+  if (g.hd == 64)
+    hipLaunchKernelGGL(prefill_merge<64>, dim3(c.rows * c.n_heads), dim3(64), 0, st, ws.part,
+                       c.out, c.rows * c.n_heads, ks);
+  else
+    hipLaunchKernelGGL(prefill_merge<128>, dim3(c.rows * c.n_heads), dim3(128), 0, st, ws.part,
+                       c.out, c.rows * c.n_heads, ks);
+  return hipGetLastError();
+}
+
+}  // namespace dbi

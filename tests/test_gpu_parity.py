@@ -274,9 +274,15 @@ def test_fused_decode_rejects_bad_input():
 
 
 @pytest.mark.parametrize("dtype", [F32, INT8])
-@pytest.mark.parametrize("nh,nkv,hd,pos0,n", [(32, 8, 64, 0, 64), (32, 8, 64, 256, 100),
-                                              (32, 8, 128, 2047, 5), (24, 8, 128, 70, 9),
-                                              (14, 2, 64, 3, 1)])
+@pytest.mark.parametrize("nh,nkv,hd,pos0,n", [
+    (32, 8, 64, 0, 64), (32, 8, 64, 256, 100),
+    (32, 8, 64, 1792, 256),   # config 2's last prefill chunk (matrix-core path for fp32)
+    (32, 8, 128, 300, 128),   # hd 128, gqa 4
+    (8, 8, 64, 5, 70),        # gqa 1
+    (16, 8, 128, 17, 77),     # gqa 2, ragged last wave
+    (32, 4, 64, 1000, 65),    # gqa 8 (config 1 shape)
+    (32, 8, 128, 2047, 5), (24, 8, 128, 70, 9),
+    (14, 2, 64, 3, 1)])
 def test_chunk_attention(dtype, nh, nkv, hd, pos0, n):
     g, o = pair(1, 2100, nkv, hd, n_sink=4, dtype=dtype)
     fill_both(g, o, 1, pos0 + n, 40 + n)
