@@ -55,7 +55,8 @@ namespace {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kMaxSplits = 32;
+constexpr int kMaxSplits = 64;  // one split per lane in the merge
+constexpr int kMergeBatch = 32;  // split records the merge loads per round
 // split-arrival counters sit 256 bytes apart: the atomics of different
 // (row, kv head) pairs never share a cache line
 constexpr int kCounterStride = 64;
@@ -330,12 +331,15 @@ __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs
   const int r0 = min(lane, P.nsplit - 1) * rec_floats;
   const float m = ld(r0 + G * HD + g);
   const float l = ld(r0 + G * HD + G + g);
-  float ov[kMaxSplits][DPL];
+  float ov[kMergeBatch][DPL];
+  auto load_batch = [&](int sp0) {
 #pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp)
+    for (int sp = 0; sp < kMergeBatch; ++sp)
 #pragma unroll
-    for (int e = 0; e < DPL; ++e)
-      ov[sp][e] = ld(min(sp, P.nsplit - 1) * rec_floats + g * HD + lane * DPL + e);
+      for (int e = 0; e < DPL; ++e)
+        ov[sp][e] = ld(min(sp0 + sp, P.nsplit - 1) * rec_floats + g * HD + lane * DPL + e);
+  };
+  load_batch(0);
   const int ns = min(P.n_sink, P.pos0 + qrow + 1);
   const size_t h = static_cast<size_t>(qrow) * P.n_heads + kh * G + g;
   float qd[DPL], kd[kSinkBatch][DPL], vd[kSinkBatch][DPL];
@@ -366,12 +370,16 @@ __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs
   const float w = on ? fast_exp2(m - M) : 0.0f;
   float L = wave_sum(on ? l * w : 0.0f);
   float O[DPL] = {};
+  for (int sp0 = 0; sp0 < P.nsplit; sp0 += kMergeBatch) {  // uniform
+    if (sp0 > 0) load_batch(sp0);
 #pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp) {
-    const float ws =
-        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), sp));
+    for (int sp = 0; sp < kMergeBatch; ++sp) {
+      // lanes past nsplit hold weight 0 (and clamped records)
+      const float ws = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), min(sp0 + sp, 63)));
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) O[e] += ws * ov[sp][e];
+      for (int e = 0; e < DPL; ++e) O[e] += ws * ov[sp][e];
+    }
   }
   // sinks as further entries, a batch at a time with a running max
   for (int p0 = 0; p0 < ns; p0 += kSinkBatch) {

@@ -152,9 +152,11 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws,
 size_t attention_workspace_need(const KvGeom& g, const AttnCall& c);
 
 // Causal chunks of at least this many rows over the dense fp32 cache run on
-// the matrix cores (prefill.hip); shorter ones through launch_attention.
+// the matrix cores (prefill.hip); shorter ones (verify rounds) through
+// launch_attention, whose many small per-wave streams keep more bytes in
+// flight than the prefill kernel's one staged stream per workgroup.
 constexpr int kPrefillMinRows = 64;
-constexpr int kPrefillMaxSplits = 4;  // key splits of one chunk (workspace records)
+constexpr int kPrefillMaxSplits = 8;  // key splits of one chunk (workspace records)
 bool prefill_supported(const KvGeom& g, int n_heads, int rows);
 size_t prefill_workspace_need(const KvGeom& g, const AttnCall& c);
 hipError_t launch_prefill(const KvGeom& g, const KvStore& s, Workspace& ws, const AttnCall& c,
