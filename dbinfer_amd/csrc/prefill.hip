@@ -61,6 +61,14 @@ __device__ __forceinline__ void lds_copy16(const float* src, float* dst) {
   __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
+// Workgroup barrier that waits for this wave's LDS accesses only. The
+// compiler's __syncthreads also waits for every vector memory load (vmcnt 0)
+// when LDS-direct copies are in flight, which would drain the prefetched
+// stages at every stage; stage arrival is waited for explicitly instead.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ float4 lds4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
@@ -72,7 +80,9 @@ struct Stage {
   static constexpr int NDMA = FL * 4 / (kPThreads * 16);       // 16-byte copies per thread
 };
 
-template <int HD, int G>
+// NBUF stage buffers: NBUF - 1 stage copies are in flight ahead of the one
+// being computed (2: two workgroups per CU share the CU's LDS).
+template <int HD, int G, int NBUF>
 __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams P) {
   using S = Stage<HD>;
   constexpr int SK = S::SK, FL = S::FL, NDMA = S::NDMA;
@@ -81,7 +91,14 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
   constexpr int NH = HD / 64;    // 16-dim runs per lane group
   constexpr int VD = HD / 16;    // V dims per lane per key = output tiles
   constexpr int NT = HD / 16;
-  __shared__ __align__(16) float s_kv[2][2][FL];  // [buffer][K, V][stage]
+  // one array per stage buffer ([K, V][stage]): with the buffer known at
+  // compile time, the compiler's own waits tell the buffers' LDS-direct
+  // copies apart instead of draining them all before every LDS read
+  __shared__ __align__(16) float s_b0[2 * FL];
+  __shared__ __align__(16) float s_b1[2 * FL];
+  __shared__ __align__(16) float s_b2[NBUF > 2 ? 2 * FL : 4];
+  __shared__ __align__(16) float s_b3[NBUF > 3 ? 2 * FL : 4];
+  auto bufp = [&](int b) -> float* { return b == 0 ? s_b0 : b == 1 ? s_b1 : b == 2 ? s_b2 : s_b3; };
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -106,13 +123,13 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
   const float* vbase = P.vf + head_el;
 
   // stage copy: K then V, contiguous, 16 bytes per lane per instruction
-  auto copy_stage = [&](int st, int buf) {
+  auto copy_stage = [&](int st, float* dst) {
     const size_t off = static_cast<size_t>(st) * FL;
 #pragma unroll
     for (int m = 0; m < NDMA; ++m) {
       const int e = (m * kPThreads + wave * 64) * 4;  // this wave's KiB of the copy
-      lds_copy16(kbase + off + e + lane * 4, &s_kv[buf][0][e]);
-      lds_copy16(vbase + off + e + lane * 4, &s_kv[buf][1][e]);
+      lds_copy16(kbase + off + e + lane * 4, dst + e);
+      lds_copy16(vbase + off + e + lane * 4, dst + FL + e);
     }
   };
 
@@ -137,18 +154,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
   for (int tt = 0; tt < NT; ++tt) acc[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = kMinitP, l_run = 0.0f;
 
-  if (st_begin < st_end) copy_stage(st_begin, 0);
-  for (int st = st_begin; st < st_end; ++st) {
-    const int buf = (st - st_begin) & 1;
-    if (st + 1 < st_end) {
-      copy_stage(st + 1, buf ^ 1);
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");  // stage st landed
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    __syncthreads();
-    const float* sk = s_kv[buf][0];
-    const float* sv = s_kv[buf][1];
+  auto compute_stage = [&](int st, const float* sk, const float* sv) {
 #pragma unroll
     for (int t = 0; t < SK / 16; ++t) {
       const int kb = st * SK + 16 * t;  // first key of the tile (wave-uniform)
@@ -218,7 +224,33 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
           acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[tt], pv[j], acc[tt], 0, 0, 0);
       }
     }
-    __syncthreads();  // every wave is done with this buffer before it is refilled
+  };
+
+#pragma unroll
+  for (int i = 0; i < NBUF - 1; ++i)
+    if (st_begin + i < st_end) copy_stage(st_begin + i, bufp(i));
+  // unrolled by the buffer count, so every buffer index is a constant
+  for (int st0 = st_begin; st0 < st_end; st0 += NBUF) {
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) {
+      const int st = st0 + b;
+      if (st >= st_end) break;  // uniform
+      if (st + NBUF - 1 < st_end) copy_stage(st + NBUF - 1, bufp((b + NBUF - 1) % NBUF));
+      // stage st has landed once at most the copies of the stages after it
+      // are outstanding (loads complete in order)
+      const int after = min(st_end - 1 - st, NBUF - 1);  // uniform
+      if (after >= 3)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * 2 * NDMA) : "memory");
+      else if (after == 2)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * 2 * NDMA) : "memory");
+      else if (after == 1)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      lds_barrier();  // every wave's part of stage st has landed
+      compute_stage(st, bufp(b), bufp(b) + FL);
+      lds_barrier();  // every wave is done with this buffer before it is refilled
+    }
   }
 
   // lane holds O^T[dim VD (4 gq + v) + tt][vec]: dims 4 VD gq .. 4 VD gq + 4 VD - 1
@@ -268,18 +300,23 @@ __global__ __launch_bounds__(HD) void prefill_merge(const float* __restrict__ pa
   out[static_cast<size_t>(rh) * HD + d] = O / L;
 }
 
-template <int HD>
+template <int HD, int NBUF>
 void* prefill_for(int G) {
   switch (G) {
-    case 1: return reinterpret_cast<void*>(&prefill_kernel<HD, 1>);
-    case 2: return reinterpret_cast<void*>(&prefill_kernel<HD, 2>);
-    case 4: return reinterpret_cast<void*>(&prefill_kernel<HD, 4>);
-    case 8: return reinterpret_cast<void*>(&prefill_kernel<HD, 8>);
+    case 1: return reinterpret_cast<void*>(&prefill_kernel<HD, 1, NBUF>);
+    case 2: return reinterpret_cast<void*>(&prefill_kernel<HD, 2, NBUF>);
+    case 4: return reinterpret_cast<void*>(&prefill_kernel<HD, 4, NBUF>);
+    case 8: return reinterpret_cast<void*>(&prefill_kernel<HD, 8, NBUF>);
     default: return nullptr;
   }
 }
 
-// key splits: enough workgroups for every CU, at least two stages each
+void* pick_prefill(int hd, int G, int /*rows*/) {
+  return hd == 64 ? prefill_for<64, 2>(G) : prefill_for<128, 2>(G);
+}
+
+// key splits: two workgroups per CU (one wave per SIMD cannot hide the LDS
+// and matrix-core latencies by itself), at least two stages each
 int prefill_splits(const KvGeom& g, const AttnCall& c) {
   const int G = c.n_heads / g.nkv;
   const int rows_per_block = kPWaves * (16 / G);
@@ -287,7 +324,7 @@ int prefill_splits(const KvGeom& g, const AttnCall& c) {
   const int sk = g.hd == 64 ? Stage<64>::SK : Stage<128>::SK;
   const int stages = (c.pos0 + c.rows - 1) / sk + 1;
   int ks = 1;
-  while (ks < kPrefillMaxSplits && blocks * ks < 256 && stages / (2 * ks) >= 2) ks *= 2;
+  while (ks < kPrefillMaxSplits && blocks * ks < 512 && stages / (2 * ks) >= 2) ks *= 2;
   return ks;
 }
 
@@ -296,8 +333,7 @@ int prefill_splits(const KvGeom& g, const AttnCall& c) {
 bool prefill_supported(const KvGeom& g, int n_heads, int rows) {
   if (g.int8 || g.ring || !g.tiled || rows < kPrefillMinRows || n_heads % g.nkv != 0)
     return false;
-  const int G = n_heads / g.nkv;
-  return (g.hd == 64 ? prefill_for<64>(G) : prefill_for<128>(G)) != nullptr;
+  return pick_prefill(g.hd, n_heads / g.nkv, rows) != nullptr;
 }
 
 size_t prefill_workspace_need(const KvGeom& g, const AttnCall& c) {
@@ -308,7 +344,7 @@ size_t prefill_workspace_need(const KvGeom& g, const AttnCall& c) {
 hipError_t launch_prefill(const KvGeom& g, const KvStore& s, Workspace& ws, const AttnCall& c,
                           hipStream_t st) {
   const int G = c.n_heads / g.nkv;
-  void* fn = g.hd == 64 ? prefill_for<64>(G) : prefill_for<128>(G);
+  void* fn = pick_prefill(g.hd, G, c.rows);
   if (fn == nullptr) return hipErrorNotSupported;
   const int ks = prefill_splits(g, c);
   if (ks > 1 && ws.part_floats < prefill_workspace_need(g, c)) return hipErrorInvalidValue;
