@@ -323,9 +323,56 @@ def run_configs(torch, HipKV, F32, INT8, args):
                             "chunk_TFLOPs": round(flops / (usc * 1e-6) / 1e12, 3)})
                 del gc
             kv.close()
+            if args.configs_cpu:
+                res["cpu"] = config_cpu(K, V, q, name, nh, nkv, hd, dt, ns, win, pos, rows, scale)
             del K, V, q, out
         torch.cuda.synchronize()
         print(json.dumps(res), flush=True)
+
+
+def config_cpu(K, V, q, name, nh, nkv, hd, dt, ns, win, pos, rows, scale):
+    """The CPU oracle on one layer of the same config (head-parallel on the
+    host cores): the decode step (append at pos + attention) and, for the
+    chunk configs, the chunk attention; median of >= 3 runs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle  # checker / baseline only
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    Kh = K.cpu().numpy()
+    Vh = V.cpu().numpy()
+    qh = q[0].cpu().numpy()
+    o = pyoracle.OracleKV(1, pos + 1 if not win else 1, nkv, hd, n_sink=ns, window=win,
+                          dtype=pyoracle.INT8 if dt == "int8" else pyoracle.F32, rope_theta=1e6)
+    t0 = time.perf_counter()
+    o.append_n(0, 0, Kh[:pos], Vh[:pos])
+    fill_s = time.perf_counter() - t0
+
+    def med(fn, n=3):
+        ts = []
+        for _ in range(n):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return statistics.median(ts)
+
+    if win:
+        step_s = med(lambda: o.attend_ring(0, pos, qh[: nh * hd], Kh[pos], Vh[pos], nh, scale,
+                                           n_threads=threads))
+    else:
+        def step():
+            o.append(0, pos, Kh[pos], Vh[pos])
+            o.attend(0, pos, qh[: nh * hd], nh, scale, n_threads=threads)
+        step_s = med(step)
+    out = {"us_per_token_layer": round(1e6 * step_s, 1), "threads": threads,
+           "fill_s": round(fill_s, 2), "kind": "port"}
+    if rows:
+        pos0 = 1792 if rows == 256 else pos + 1 - rows
+        if dt == "f32" and not win:
+            chunk_s = med(lambda: o.attend_chunk(0, pos0, qh[: rows * nh * hd], nh, scale,
+                                                 n_threads=threads), 1 if rows > 16 else 3)
+            out["chunk_us"] = round(1e6 * chunk_s, 1)
+    o.close()
+    return out
 
 
 def _cpu_model() -> str:
@@ -348,6 +395,8 @@ def main():
     ap.add_argument("--configs", action="store_true",
                     help="instead of the bench line, one JSON line per SURVEY config (C1-C5)")
     ap.add_argument("--config-steps", type=int, default=30)
+    ap.add_argument("--configs-cpu", action="store_true",
+                    help="with --configs: also time the CPU oracle on one layer of each config")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (PMC calibration)")
     args = ap.parse_args()
