@@ -164,6 +164,9 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
 __device__ __forceinline__ float4 load_b128(rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
+__device__ __forceinline__ float2 load_b64(rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
 __device__ __forceinline__ float load_b32(rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
@@ -769,8 +772,17 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
           cs[sl][0] = load_b128(rcs, co, 0);
           cs[sl][1] = load_b128(rcs, co + 16, 0);
           if constexpr (KIND == kI8Ring) {
-            ksc[sl][0] = load_b32(rks, (p * NB + (4 * c) / kBlock) * 4, 0);
-            ksc[sl][1] = load_b32(rks, (p * NB + (HD / 2 + 4 * c) / kBlock) * 4, 0);
+            // the position's block scales in one load: the lane's dims 4c..
+            // and hd/2 + 4c.. sit in blocks c / 8 and NB / 2 + c / 8
+            if constexpr (HD == 128) {
+              const float4 t = load_b128(rks, p * NB * 4, 0);
+              ksc[sl][0] = c >= 8 ? t.y : t.x;
+              ksc[sl][1] = c >= 8 ? t.w : t.z;
+            } else {
+              const float2 t = load_b64(rks, p * NB * 4, 0);
+              ksc[sl][0] = t.x;
+              ksc[sl][1] = t.y;
+            }
           }
         }
       }
