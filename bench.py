@@ -301,6 +301,8 @@ def run_configs(torch, HipKV, F32, INT8, args):
                         "frac_of_peak": round(byts / (us * 1e-6) / 1e9 / PEAK_GBS, 4),
                         "working_set_MB": round(L_ * byts / 1e6, 1)})
             del gr
+            if name.startswith("C5") and dt == "f32":
+                res["prefix_io"] = prefix_io(HipKV, F32, kv, L_, pos + 1, nkv, hd, 2048)
             if rows:
                 pos0 = 1792 if rows == 256 else pos + 1 - rows
                 kv.truncate(pos0 + rows)
@@ -328,6 +330,30 @@ def run_configs(torch, HipKV, F32, INT8, args):
             del K, V, q, out
         torch.cuda.synchronize()
         print(json.dumps(res), flush=True)
+
+
+def prefix_io(HipKV, F32, kv, L_, cap, nkv, hd, n_tok):
+    """Config 5's prefix cache: save the first n_tok positions of every layer
+    as a DBKVCACH v1 file, then load it into a fresh cache (model.cpp
+    :1023-1156), timed end to end (device pack, PCIe, file)."""
+    import tempfile
+
+    tokens = np.arange(n_tok, dtype=np.int32)
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as d:
+        path = os.path.join(d, "prefix.dbkv")
+        t = time.perf_counter()
+        kv.save_prefix(path, tokens)
+        save_s = time.perf_counter() - t
+        size = os.path.getsize(path)
+        fresh = HipKV(L_, cap, nkv, hd, 0, 0, F32, 1e6)
+        t = time.perf_counter()
+        n = fresh.load_prefix(path, tokens)
+        load_s = time.perf_counter() - t
+        fresh.close()
+    assert n == n_tok
+    return {"tokens": n_tok, "file_bytes": size, "save_ms": round(1e3 * save_s, 1),
+            "load_ms": round(1e3 * load_s, 1), "save_GBs": round(size / save_s / 1e9, 2),
+            "load_GBs": round(size / load_s / 1e9, 2)}
 
 
 def config_cpu(K, V, q, name, nh, nkv, hd, dt, ns, win, pos, rows, scale):

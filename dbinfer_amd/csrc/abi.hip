@@ -33,6 +33,11 @@ dbi_status hip_fail(hipError_t e, const char* what) {
   return fail(DBI_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// Prefix files move through one pinned host chunk per handle (allocated on
+// first use, kept): PCIe copies run at DMA speed and no pageable bounce or
+// whole-file host buffer is needed.
+constexpr size_t kPinChunk = size_t(32) << 20;
+
 #define HIP_TRY(expr, what)                  \
   do {                                       \
     hipError_t e_ = (expr);                  \
@@ -58,6 +63,7 @@ void free_store(dbi::KvStore& s) {
 
 void free_ws(dbi::Workspace& w) {
   if (w.part) (void)hipFree(w.part);
+  if (w.pinned) (void)hipHostFree(w.pinned);
   if (w.counters) (void)hipFree(w.counters);
   if (w.staging) (void)hipFree(w.staging);
   w = dbi::Workspace{};
@@ -99,6 +105,15 @@ dbi::RingView ring_view(const dbi_kv* kv, uint32_t n_seen) {
   r.n_res = full ? static_cast<int>(s + W) : static_cast<int>(n_seen);
   r.base = full ? static_cast<int>((n_seen - s) % W) : 0;
   return r;
+}
+
+dbi_status need_pinned(dbi_kv* kv) {
+  if (kv->ws.pinned) return DBI_OK;
+  if (hipHostMalloc(reinterpret_cast<void**>(&kv->ws.pinned), kPinChunk, 0) != hipSuccess) {
+    kv->ws.pinned = nullptr;
+    return fail(DBI_ERR_NOMEM, "out of pinned host memory for prefix-file transfers");
+  }
+  return DBI_OK;
 }
 
 dbi_status ensure_part(dbi_kv* kv, size_t part) {
@@ -535,42 +550,46 @@ dbi_status dbi_kv_prefix_save(dbi_kv* kv, const char* path, const int32_t* token
 
   const dbi::KvGeom& g = kv->geom;
   const size_t elems = size_t(g.n_layers) * len * g.nkv * g.hd;
-  const size_t hdr = 8 + 5 * 4 + size_t(len) * 4;
-  std::vector<unsigned char> buf;
-  try {
-    buf.resize(hdr + 2 * elems * sizeof(float));
-  } catch (...) {
-    return fail(DBI_ERR_NOMEM, "out of host memory");
-  }
-  std::memcpy(buf.data(), kMagic, 8);
+  if (dbi_status st = need_pinned(kv)) return st;
+  std::vector<unsigned char> hdr(8 + 5 * 4 + size_t(len) * 4);
+  std::memcpy(hdr.data(), kMagic, 8);
   const uint32_t h[5] = {kVersion, kv->cfg.n_layers, kv->cfg.n_kv_heads, kv->cfg.head_dim, len};
-  std::memcpy(buf.data() + 8, h, sizeof h);
-  std::memcpy(buf.data() + 28, tokens, size_t(len) * 4);
+  std::memcpy(hdr.data() + 8, h, sizeof h);
+  std::memcpy(hdr.data() + 28, tokens, size_t(len) * 4);
 
-  float* dev = nullptr;
-  if (hipMalloc(reinterpret_cast<void**>(&dev), elems * sizeof(float)) != hipSuccess)
+  // K then V packed into [L][len][nkv][hd] on the device, then streamed out
+  unsigned char* dev = nullptr;
+  const size_t payload = 2 * elems * sizeof(float);
+  if (hipMalloc(reinterpret_cast<void**>(&dev), payload) != hipSuccess)
     return fail(DBI_ERR_NOMEM, "prefix staging allocation failed");
+  float* devf = reinterpret_cast<float*>(dev);
   hipError_t e =
-      dbi::launch_prefix_pack(g, kv->store.k, dev, static_cast<int>(len), true, kv->stream);
+      dbi::launch_prefix_pack(g, kv->store.k, devf, static_cast<int>(len), true, kv->stream);
   if (e == hipSuccess)
-    e = hipMemcpyAsync(buf.data() + hdr, dev, elems * sizeof(float), hipMemcpyDeviceToHost,
-                       kv->stream);
-  if (e == hipSuccess)
-    e = dbi::launch_prefix_pack(g, kv->store.v, dev, static_cast<int>(len), false, kv->stream);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(buf.data() + hdr + elems * sizeof(float), dev, elems * sizeof(float),
-                       hipMemcpyDeviceToHost, kv->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(kv->stream);
+    e = dbi::launch_prefix_pack(g, kv->store.v, devf + elems, static_cast<int>(len), false,
+                                kv->stream);
+  std::FILE* f = nullptr;
+  if (e == hipSuccess) {
+    f = std::fopen(path, "wb");
+    if (f == nullptr) {
+      (void)hipStreamSynchronize(kv->stream);
+      (void)hipFree(dev);
+      return fail(DBI_ERR_IO, std::string("cannot open kv prefix cache for writing ") + path);
+    }
+  }
+  bool ok = f != nullptr && std::fwrite(hdr.data(), 1, hdr.size(), f) == hdr.size();
+  for (size_t off = 0; ok && e == hipSuccess && off < payload; off += kPinChunk) {
+    const size_t n = payload - off < kPinChunk ? payload - off : kPinChunk;
+    e = hipMemcpyAsync(kv->ws.pinned, dev + off, n, hipMemcpyDeviceToHost, kv->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(kv->stream);
+    if (e == hipSuccess) ok = std::fwrite(kv->ws.pinned, 1, n, f) == n;
+  }
+  if (e != hipSuccess) (void)hipStreamSynchronize(kv->stream);
   (void)hipFree(dev);
+  ok = ok && f != nullptr && std::ferror(f) == 0;
+  if (f != nullptr && std::fclose(f) != 0) ok = false;
   if (e != hipSuccess) return hip_fail(e, "prefix readback");
-
-  std::FILE* f = std::fopen(path, "wb");
-  if (f == nullptr)
-    return fail(DBI_ERR_IO, std::string("cannot open kv prefix cache for writing ") + path);
-  const size_t wrote = std::fwrite(buf.data(), 1, buf.size(), f);
-  const bool ok = wrote == buf.size() && std::ferror(f) == 0;
-  if (std::fclose(f) != 0 || !ok)
-    return fail(DBI_ERR_IO, std::string("write error on kv prefix cache ") + path);
+  if (!ok) return fail(DBI_ERR_IO, std::string("write error on kv prefix cache ") + path);
   return DBI_OK;
 }
 
@@ -581,29 +600,37 @@ dbi_status dbi_kv_prefix_load(dbi_kv* kv, const char* path, const int32_t* token
     return fail(DBI_ERR_UNSUPPORTED, "kv prefix cache supports only the dense fp32 cache");
   std::FILE* f = std::fopen(path, "rb");
   if (f == nullptr) return fail(DBI_ERR_IO, std::string("cannot open kv prefix cache ") + path);
-  std::vector<unsigned char> data;
-  {
-    unsigned char chunk[65536];
-    size_t got = 0;
-    while ((got = std::fread(chunk, 1, sizeof chunk, f)) > 0) data.insert(data.end(), chunk, chunk + got);
-  }
-  const bool rd_ok = std::ferror(f) == 0;
-  std::fclose(f);
+  struct Closer {
+    std::FILE* f;
+    ~Closer() { std::fclose(f); }
+  } closer{f};
+  // the file size stands for the reference's whole-file read; the header
+  // and token list are read in front, the payload streamed to the device
+  bool rd_ok = std::fseek(f, 0, SEEK_END) == 0;
+  const long fsize = rd_ok ? std::ftell(f) : -1;
+  rd_ok = rd_ok && fsize >= 0 && std::fseek(f, 0, SEEK_SET) == 0;
   if (!rd_ok) return fail(DBI_ERR_IO, std::string("read error on kv prefix cache ") + path);
+  const size_t total = static_cast<size_t>(fsize);
+  size_t p = 0;  // bytes consumed
+  auto need = [&](size_t n) { return p + n <= total; };
+  auto take = [&](void* dst, size_t n) {
+    if (std::fread(dst, 1, n, f) != n) return false;
+    p += n;
+    return true;
+  };
+  auto io_fail = [&] { return fail(DBI_ERR_IO, std::string("read error on kv prefix cache ") + path); };
 
   // validation in the order of model.cpp:1117-1148
-  size_t p = 0;
-  auto need = [&](size_t n) { return p + n <= data.size(); };
   for (int i = 0; i < 8; ++i) {
     if (!need(1)) return fail(DBI_ERR_FORMAT, "kv prefix cache truncated");
-    if (data[p] != kMagic[i]) return fail(DBI_ERR_FORMAT, "kv prefix cache bad magic");
-    ++p;
+    unsigned char ch;
+    if (!take(&ch, 1)) return io_fail();
+    if (ch != kMagic[i]) return fail(DBI_ERR_FORMAT, "kv prefix cache bad magic");
   }
   uint32_t u[5];
   for (int i = 0; i < 5; ++i) {
     if (!need(4)) return fail(DBI_ERR_FORMAT, "kv prefix cache truncated");
-    std::memcpy(&u[i], data.data() + p, 4);
-    p += 4;
+    if (!take(&u[i], 4)) return io_fail();
     if (i == 0 && u[0] != kVersion)
       return fail(DBI_ERR_FORMAT,
                   "kv prefix cache version " + std::to_string(u[0]) + " unsupported");
@@ -619,30 +646,41 @@ dbi_status dbi_kv_prefix_load(dbi_kv* kv, const char* path, const int32_t* token
   for (uint32_t i = 0; i < prefix_len; ++i) {
     if (!need(4)) return fail(DBI_ERR_FORMAT, "kv prefix cache truncated");
     int32_t saved;
-    std::memcpy(&saved, data.data() + p, 4);
-    p += 4;
+    if (!take(&saved, 4)) return io_fail();
     if (saved != tokens[i])
       return fail(DBI_ERR_FORMAT,
                   "prompt prefix differs from saved cache at token " + std::to_string(i));
   }
   const dbi::KvGeom& g = kv->geom;
   const size_t elems = size_t(g.n_layers) * prefix_len * g.nkv * g.hd;
-  if (p + 2 * elems * sizeof(float) != data.size())
-    return fail(DBI_ERR_FORMAT, "kv prefix cache payload size mismatch");
+  const size_t payload = 2 * elems * sizeof(float);
+  if (p + payload != total) return fail(DBI_ERR_FORMAT, "kv prefix cache payload size mismatch");
+  if (dbi_status st = need_pinned(kv)) return st;
 
-  float* dev = nullptr;
-  if (hipMalloc(reinterpret_cast<void**>(&dev), 2 * elems * sizeof(float)) != hipSuccess)
+  // payload to the device in pinned chunks, then unpacked (the cache is
+  // untouched until every byte has arrived)
+  unsigned char* dev = nullptr;
+  if (hipMalloc(reinterpret_cast<void**>(&dev), payload) != hipSuccess)
     return fail(DBI_ERR_NOMEM, "prefix staging allocation failed");
-  hipError_t e = hipMemcpyAsync(dev, data.data() + p, 2 * elems * sizeof(float),
-                                hipMemcpyHostToDevice, kv->stream);
-  if (e == hipSuccess)
-    e = dbi::launch_prefix_unpack(g, dev, kv->store.k, static_cast<int>(prefix_len), true,
+  hipError_t e = hipSuccess;
+  bool ok = true;
+  for (size_t off = 0; ok && e == hipSuccess && off < payload; off += kPinChunk) {
+    const size_t n = payload - off < kPinChunk ? payload - off : kPinChunk;
+    ok = std::fread(kv->ws.pinned, 1, n, f) == n;
+    if (ok) e = hipMemcpyAsync(dev + off, kv->ws.pinned, n, hipMemcpyHostToDevice, kv->stream);
+    if (ok && e == hipSuccess) e = hipStreamSynchronize(kv->stream);
+  }
+  const float* devf = reinterpret_cast<const float*>(dev);
+  if (ok && e == hipSuccess)
+    e = dbi::launch_prefix_unpack(g, devf, kv->store.k, static_cast<int>(prefix_len), true,
                                   kv->stream);
-  if (e == hipSuccess)
-    e = dbi::launch_prefix_unpack(g, dev + elems, kv->store.v, static_cast<int>(prefix_len),
+  if (ok && e == hipSuccess)
+    e = dbi::launch_prefix_unpack(g, devf + elems, kv->store.v, static_cast<int>(prefix_len),
                                   false, kv->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(kv->stream);
+  if (ok && e == hipSuccess) e = hipStreamSynchronize(kv->stream);
+  if (e != hipSuccess) (void)hipStreamSynchronize(kv->stream);
   (void)hipFree(dev);
+  if (!ok) return io_fail();
   if (e != hipSuccess) return hip_fail(e, "prefix upload");
   kv->n_seen = prefix_len;
   if (out_len) *out_len = prefix_len;

@@ -113,6 +113,7 @@ struct Workspace {
   unsigned* counters = nullptr;  // split arrivals per (row, kv head); zero between launches
   size_t counters_n = 0;
   float* staging = nullptr;  // device staging for host-pointer calls
+  unsigned char* pinned = nullptr;  // pinned host chunk for prefix-file transfers
   size_t staging_floats = 0;
 };
 
