@@ -301,6 +301,26 @@ def run_configs(torch, HipKV, F32, INT8, args):
                         "frac_of_peak": round(byts / (us * 1e-6) / 1e9 / PEAK_GBS, 4),
                         "working_set_MB": round(L_ * byts / 1e6, 1)})
             del gr
+            # the same step from raw projections: bias (Qwen2.5, C4) and rope
+            # on the device, then the fused step (dbi_kv_decode_qkv_async)
+            bias = torch.randn(nh * hd + 2 * P, device="cuda", generator=g) if win else None
+            bp = ([bias[:nh * hd].data_ptr(), bias[nh * hd:nh * hd + P].data_ptr(),
+                   bias[nh * hd + P:].data_ptr()] if bias is not None else [None] * 3)
+
+            def pstep(s_):
+                kv.set_stream(s_.cuda_stream)
+                for layer in range(L_):
+                    kv.decode_qkv_async(layer, pos, nh, scale, q[layer].data_ptr(),
+                                        K[pos].data_ptr(), V[pos].data_ptr(), *bp,
+                                        out[layer].data_ptr())
+
+            gp = capture(torch, pstep)  # its warm-up call builds the rope table
+            for _ in range(5):
+                gp.replay()
+            usp = 1000.0 * time_graph(torch, gp, args.config_steps) / L_
+            res.update({"producer_us_per_token_layer": round(usp, 3),
+                        "producer_bias": bias is not None})
+            del gp
             if name.startswith("C5") and dt == "f32":
                 res["prefix_io"] = prefix_io(HipKV, F32, kv, L_, pos + 1, nkv, hd, 2048)
             if rows:

@@ -6,6 +6,7 @@ fails loudly when it is missing: there is no CPU fallback on this path.
 from __future__ import annotations
 
 import ctypes
+import importlib.util
 import os
 import re
 
@@ -70,6 +71,10 @@ SIGNATURES = {
     "dbi_kv_decode_async": (_st, [_vp, _u32, _u32, _vp, _vp, _u32, _f32, _vp, _vp]),
     "dbi_attn_chunk": (_st, [_vp, _u32, _u32, _u32, _u32, _f32, _vp, _vp]),
     "dbi_attn_chunk_async": (_st, [_vp, _u32, _u32, _u32, _u32, _f32, _vp, _vp]),
+    "dbi_kv_decode_qkv": (_st, [_vp, _u32, _u32, _u32, _f32] + [_vp] * 7),
+    "dbi_kv_decode_qkv_async": (_st, [_vp, _u32, _u32, _u32, _f32] + [_vp] * 7),
+    "dbi_kv_chunk_qkv": (_st, [_vp, _u32, _u32, _u32, _u32, _f32] + [_vp] * 7),
+    "dbi_kv_chunk_qkv_async": (_st, [_vp, _u32, _u32, _u32, _u32, _f32] + [_vp] * 7),
     "dbi_kv_prefix_save": (_st, [_vp, ctypes.c_char_p, _vp, _u32]),
     "dbi_kv_prefix_load": (_st, [_vp, ctypes.c_char_p, _vp, _u32, ctypes.POINTER(_u32)]),
     "dbi_kv_export_bytes": (ctypes.c_size_t, [_vp, _u32]),
@@ -95,6 +100,12 @@ def load() -> ctypes.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ImportError(
             f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+    # ROCm builds of torch ship their own HIP runtime (soname libamdhip64.so.7,
+    # file libamdhip64.so). Loaded after this library, torch would map a second
+    # HIP and HSA runtime into the process and find no GPU; loaded first, it
+    # lets this library bind to that same runtime by soname.
+    if importlib.util.find_spec("torch") is not None:
+        import torch  # noqa: F401
     lib = ctypes.CDLL(LIB_PATH)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)

@@ -55,7 +55,7 @@ hipError_t dalloc(T** p, size_t n, int fill = 0) {
 
 void free_store(dbi::KvStore& s) {
   void* ptrs[] = {s.k, s.v, s.k8, s.v8, s.k_scale, s.v_scale, s.k_raw, s.k_sink, s.v_sink,
-                  s.rope_cs};
+                  s.rope_cs, s.rope_dd};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   s = dbi::KvStore{};
@@ -66,6 +66,7 @@ void free_ws(dbi::Workspace& w) {
   if (w.pinned) (void)hipHostFree(w.pinned);
   if (w.counters) (void)hipFree(w.counters);
   if (w.staging) (void)hipFree(w.staging);
+  if (w.prod) (void)hipFree(w.prod);
   w = dbi::Workspace{};
 }
 
@@ -175,17 +176,11 @@ dbi_status check_attend(const dbi_kv* kv, uint32_t layer, uint32_t n_heads, cons
 dbi_status append_impl(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, const float* k_dev,
                        const float* v_dev);
 
-dbi_status decode_impl(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads, float scale,
-                       const float* q_dev, float* out_dev, const float* k_dev = nullptr,
-                       const float* v_dev = nullptr) {
-  if (dbi_status st = check_rows(kv, pos, 1)) return st;
-  // the fused kernel reads the new rows 16 bytes per lane; rows that are not
-  // 16-byte aligned go through the append kernel first
-  if (k_dev != nullptr &&
-      ((reinterpret_cast<uintptr_t>(k_dev) | reinterpret_cast<uintptr_t>(v_dev)) & 15) != 0) {
-    if (dbi_status st = append_impl(kv, layer, pos, 1, k_dev, v_dev)) return st;
-    k_dev = v_dev = nullptr;
-  }
+// The attention call of one decode step at pos; with k_dev/v_dev set, the
+// fused step that appends that row first.
+dbi::AttnCall decode_call(const dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
+                          float scale, const float* q_dev, float* out_dev, const float* k_dev,
+                          const float* v_dev) {
   dbi::AttnCall c{};
   if (k_dev != nullptr) {
     const dbi::KvGeom& g = kv->geom;
@@ -205,18 +200,29 @@ dbi_status decode_impl(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_head
   c.q = q_dev;
   c.out = out_dev;
   if (kv->geom.ring) c.ring = ring_view(kv, pos + 1);
+  return c;
+}
+
+dbi_status decode_impl(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads, float scale,
+                       const float* q_dev, float* out_dev, const float* k_dev = nullptr,
+                       const float* v_dev = nullptr) {
+  if (dbi_status st = check_rows(kv, pos, 1)) return st;
+  // the fused kernel reads the new rows 16 bytes per lane; rows that are not
+  // 16-byte aligned go through the append kernel first
+  if (k_dev != nullptr &&
+      ((reinterpret_cast<uintptr_t>(k_dev) | reinterpret_cast<uintptr_t>(v_dev)) & 15) != 0) {
+    if (dbi_status st = append_impl(kv, layer, pos, 1, k_dev, v_dev)) return st;
+    k_dev = v_dev = nullptr;
+  }
+  const dbi::AttnCall c = decode_call(kv, layer, pos, n_heads, scale, q_dev, out_dev, k_dev, v_dev);
   if (dbi_status st = ensure_workspace(kv, c)) return st;
   HIP_TRY(dbi::launch_attention(kv->geom, kv->store, kv->ws, c, kv->stream), "attention launch");
   if (k_dev != nullptr) kv->n_seen = pos + 1;
   return DBI_OK;
 }
 
-dbi_status chunk_impl(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, uint32_t n_heads,
-                      float scale, const float* q_dev, float* out_dev) {
-  if (kv->geom.ring)
-    return fail(DBI_ERR_UNSUPPORTED, "chunk attention serves the dense layouts only");
-  if (n == 0) return DBI_OK;
-  if (dbi_status st = check_rows(kv, pos0, n)) return st;
+dbi::AttnCall chunk_call(uint32_t layer, uint32_t pos0, uint32_t n, uint32_t n_heads,
+                         float scale, const float* q_dev, float* out_dev) {
   dbi::AttnCall c{};
   c.layer = static_cast<int>(layer);
   c.rows = static_cast<int>(n);
@@ -225,15 +231,43 @@ dbi_status chunk_impl(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, uin
   c.scale = scale;
   c.q = q_dev;
   c.out = out_dev;
+  return c;
+}
+
+dbi_status check_chunk(const dbi_kv* kv, uint32_t pos0, uint32_t n) {
+  if (kv->geom.ring)
+    return fail(DBI_ERR_UNSUPPORTED, "chunk attention serves the dense layouts only");
+  if (n == 0) return DBI_OK;
+  if (dbi_status st = check_rows(kv, pos0, n)) return st;
   if (n > 65535) return fail(DBI_ERR_INVALID, "chunk longer than 65535 rows");
-  if (dbi::prefill_supported(kv->geom, static_cast<int>(n_heads), static_cast<int>(n))) {
-    if (dbi_status st = ensure_part(kv, dbi::prefill_workspace_need(kv->geom, c))) return st;
-    HIP_TRY(dbi::launch_prefill(kv->geom, kv->store, kv->ws, c, kv->stream), "prefill launch");
-    return DBI_OK;
-  }
-  if (dbi_status st = ensure_workspace(kv, c)) return st;
-  HIP_TRY(dbi::launch_attention(kv->geom, kv->store, kv->ws, c, kv->stream), "attention launch");
   return DBI_OK;
+}
+
+// workspace of a chunk call (no launch)
+dbi_status chunk_prepare(dbi_kv* kv, const dbi::AttnCall& c, bool* prefill) {
+  *prefill = dbi::prefill_supported(kv->geom, c.n_heads, c.rows);
+  if (*prefill) return ensure_part(kv, dbi::prefill_workspace_need(kv->geom, c));
+  return ensure_workspace(kv, c);
+}
+
+dbi_status chunk_launch(dbi_kv* kv, const dbi::AttnCall& c, bool prefill) {
+  if (prefill) {
+    HIP_TRY(dbi::launch_prefill(kv->geom, kv->store, kv->ws, c, kv->stream), "prefill launch");
+  } else {
+    HIP_TRY(dbi::launch_attention(kv->geom, kv->store, kv->ws, c, kv->stream),
+            "attention launch");
+  }
+  return DBI_OK;
+}
+
+dbi_status chunk_impl(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, uint32_t n_heads,
+                      float scale, const float* q_dev, float* out_dev) {
+  if (dbi_status st = check_chunk(kv, pos0, n)) return st;
+  if (n == 0) return DBI_OK;
+  const dbi::AttnCall c = chunk_call(layer, pos0, n, n_heads, scale, q_dev, out_dev);
+  bool prefill = false;
+  if (dbi_status st = chunk_prepare(kv, c, &prefill)) return st;
+  return chunk_launch(kv, c, prefill);
 }
 
 dbi_status append_impl(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, const float* k_dev,
@@ -251,6 +285,153 @@ dbi_status append_check(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, c
   if (dbi_status st = check_layer(kv, layer)) return st;
   if (n > 0 && (k == nullptr || v == nullptr)) return fail(DBI_ERR_INVALID, "null k or v");
   return check_rows(kv, pos0, n);
+}
+
+// ---------------------------------------------------------------------------
+// q/k/v producer: raw projections in, roped rows into the workspace, then
+// the append and attention launches of the plain entry points.
+
+struct RawQkv {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* qb;
+  const float* kb;
+  const float* vb;
+};
+
+// The producer's fp64 (cos, sin) table of a dense cache, built on its first
+// producer call with the host's libm and uploaded once. A ring needs none:
+// its keys are stored un-roped.
+dbi_status ensure_rope_table(dbi_kv* kv) {
+  const dbi::KvGeom& g = kv->geom;
+  if (g.ring || kv->store.rope_dd != nullptr) return DBI_OK;
+  if (!(kv->cfg.rope_theta > 0.0f))
+    return fail(DBI_ERR_INVALID, "the q/k/v producer needs rope_theta > 0");
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(kv->stream, &cap), "capture status");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(DBI_ERR_INVALID,
+                "the first q/k/v producer call of a handle builds its rope table and cannot be "
+                "captured; make one call before capturing");
+  std::vector<double2> tab(size_t(g.cap) * (g.hd / 2));
+  if (!dbi::rope_table_host(g, kv->cfg.rope_theta, tab.data()))
+    return fail(DBI_ERR_UNSUPPORTED, "the q/k/v producer needs an even head_dim");
+  double2* d = nullptr;
+  if (hipMalloc(reinterpret_cast<void**>(&d), tab.size() * sizeof(double2)) != hipSuccess)
+    return fail(DBI_ERR_NOMEM, "rope table allocation failed");
+  const hipError_t e = hipMemcpy(d, tab.data(), tab.size() * sizeof(double2),
+                                 hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    return hip_fail(e, "rope table upload");
+  }
+  kv->store.rope_dd = d;
+  return DBI_OK;
+}
+
+dbi_status ensure_prod(dbi_kv* kv, size_t floats) {
+  if (floats <= kv->ws.prod_floats) return DBI_OK;
+  HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+  if (kv->ws.prod) (void)hipFree(kv->ws.prod);
+  kv->ws.prod = nullptr;
+  kv->ws.prod_floats = 0;
+  if (hipMalloc(reinterpret_cast<void**>(&kv->ws.prod), floats * sizeof(float)) != hipSuccess)
+    return fail(DBI_ERR_NOMEM, "producer workspace allocation failed");
+  kv->ws.prod_floats = floats;
+  return DBI_OK;
+}
+
+dbi_status check_qkv(const dbi_kv* kv, uint32_t layer, uint32_t n_heads, const RawQkv& r,
+                     const void* out) {
+  if (dbi_status st = check_attend(kv, layer, n_heads, r.q, out)) return st;
+  if (r.k == nullptr || r.v == nullptr) return fail(DBI_ERR_INVALID, "null k or v");
+  return DBI_OK;
+}
+
+// decode_layer (model.cpp:747-771) from the projections: produce, then the
+// fused append + attention launch. Every check and allocation comes first,
+// so a failure leaves the cache as it was.
+dbi_status decode_qkv_impl(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
+                           float scale, const RawQkv& r, float* out_dev) {
+  if (dbi_status st = check_rows(kv, pos, 1)) return st;
+  if (dbi_status st = ensure_rope_table(kv)) return st;
+  const size_t qn = size_t(n_heads) * kv->geom.hd, P = size_t(kv->geom.nkv) * kv->geom.hd;
+  if (dbi_status st = ensure_prod(kv, qn + 2 * P)) return st;
+  float* qo = kv->ws.prod;  // 16-byte aligned rows (hd is a multiple of 4)
+  float* ko = qo + qn;
+  float* vo = ko + P;
+  const dbi::AttnCall c = decode_call(kv, layer, pos, n_heads, scale, qo, out_dev, ko, vo);
+  if (dbi_status st = ensure_workspace(kv, c)) return st;
+  const dbi::ProduceCall pc{1, static_cast<int>(pos), static_cast<int>(n_heads), r.q, r.k, r.v,
+                            r.qb, r.kb, r.vb, qo, ko, vo};
+  HIP_TRY(dbi::launch_produce(kv->geom, kv->store.rope_dd, pc, kv->stream), "producer launch");
+  HIP_TRY(dbi::launch_attention(kv->geom, kv->store, kv->ws, c, kv->stream), "attention launch");
+  kv->n_seen = pos + 1;
+  return DBI_OK;
+}
+
+// decode_layer_chunk (model.cpp:933-981) from the projections: produce all n
+// rows, append them, then the causal chunk attention.
+dbi_status chunk_qkv_impl(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                          uint32_t n_heads, float scale, const RawQkv& r, float* out_dev) {
+  if (dbi_status st = check_chunk(kv, pos0, n)) return st;
+  if (n == 0) return DBI_OK;
+  if (dbi_status st = ensure_rope_table(kv)) return st;
+  const size_t qn = size_t(n) * n_heads * kv->geom.hd;
+  const size_t kn = size_t(n) * kv->geom.nkv * kv->geom.hd;
+  if (dbi_status st = ensure_prod(kv, qn + 2 * kn)) return st;
+  float* qo = kv->ws.prod;
+  float* ko = qo + qn;
+  float* vo = ko + kn;
+  const dbi::AttnCall c = chunk_call(layer, pos0, n, n_heads, scale, qo, out_dev);
+  bool prefill = false;
+  if (dbi_status st = chunk_prepare(kv, c, &prefill)) return st;
+  const dbi::ProduceCall pc{static_cast<int>(n), static_cast<int>(pos0),
+                            static_cast<int>(n_heads), r.q, r.k, r.v, r.qb, r.kb, r.vb,
+                            qo, ko, vo};
+  HIP_TRY(dbi::launch_produce(kv->geom, kv->store.rope_dd, pc, kv->stream), "producer launch");
+  if (dbi_status st = append_impl(kv, layer, pos0, n, ko, vo)) return st;
+  return chunk_launch(kv, c, prefill);
+}
+
+// Host-pointer form of the producer calls: q, k, v rows, the biases that are
+// given, and the output share one staging buffer.
+dbi_status qkv_host(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, uint32_t n_heads,
+                    float scale, const RawQkv& h, float* out, bool chunk) {
+  if (dbi_status st = check_qkv(kv, layer, n_heads, h, out)) return st;
+  if (n == 0) return chunk ? check_chunk(kv, pos0, n) : DBI_OK;
+  const size_t hq = size_t(n_heads) * kv->geom.hd, hk = size_t(kv->geom.nkv) * kv->geom.hd;
+  const size_t qn = n * hq, kn = n * hk;
+  const size_t need = 2 * qn + 2 * kn + (h.qb ? hq : 0) + (h.kb ? hk : 0) + (h.vb ? hk : 0);
+  if (dbi_status st = need_staging(kv, need)) return st;
+  float* at = kv->ws.staging;
+  auto up = [&](const float* src, size_t elems, const float** dst) -> hipError_t {
+    *dst = nullptr;
+    if (src == nullptr) return hipSuccess;
+    *dst = at;
+    at += elems;
+    return hipMemcpyAsync(const_cast<float*>(*dst), src, elems * sizeof(float),
+                          hipMemcpyHostToDevice, kv->stream);
+  };
+  RawQkv d{};
+  HIP_TRY(up(h.q, qn, &d.q), "q upload");
+  HIP_TRY(up(h.k, kn, &d.k), "k upload");
+  HIP_TRY(up(h.v, kn, &d.v), "v upload");
+  HIP_TRY(up(h.qb, hq, &d.qb), "q bias upload");
+  HIP_TRY(up(h.kb, hk, &d.kb), "k bias upload");
+  HIP_TRY(up(h.vb, hk, &d.vb), "v bias upload");
+  float* od = at;
+  const dbi_status st = chunk ? chunk_qkv_impl(kv, layer, pos0, n, n_heads, scale, d, od)
+                              : decode_qkv_impl(kv, layer, pos0, n_heads, scale, d, od);
+  if (st != DBI_OK) {
+    (void)hipStreamSynchronize(kv->stream);  // the uploads read the caller's buffers
+    return st;
+  }
+  HIP_TRY(hipMemcpyAsync(out, od, qn * sizeof(float), hipMemcpyDeviceToHost, kv->stream),
+          "out readback");
+  HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+  return DBI_OK;
 }
 
 }  // namespace
@@ -528,6 +709,46 @@ dbi_status dbi_attn_chunk_async(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint3
   if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
   if (dbi_status st = check_attend(kv, layer, n_heads, q_dev, out_dev)) return st;
   return chunk_impl(kv, layer, pos0, n, n_heads, scale, q_dev, out_dev);
+}
+
+dbi_status dbi_kv_decode_qkv(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
+                             float scale, const float* q, const float* k, const float* v,
+                             const float* q_bias, const float* k_bias, const float* v_bias,
+                             float* out) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  return qkv_host(kv, layer, pos, 1, n_heads, scale, RawQkv{q, k, v, q_bias, k_bias, v_bias},
+                  out, false);
+}
+
+dbi_status dbi_kv_decode_qkv_async(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
+                                   float scale, const float* q_dev, const float* k_dev,
+                                   const float* v_dev, const float* q_bias_dev,
+                                   const float* k_bias_dev, const float* v_bias_dev,
+                                   float* out_dev) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  const RawQkv r{q_dev, k_dev, v_dev, q_bias_dev, k_bias_dev, v_bias_dev};
+  if (dbi_status st = check_qkv(kv, layer, n_heads, r, out_dev)) return st;
+  return decode_qkv_impl(kv, layer, pos, n_heads, scale, r, out_dev);
+}
+
+dbi_status dbi_kv_chunk_qkv(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                            uint32_t n_heads, float scale, const float* q, const float* k,
+                            const float* v, const float* q_bias, const float* k_bias,
+                            const float* v_bias, float* out) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  return qkv_host(kv, layer, pos0, n, n_heads, scale, RawQkv{q, k, v, q_bias, k_bias, v_bias},
+                  out, true);
+}
+
+dbi_status dbi_kv_chunk_qkv_async(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                                  uint32_t n_heads, float scale, const float* q_dev,
+                                  const float* k_dev, const float* v_dev,
+                                  const float* q_bias_dev, const float* k_bias_dev,
+                                  const float* v_bias_dev, float* out_dev) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  const RawQkv r{q_dev, k_dev, v_dev, q_bias_dev, k_bias_dev, v_bias_dev};
+  if (dbi_status st = check_qkv(kv, layer, n_heads, r, out_dev)) return st;
+  return chunk_qkv_impl(kv, layer, pos0, n, n_heads, scale, r, out_dev);
 }
 
 // ---------------------------------------------------------------------------

@@ -12,6 +12,8 @@
 //                       k_raw         [L][32][nkv*hd]     fp32 (reference order)
 //                       k_sink,v_sink [L][nkv][ns][hd]    fp32
 //   ring                rope_cs       [cap][hd/2]         float2 (cos, sin)
+//   dense (producer)    rope_dd       [cap][hd/2]         double2 (cos, sin), built on
+//                                                         the producer's first call
 // capg is the capacity rounded up to a multiple of 64 positions (the reads of
 // the attention and prefill kernels are whole 32- / 64-position pieces).
 //
@@ -104,6 +106,7 @@ struct KvStore {
   float* k_sink = nullptr;
   float* v_sink = nullptr;
   float2* rope_cs = nullptr;
+  double2* rope_dd = nullptr;
 };
 
 // Split-K workspace: partial (o, m, l) of every split of one attention call.
@@ -115,6 +118,8 @@ struct Workspace {
   float* staging = nullptr;  // device staging for host-pointer calls
   unsigned char* pinned = nullptr;  // pinned host chunk for prefix-file transfers
   size_t staging_floats = 0;
+  float* prod = nullptr;  // producer output: roped q, roped k, biased v rows
+  size_t prod_floats = 0;
 };
 
 // Ring state of one attention call (resident set of n_seen = pos + 1).
@@ -164,6 +169,29 @@ hipError_t launch_prefill(const KvGeom& g, const KvStore& s, Workspace& ws, cons
                           hipStream_t st);
 size_t attention_counters_need(const KvGeom& g, const AttnCall& c);
 bool attention_supported(const KvGeom& g, int n_heads);
+
+// One producer launch (produce.hip): rows [pos0, pos0 + rows) of raw q/k/v
+// projections (device, row-major [rows][heads*hd]) plus optional biases
+// become the roped q, roped k and biased v rows the append and attention
+// kernels take (a ring: biases only).
+struct ProduceCall {
+  int rows, pos0, n_heads;
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* q_bias;
+  const float* k_bias;
+  const float* v_bias;
+  float* q_out;
+  float* k_out;
+  float* v_out;
+};
+hipError_t launch_produce(const KvGeom& g, const double2* rope_dd, const ProduceCall& c,
+                          hipStream_t st);
+// Host table of (cos, sin) for every position < cap and pair of the head
+// dim, [cap][hd/2], with tensor::rope's fp64 expressions (ops.cpp:27-30).
+// False for an odd head dim.
+bool rope_table_host(const KvGeom& g, float theta, double2* tab);
 
 // Prefix pack/unpack between [L][len][nkv][hd] and the head-major store
 // (is_k selects the K or the V granule layout).

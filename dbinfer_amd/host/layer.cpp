@@ -63,6 +63,28 @@ bool chunk_attention(KVCache& kv, const Config& cfg, std::size_t layer, std::int
                                  attn_out));
 }
 
+bool decode_attention_qkv(KVCache& kv, const Config& cfg, std::size_t layer, std::int32_t pos,
+                          const float* q, const float* k, const float* v, const AttnBias& bias,
+                          float* attn_out) {
+  if (!kv.ok()) return false;
+  return kv.check(dbi_kv_decode_qkv(kv.handle(), static_cast<std::uint32_t>(layer),
+                                    static_cast<std::uint32_t>(pos),
+                                    static_cast<std::uint32_t>(cfg.n_heads), attn_scale(cfg), q,
+                                    k, v, bias.attn_q_bias, bias.attn_k_bias, bias.attn_v_bias,
+                                    attn_out));
+}
+
+bool chunk_attention_qkv(KVCache& kv, const Config& cfg, std::size_t layer, std::int32_t pos0,
+                         std::size_t n, const float* q, const float* k, const float* v,
+                         const AttnBias& bias, float* attn_out) {
+  if (!kv.ok()) return false;
+  return kv.check(dbi_kv_chunk_qkv(kv.handle(), static_cast<std::uint32_t>(layer),
+                                   static_cast<std::uint32_t>(pos0), static_cast<std::uint32_t>(n),
+                                   static_cast<std::uint32_t>(cfg.n_heads), attn_scale(cfg), q, k,
+                                   v, bias.attn_q_bias, bias.attn_k_bias, bias.attn_v_bias,
+                                   attn_out));
+}
+
 Result<Unit> save_kv_prefix(const KVCache& kv, const std::string& path,
                             std::span<const std::int32_t> prefix_tokens) {
   const dbi_status st = dbi_kv_prefix_save(kv.handle(), path.c_str(), prefix_tokens.data(),

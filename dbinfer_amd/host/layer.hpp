@@ -68,6 +68,27 @@ bool decode_attention(KVCache& kv, const Config& cfg, std::size_t layer, std::in
 bool chunk_attention(KVCache& kv, const Config& cfg, std::size_t layer, std::int32_t pos0,
                      std::size_t n, float* q, float* k, const float* v, float* attn_out);
 
+// The optional q/k/v projection biases of LayerWeights (model.hpp:41-43).
+struct AttnBias {
+  const float* attn_q_bias = nullptr;
+  const float* attn_k_bias = nullptr;
+  const float* attn_v_bias = nullptr;
+};
+
+// decode_attention from the raw projections, with the bias adds and the rope
+// on the device (dbi_kv_decode_qkv; model.cpp:747-771): q, k, v are not
+// modified. Same cache state and output as adding the biases on the host
+// and calling decode_attention.
+bool decode_attention_qkv(KVCache& kv, const Config& cfg, std::size_t layer, std::int32_t pos,
+                          const float* q, const float* k, const float* v, const AttnBias& bias,
+                          float* attn_out);
+
+// chunk_attention from the raw projections (dbi_kv_chunk_qkv;
+// model.cpp:933-981): bias and rope every row on the device, append, attend.
+bool chunk_attention_qkv(KVCache& kv, const Config& cfg, std::size_t layer, std::int32_t pos0,
+                         std::size_t n, const float* q, const float* k, const float* v,
+                         const AttnBias& bias, float* attn_out);
+
 // Model::save_kv_prefix / load_kv_prefix (model.hpp:292-299).
 Result<Unit> save_kv_prefix(const KVCache& kv, const std::string& path,
                             std::span<const std::int32_t> prefix_tokens);

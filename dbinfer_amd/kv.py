@@ -182,6 +182,60 @@ class HipKV:
         _check(self._lib, self._lib.dbi_attn_chunk_async(self._h, layer, pos0, n, n_heads, scale,
                                                          q_dev, out_dev))
 
+    # ---- q/k/v producer (bias + rope on the device, then append + attention)
+    def _biases(self, n_heads, q_bias, k_bias, v_bias):
+        out = []
+        for b, size in ((q_bias, n_heads * self.head_dim), (k_bias, self.pos_stride),
+                        (v_bias, self.pos_stride)):
+            if b is None:
+                out.append(None)
+            else:
+                b = _f32(b)
+                assert b.size == size
+                out.append(b)
+        return out
+
+    def decode_qkv(self, layer: int, pos: int, q, k, v, n_heads: int, scale: float,
+                   q_bias=None, k_bias=None, v_bias=None) -> np.ndarray:
+        """decode_layer's attention half from raw projections (model.cpp:747-771)."""
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        assert q.size == n_heads * self.head_dim
+        assert k.size == self.pos_stride and v.size == self.pos_stride
+        bs = self._biases(n_heads, q_bias, k_bias, v_bias)
+        out = np.empty(q.size, np.float32)
+        _check(self._lib, self._lib.dbi_kv_decode_qkv(
+            self._h, layer, pos, n_heads, scale, _ptr(q), _ptr(k), _ptr(v),
+            *[None if b is None else _ptr(b) for b in bs], _ptr(out)))
+        return out
+
+    def decode_qkv_async(self, layer: int, pos: int, n_heads: int, scale: float, q_dev: int,
+                         k_dev: int, v_dev: int, q_bias_dev, k_bias_dev, v_bias_dev,
+                         out_dev: int) -> None:
+        _check(self._lib, self._lib.dbi_kv_decode_qkv_async(
+            self._h, layer, pos, n_heads, scale, q_dev, k_dev, v_dev, q_bias_dev, k_bias_dev,
+            v_bias_dev, out_dev))
+
+    def chunk_qkv(self, layer: int, pos0: int, q, k, v, n_heads: int, scale: float,
+                  q_bias=None, k_bias=None, v_bias=None) -> np.ndarray:
+        """decode_layer_chunk's attention half from raw projections (model.cpp:933-981)."""
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        n = q.size // (n_heads * self.head_dim)
+        assert q.size == n * n_heads * self.head_dim
+        assert k.size == n * self.pos_stride and v.size == n * self.pos_stride
+        bs = self._biases(n_heads, q_bias, k_bias, v_bias)
+        out = np.empty(q.size, np.float32)
+        _check(self._lib, self._lib.dbi_kv_chunk_qkv(
+            self._h, layer, pos0, n, n_heads, scale, _ptr(q), _ptr(k), _ptr(v),
+            *[None if b is None else _ptr(b) for b in bs], _ptr(out)))
+        return out
+
+    def chunk_qkv_async(self, layer: int, pos0: int, n: int, n_heads: int, scale: float,
+                        q_dev: int, k_dev: int, v_dev: int, q_bias_dev, k_bias_dev,
+                        v_bias_dev, out_dev: int) -> None:
+        _check(self._lib, self._lib.dbi_kv_chunk_qkv_async(
+            self._h, layer, pos0, n, n_heads, scale, q_dev, k_dev, v_dev, q_bias_dev,
+            k_bias_dev, v_bias_dev, out_dev))
+
     # ---- prefix cache
     def save_prefix(self, path: str, tokens) -> None:
         t = np.ascontiguousarray(tokens, dtype=np.int32)

@@ -59,7 +59,8 @@ typedef struct dbi_kv_config {
   uint32_t n_sink;     /* ring: pinned sinks; dense int8: fp32 sink tokens */
   uint32_t window;     /* 0 = dense full-context cache, > 0 = ring of n_sink + window */
   uint32_t dtype;      /* DBI_KV_F32 or DBI_KV_INT8 */
-  float rope_theta;    /* ring only: rope base for cache-relative re-rope */
+  float rope_theta;    /* rope base: a ring's cache-relative re-rope, and the
+                          q/k/v producer's rope (dbi_kv_decode_qkv) */
 } dbi_kv_config;
 
 /* Message of the last failed call on this thread ("" if none). */
@@ -146,6 +147,43 @@ dbi_status dbi_attn_chunk(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
 dbi_status dbi_attn_chunk_async(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
                                 uint32_t n_heads, float scale, const float* q_dev,
                                 float* out_dev);
+
+/* The attention half of Model::decode_layer from the q/k/v projections
+ * (model.cpp:747-771), on the device. Adds the biases (each may be null, as
+ * the reference's optional attn_*_bias; model.cpp:747-755), ropes q and k at
+ * pos on dense layouts (tensor::rope's NeoX pairs in fp64, ops.cpp:19-38;
+ * a ring appends k un-roped and ropes inside attention, model.cpp:662-700),
+ * then appends k/v at pos and attends, as dbi_kv_decode does. q, out
+ * [n_heads*head_dim], k, v [n_kv_heads*head_dim], biases the same sizes; the
+ * inputs are not modified. Appended rows are bit-identical to what the
+ * reference appends after its host-side bias and rope. Needs
+ * rope_theta > 0 for dense layouts; the first such call on a handle builds
+ * its (cos, sin) table and must not be under graph capture. */
+dbi_status dbi_kv_decode_qkv(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
+                             float scale, const float* q, const float* k, const float* v,
+                             const float* q_bias, const float* k_bias, const float* v_bias,
+                             float* out);
+dbi_status dbi_kv_decode_qkv_async(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
+                                   float scale, const float* q_dev, const float* k_dev,
+                                   const float* v_dev, const float* q_bias_dev,
+                                   const float* k_bias_dev, const float* v_bias_dev,
+                                   float* out_dev);
+
+/* The attention half of Model::decode_layer_chunk from the projections
+ * (model.cpp:933-981), on the device: bias and rope every row c at
+ * pos0 + c (model.cpp:935-952), append all n rows (:953), then the causal
+ * chunk attention of dbi_attn_chunk. q, out [n][n_heads*head_dim], k, v
+ * [n][n_kv_heads*head_dim]; each bias (or null) is one row's worth and is
+ * added to every row. Dense layouts only. */
+dbi_status dbi_kv_chunk_qkv(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                            uint32_t n_heads, float scale, const float* q, const float* k,
+                            const float* v, const float* q_bias, const float* k_bias,
+                            const float* v_bias, float* out);
+dbi_status dbi_kv_chunk_qkv_async(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
+                                  uint32_t n_heads, float scale, const float* q_dev,
+                                  const float* k_dev, const float* v_dev,
+                                  const float* q_bias_dev, const float* k_bias_dev,
+                                  const float* v_bias_dev, float* out_dev);
 
 /* Model::save_kv_prefix (model.hpp:292-293, model.cpp:1072-1107): writes the
  * DBKVCACH v1 file of positions [0, len) with the token ids. Dense fp32 only. */

@@ -275,6 +275,55 @@ void test_chunk_parity(KvDtype dt) {
   okv_destroy(o);
 }
 
+// decode_layer / decode_layer_chunk from the raw projections with biases
+// (model.cpp:747-755, 935-953): the device producer against the host flow
+// (bias adds, rope, then decode_attention / chunk_attention) on a second
+// cache; outputs bitwise equal, since the device rope reproduces the host's
+void test_producer_parity(KvPolicy pol, const Config& cfg, std::size_t steps, const char* name) {
+  const std::size_t cap = pol.window ? 0 : steps + 8;
+  KVCache dev(1, cap, cfg.n_kv_heads, cfg.head_dim, pol, cfg.rope_theta);
+  KVCache host(1, cap, cfg.n_kv_heads, cfg.head_dim, pol, cfg.rope_theta);
+  const std::size_t qn = cfg.n_heads * cfg.head_dim, kn = cfg.n_kv_heads * cfg.head_dim;
+  Lcg rng{0xB1A5 + steps};
+  std::vector<float> qb(qn), kb(kn), vb(kn);
+  for (auto& x : qb) x = rng.next();
+  for (auto& x : kb) x = rng.next();
+  for (auto& x : vb) x = rng.next();
+  const dbinfer_amd::model::AttnBias bias{qb.data(), kb.data(), vb.data()};
+  auto biased = [](std::vector<float> x, const std::vector<float>& b) {
+    for (std::size_t i = 0; i < x.size(); ++i) x[i] += b[i % b.size()];
+    return x;
+  };
+  bool ok = dev.ok() && host.ok(), same = true;
+  for (std::size_t t = 0; t < steps && ok; ++t) {
+    std::vector<float> q(qn), k(kn), v(kn), oa(qn), ob(qn);
+    for (auto& x : q) x = rng.next();
+    for (auto& x : k) x = rng.next();
+    for (auto& x : v) x = rng.next();
+    const auto pos = static_cast<std::int32_t>(t);
+    ok = dbinfer_amd::model::decode_attention_qkv(dev, cfg, 0, pos, q.data(), k.data(), v.data(),
+                                                  bias, oa.data());
+    std::vector<float> q1 = biased(q, qb), k1 = biased(k, kb), v1 = biased(v, vb);
+    ok = ok && dbinfer_amd::model::decode_attention(host, cfg, 0, pos, q1.data(), k1.data(),
+                                                    v1.data(), ob.data());
+    same = same && std::memcmp(oa.data(), ob.data(), qn * 4) == 0;
+  }
+  if (!pol.window && ok) {  // one chunk after the decode steps
+    const std::size_t n = 6, pos0 = steps;
+    std::vector<float> q(n * qn), k(n * kn), v(n * kn), oa(n * qn), ob(n * qn);
+    for (auto& x : q) x = rng.next();
+    for (auto& x : k) x = rng.next();
+    for (auto& x : v) x = rng.next();
+    ok = dbinfer_amd::model::chunk_attention_qkv(dev, cfg, 0, static_cast<std::int32_t>(pos0), n,
+                                                 q.data(), k.data(), v.data(), bias, oa.data());
+    std::vector<float> q1 = biased(q, qb), k1 = biased(k, kb), v1 = biased(v, vb);
+    ok = ok && dbinfer_amd::model::chunk_attention(host, cfg, 0, static_cast<std::int32_t>(pos0),
+                                                   n, q1.data(), k1.data(), v1.data(), ob.data());
+    same = same && std::memcmp(oa.data(), ob.data(), n * qn * 4) == 0;
+  }
+  check(ok && same, std::string("q/k/v producer == host bias + rope flow (bitwise): ") + name);
+}
+
 void test_prefix_cache() {
   const Config cfg{14, 2, 64, 1e6f};
   const std::size_t L = 3, cap = 64, n = 20;
@@ -372,6 +421,9 @@ int main(int argc, char** argv) {
     test_decode_layer_parity({4, 16, KvDtype::Int8}, {28, 4, 128, 1e6f}, 2, 50, "ring int8 gqa7 hd128");
     test_chunk_parity(KvDtype::F32);
     test_chunk_parity(KvDtype::Int8);
+    test_producer_parity({0, 0, KvDtype::F32}, {32, 8, 128, 1e6f}, 20, "dense fp32 gqa4 hd128");
+    test_producer_parity({4, 0, KvDtype::Int8}, {24, 8, 128, 5e5f}, 40, "dense int8 gqa3 hd128");
+    test_producer_parity({4, 16, KvDtype::F32}, {28, 4, 128, 1e6f}, 30, "ring fp32 gqa7 hd128");
     test_prefix_cache();
     test_speculative_rollback();
   }
