@@ -356,6 +356,26 @@ dbi_status decode_qkv_impl(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_
                            float scale, const RawQkv& r, float* out_dev) {
   if (dbi_status st = check_rows(kv, pos, 1)) return st;
   if (dbi_status st = ensure_rope_table(kv)) return st;
+  const double2* rope_row =
+      kv->geom.ring ? nullptr : kv->store.rope_dd + size_t(pos) * (kv->geom.hd / 2);
+  // one launch: the attention kernel produces q, k and v itself (its row and
+  // bias loads are 16 bytes per lane)
+  const uintptr_t addr_bits = reinterpret_cast<uintptr_t>(r.q) | reinterpret_cast<uintptr_t>(r.k) |
+                              reinterpret_cast<uintptr_t>(r.v) | reinterpret_cast<uintptr_t>(r.qb) |
+                              reinterpret_cast<uintptr_t>(r.kb) | reinterpret_cast<uintptr_t>(r.vb);
+  if ((addr_bits & 15) == 0) {
+    dbi::AttnCall c = decode_call(kv, layer, pos, n_heads, scale, r.q, out_dev, r.k, r.v);
+    c.q_bias = r.qb;
+    c.k_bias = r.kb;
+    c.v_bias = r.vb;
+    c.rope_row = rope_row;
+    if (dbi_status st = ensure_workspace(kv, c)) return st;
+    HIP_TRY(dbi::launch_attention(kv->geom, kv->store, kv->ws, c, kv->stream),
+            "attention launch");
+    kv->n_seen = pos + 1;
+    return DBI_OK;
+  }
+  // otherwise the producer kernel writes aligned rows for the fused step
   const size_t qn = size_t(n_heads) * kv->geom.hd, P = size_t(kv->geom.nkv) * kv->geom.hd;
   if (dbi_status st = ensure_prod(kv, qn + 2 * P)) return st;
   float* qo = kv->ws.prod;  // 16-byte aligned rows (hd is a multiple of 4)

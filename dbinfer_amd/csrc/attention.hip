@@ -77,6 +77,10 @@ struct AttnParams {
   const float2* rope;
   int rope_rows;
   const float* q;
+  // decode from raw projections (rows == 1): q bias [n_heads*hd] or null, and
+  // the (cos, sin) row of the decode position for a dense rope, or null
+  const float* qb;
+  const double2* qcs;
   float* out;
   float* part;
   unsigned* cnt;  // split arrivals per (row, kv head), zero between launches
@@ -153,6 +157,39 @@ __device__ __forceinline__ float swap16_sum(float a, float b) {
 // Raw v_exp_f32 (2^x). Softmax weights below 2^-126 are far under the
 // output tolerance, so the denormal-range handling of exp2f is not needed.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroup barrier that waits for this wave's LDS operations only (no
+// wait on outstanding vector-memory loads, which __syncthreads would add).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// tensor::rope's fp64 NeoX rotation of one pair (ops.cpp:31-34): products
+// and sums rounded one by one, as the reference's scalar code does
+__device__ __forceinline__ void rope_pair(float& a, float& b, double2 cs) {
+#pragma clang fp contract(off)
+  const double x = static_cast<double>(a) * cs.x - static_cast<double>(b) * cs.y;
+  const double y = static_cast<double>(b) * cs.x + static_cast<double>(a) * cs.y;
+  a = static_cast<float>(x);
+  b = static_cast<float>(y);
+}
+
+// Element d of one head row as the reference's host code hands it to the
+// cache (model.cpp:747-763): x + bias (one fp32 add; no add without a
+// bias), then, with a (cos, sin) row, the rope of its pair (d, d +- hd/2).
+template <int HD>
+__device__ __forceinline__ float produced(const float* x, const float* bias, const double2* cs,
+                                          int d) {
+  constexpr int H2 = HD / 2;
+  const int j = d % H2;
+  float a = x[j], b = x[j + H2];
+  if (bias != nullptr) {
+    a += bias[j];
+    b += bias[j + H2];
+  }
+  if (cs != nullptr) rope_pair(a, b, cs[j]);
+  return d < H2 ? a : b;
+}
 
 // Raw buffer resources (gfx9 descriptor word 3 = 0x00020000: 32-bit raw
 // data, bounds-checked against num_records bytes; reads past it return 0).
@@ -232,6 +269,12 @@ __device__ __forceinline__ float treduce(const float* a) {
 struct AppendArgs {
   const float* k;  // new row, device [nkv][hd]; nullptr: no append
   const float* v;
+  // raw-projection step: the row is k + kb roped by kcs (dense) and v + vb;
+  // each may be null (no bias / no rope); prod = any of them set
+  const float* kb;
+  const float* vb;
+  const double2* kcs;
+  int prod;
   int slot;        // storage row (dense: pos; ring: slot_for(pos)); -1: no append
   int pos;
   int nkv, n_sink, capg, ng;
@@ -312,9 +355,9 @@ __device__ __forceinline__ void finish(const AttnParams& P, float (&s_o)[kWaves]
 // records, then the fp32 sink positions, when the layout has them
 // (model.cpp:612-614), are attended as further entries with a running max.
 // Records are read at device coherence.
-template <int HD, int G>
+template <int HD, int G, bool PROD>
 __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs& A, int kh,
-                                           int qrow, int wave, int lane) {
+                                           int qrow, int wave, int lane, const float* qw) {
   constexpr int DPL = HD / 64;
   constexpr int kSinkBatch = 8;
   constexpr int kSC1 = 16;  // cache policy: agent-coherent load
@@ -354,18 +397,31 @@ __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs
       const int p = min(p0 + b, ns - 1);
       const bool fresh = A.slot >= 0 && p == A.pos;
       const size_t at = (static_cast<size_t>(kh) * P.n_sink + p) * HD + lane * DPL;
-      const float* kr = fresh ? A.k + kh * HD + lane * DPL : P.ksink + at;
-      const float* vr = fresh ? A.v + kh * HD + lane * DPL : P.vsink + at;
+      if (PROD && fresh && A.prod) {  // raw projections: the produced row
+        const float* kb = A.kb != nullptr ? A.kb + kh * HD : nullptr;
+        const float* vb = A.vb != nullptr ? A.vb + kh * HD : nullptr;
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) {
-        kd[b][e] = kr[e];
-        vd[b][e] = vr[e];
+        for (int e = 0; e < DPL; ++e) {
+          kd[b][e] = produced<HD>(A.k + kh * HD, kb, A.kcs, lane * DPL + e);
+          vd[b][e] = produced<HD>(A.v + kh * HD, vb, nullptr, lane * DPL + e);
+        }
+      } else {
+        const float* kr = fresh ? A.k + kh * HD + lane * DPL : P.ksink + at;
+        const float* vr = fresh ? A.v + kh * HD + lane * DPL : P.vsink + at;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) {
+          kd[b][e] = kr[e];
+          vd[b][e] = vr[e];
+        }
       }
     }
   };
   if (ns > 0) {
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) qd[e] = P.q[h * HD + lane * DPL + e] * P.qscale;
+    for (int e = 0; e < DPL; ++e)
+      // raw projections: the produced, scaled q row kept in LDS (qw, the
+      // same bits as q * qscale); otherwise q itself
+      qd[e] = PROD ? qw[lane * DPL + e] : P.q[h * HD + lane * DPL + e] * P.qscale;
     sink_rows(0);
   }
 
@@ -458,7 +514,7 @@ struct KGroupStage {
 // v_dev are 16-byte aligned) and a wave's channels of the group's 32 staged
 // raw rows into its `raw` share ([32][CPW]). The compiler does not track
 // these loads: the consumers wait for them explicitly.
-template <int HD, int KIND>
+template <int HD, int KIND, bool PROD>
 struct FusedAppend {
   static constexpr bool kInt8 = (KIND == kI8Dense || KIND == kI8Ring);
   static constexpr int NB = HD / kBlock;
@@ -481,12 +537,67 @@ struct FusedAppend {
     const int hl = lane % (2 * Q);    // lanes past 2Q (hd 64) repeat into row[2 HD, 4 HD)
     const float* src = (hl < Q ? A.k : A.v) + kh * HD + (hl % Q) * 4;
     __builtin_amdgcn_global_load_lds(src, row, 16, 0, 0);
+    if (PROD && A.prod) {  // raw projections: the (cos, sin) row and the biases too
+      if (A.kcs != nullptr)
+        __builtin_amdgcn_global_load_lds(A.kcs + lane % (HD / 2), row + 256, 16, 0, 0);
+      if (A.kb != nullptr || A.vb != nullptr) {  // a missing one is loaded but not added
+        const float* kb = A.kb != nullptr ? A.kb : A.vb;
+        const float* vb = A.vb != nullptr ? A.vb : A.kb;
+        __builtin_amdgcn_global_load_lds((hl < Q ? kb : vb) + kh * HD + (hl % Q) * 4, row + 512,
+                                         16, 0, 0);
+      }
+    }
   }
 
-  // dense int8, wave < RW: its raw share (LDS-direct) and its channels of
-  // the new K row (returned; lane l holds channel l % CPW of the share)
-  __device__ __forceinline__ static float load_share(const AppendArgs& A, int kh, int wave,
-                                                     int lane, float* raw) {
+  // raw projections, owner wave, after wait_loads(): the row in LDS becomes
+  // k + kb roped and v + vb, exactly as produced() computes each element
+  __device__ __forceinline__ static void produce_row(const AppendArgs& A, int lane, float* row) {
+    constexpr int H2 = HD / 2;
+    const float* bias = row + 512;  // kb [0, HD), vb [HD, 2 HD)
+    if (lane < H2) {
+      float a = row[lane], b = row[lane + H2];
+      if (A.kb != nullptr) {
+        a += bias[lane];
+        b += bias[lane + H2];
+      }
+      if (A.kcs != nullptr) rope_pair(a, b, reinterpret_cast<const double2*>(row + 256)[lane]);
+      row[lane] = a;
+      row[lane + H2] = b;
+    }
+    if (A.vb != nullptr && 2 * lane < HD) {
+      row[HD + 2 * lane] += bias[HD + 2 * lane];
+      row[HD + 2 * lane + 1] += bias[HD + 2 * lane + 1];
+    }
+    wave_sync();
+  }
+
+  // the loaded inputs of a share's channel of the new K row: the value
+  // (raw projections: the pair's raw values and biases and its (cos, sin),
+  // combined only after the wait, so no wait stalls the share's loads)
+  struct ShareIn {
+    float x0, x1, b0, b1;
+    double2 cs;
+  };
+  __device__ __forceinline__ static float share_value(const AppendArgs& A, const ShareIn& in,
+                                                      int d) {
+    if constexpr (PROD) {
+      if (A.prod) {
+        float a = in.x0, b = in.x1;
+        if (A.kb != nullptr) {
+          a += in.b0;
+          b += in.b1;
+        }
+        if (A.kcs != nullptr) rope_pair(a, b, in.cs);
+        return d % HD < HD / 2 ? a : b;
+      }
+    }
+    return in.x0;
+  }
+
+  // dense int8, wave < RW: its raw share (LDS-direct) and its channel of
+  // the new K row (lane l holds channel l % CPW of the share)
+  __device__ __forceinline__ static ShareIn load_share(const AppendArgs& A, int kh, int wave,
+                                                       int lane, float* raw) {
     constexpr int LPRW = CPW / 4, RPI = 64 / LPRW;  // lanes per share row, rows per load
     const size_t P_ = static_cast<size_t>(A.nkv) * HD;
     const float* src = A.k_raw + static_cast<size_t>(lane / LPRW) * P_ + kh * HD + wave * CPW +
@@ -494,7 +605,22 @@ struct FusedAppend {
 #pragma unroll
     for (int m = 0; m < kKGroup / RPI; ++m)
       __builtin_amdgcn_global_load_lds(src + m * RPI * P_, raw + m * RPI * CPW, 16, 0, 0);
-    return A.k[kh * HD + wave * CPW + lane % CPW];
+    const int d = wave * CPW + lane % CPW;
+    ShareIn in{};
+    if (PROD && A.prod) {
+      const int j = d % (HD / 2);
+      const float* x = A.k + kh * HD;
+      in.x0 = x[j];
+      in.x1 = x[j + HD / 2];
+      if (A.kb != nullptr) {
+        in.b0 = A.kb[kh * HD + j];
+        in.b1 = A.kb[kh * HD + j + HD / 2];
+      }
+      if (A.kcs != nullptr) in.cs = A.kcs[j];
+    } else {
+      in.x0 = A.k[kh * HD + d];
+    }
+    return in;
   }
 
   // dense int8, wave < RW, after wait_loads(): requantize_kgroup
@@ -505,10 +631,11 @@ struct FusedAppend {
   // max_f skips as it skips NaN inputs) and their codes are neither
   // attended (masked positions) nor flushed.
   __device__ __forceinline__ static void requant_share(const AppendArgs& A, int wave, int lane,
-                                                       float knew, float* raw,
+                                                       const ShareIn& in, float* raw,
                                                        KGroupStage& kg) {
     const int within = A.pos % kKGroup, first = A.pos - within;
     const int c = lane % CPW, rb = lane / CPW;
+    const float knew = share_value(A, in, wave * CPW + c);
     if (lane < CPW) raw[within * CPW + c] = knew;
     wave_sync();
     float x[RPL];
@@ -665,7 +792,7 @@ struct FusedAppend {
   }
 };
 
-template <int HD, int G, int KIND>
+template <int HD, int G, int KIND, bool PROD>
 __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, const AppendArgs A) {
   using C = Cfg<HD, G, KIND>;
   constexpr int LPR = C::LPR, RPW = C::RPW, NSG = C::NSG, NGC = C::NGC, NS = C::NS;
@@ -687,7 +814,9 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
   // dense int8 fused step: each head group's copy of the group's raw K rows
   // fused step inputs, per head group: the new K and V rows, and (dense
   // int8) the group's raw K rows
-  __shared__ __align__(16) float s_row[C::NHG][256];
+  // ([0, 256): K and V rows; raw projections: [256, 512) the (cos, sin)
+  // row, [512, 768) the K and V biases)
+  __shared__ __align__(16) float s_row[C::NHG][PROD ? 768 : 256];
   __shared__ __align__(16) float s_raw[KIND == kI8Dense ? kWaves / 2 : 1][KIND == kI8Dense ? kKGroup * HD / (kWaves / 2) : 1];
   __shared__ __align__(16) uint8_t s_kgbuf[KIND == kI8Dense ? sizeof(KGroupStage) : 16];
   KGroupStage& s_kg = *reinterpret_cast<KGroupStage*>(s_kgbuf);
@@ -821,6 +950,24 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
   // before the first chunk's: vector loads return in order, so q issued last
   // would hold QK back until the whole chunk (V included) had arrived.
   float4 qa[GW], qc[GW], cq[2];
+  // Raw projections (PROD, decode): the q bias of the lane's dims and the
+  // (cos, sin) of its 4 pairs load with q and are applied with the scaling
+  // below (bias, then the fp64 rope of every head the lane holds)
+  float4 qba[GW], qbc[GW];
+  double2 qt[4];
+  const bool q_bias = PROD && P.qb != nullptr, q_rope = PROD && !kRing && P.qcs != nullptr;
+  if (q_bias) {
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      const float* bg = P.qb + (kh * G + min(g0 + g, G - 1)) * HD;
+      qba[g] = *reinterpret_cast<const float4*>(bg + 4 * c);
+      qbc[g] = *reinterpret_cast<const float4*>(bg + HD / 2 + 4 * c);
+    }
+  }
+  if (q_rope) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) qt[t] = P.qcs[4 * c + t];
+  }
   {
     const float* qb = P.q + (static_cast<size_t>(qrow) * P.n_heads + kh * G) * HD;
     if constexpr (kRing) {
@@ -848,7 +995,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
   const int app_rel = app_chunk - split * P.chunks_per_split;
   const bool app_owner = app_here && wl == app_rel % WPG;  // wave-uniform
   const bool app_first = app_rel / WPG == 0;
-  using App = FusedAppend<HD, KIND>;
+  using App = FusedAppend<HD, KIND, PROD>;
   float* app_row = s_row[wave / WPG];
   constexpr bool kShare = KIND == kI8Dense;
   const bool app_share = kShare && app_here && wave < App::RW;  // wave-uniform
@@ -859,7 +1006,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
       __syncthreads();
     }
   }
-  float app_knew = 0.0f;
+  typename App::ShareIn app_knew{};
   if (app_share) app_knew = App::load_share(A, kh, wave, lane, app_raw);
   if (app_owner && app_first) App::load_row(A, kh, lane, app_row);
   __builtin_amdgcn_sched_barrier(0);
@@ -881,14 +1028,25 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
     // a head group's padding head (odd G) gets q = 0 and is never stored
     const bool hv = g0 + g < G;
     float x[8] = {qa[g].x, qa[g].y, qa[g].z, qa[g].w, qc[g].x, qc[g].y, qc[g].z, qc[g].w};
+    if (q_bias) {
+      const float b[8] = {qba[g].x, qba[g].y, qba[g].z, qba[g].w,
+                          qbc[g].x, qbc[g].y, qbc[g].z, qbc[g].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] += b[e];
+    }
+    if (q_rope) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) rope_pair(x[t], x[4 + t], qt[t]);
+    }
     if constexpr (kRing) {
       const float cv[4] = {cq[0].x, cq[0].z, cq[1].x, cq[1].z};
       const float sv[4] = {cq[0].y, cq[0].w, cq[1].y, cq[1].w};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const float u = x[t], w = x[4 + t];
-        x[t] = u * cv[t] - w * sv[t];
-        x[4 + t] = w * cv[t] + u * sv[t];
+        // explicit fused forms: every instance rounds the same way
+        x[t] = fmaf(u, cv[t], -(w * sv[t]));
+        x[4 + t] = fmaf(w, cv[t], u * sv[t]);
       }
     }
 #pragma unroll
@@ -929,6 +1087,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
     const int app_r = (app_pc & 15) % RPW, app_i = (app_pc & 15) / RPW, app_gs = app_pc >> 4;
     if (app_now) {
       App::wait_loads();
+      if (PROD && A.prod) App::produce_row(A, lane, app_row);
       App::stage_row(A, lane, s_app, app_row);
       if constexpr (kShare) App::await_shares(s_kg);
       if constexpr (KIND == kI8Dense) {
@@ -1013,8 +1172,8 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const float a = kx[t], b = kx[4 + t];
-            kx[t] = a * cv[t] - b * sv[t];
-            kx[4 + t] = b * cv[t] + a * sv[t];
+            kx[t] = fmaf(a, cv[t], -(b * sv[t]));
+            kx[4 + t] = fmaf(b, cv[t], a * sv[t]);
           }
         }
 #pragma unroll
@@ -1200,7 +1359,12 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
       s_last = last;
     }
     __syncthreads();
-    if (s_last) merge_last<HD, G>(P, A, kh, qrow, wave, lane);
+    // (wave g merges head g; its scaled q row in s_qw, dense int8 only,
+    // belongs to the first wave of head g's group)
+    if (s_last)
+      merge_last<HD, G, PROD>(P, A, kh, qrow, wave, lane,
+                              &s_qw[KIND == kI8Dense ? (min(wave, G - 1) / GW) * WPG : 0]
+                                   [KIND == kI8Dense ? min(wave, G - 1) % GW : 0][0]);
   }
   if (app_owner && g0 == 0) App::flush(A, kh, lane, s_app, s_kg, app_row);
 }
@@ -1208,40 +1372,43 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
 // ---------------------------------------------------------------------------
 // dispatch
 
+// PROD: the decode step from raw projections (bias and rope inside the
+// launch); a separate instance, so the plain path carries none of it
 template <int HD, int G, int KIND>
-void* kernel_for() {
-  return reinterpret_cast<void*>(&attn_kernel<HD, G, KIND>);
+void* kernel_for(bool prod) {
+  return prod ? reinterpret_cast<void*>(&attn_kernel<HD, G, KIND, true>)
+              : reinterpret_cast<void*>(&attn_kernel<HD, G, KIND, false>);
 }
 
 template <int HD, int KIND>
-void* pick_g(int G) {
+void* pick_g(int G, bool prod) {
   switch (G) {
-    case 1: return kernel_for<HD, 1, KIND>();
-    case 2: return kernel_for<HD, 2, KIND>();
-    case 3: return kernel_for<HD, 3, KIND>();
-    case 4: return kernel_for<HD, 4, KIND>();
-    case 5: return kernel_for<HD, 5, KIND>();
-    case 6: return kernel_for<HD, 6, KIND>();
-    case 7: return kernel_for<HD, 7, KIND>();
-    case 8: return kernel_for<HD, 8, KIND>();
+    case 1: return kernel_for<HD, 1, KIND>(prod);
+    case 2: return kernel_for<HD, 2, KIND>(prod);
+    case 3: return kernel_for<HD, 3, KIND>(prod);
+    case 4: return kernel_for<HD, 4, KIND>(prod);
+    case 5: return kernel_for<HD, 5, KIND>(prod);
+    case 6: return kernel_for<HD, 6, KIND>(prod);
+    case 7: return kernel_for<HD, 7, KIND>(prod);
+    case 8: return kernel_for<HD, 8, KIND>(prod);
     default: return nullptr;
   }
 }
 
 template <int HD>
-void* pick_kind(int kind, int G) {
+void* pick_kind(int kind, int G, bool prod) {
   switch (kind) {
-    case kF32Dense: return pick_g<HD, kF32Dense>(G);
-    case kI8Dense: return pick_g<HD, kI8Dense>(G);
-    case kF32Ring: return pick_g<HD, kF32Ring>(G);
-    case kI8Ring: return pick_g<HD, kI8Ring>(G);
+    case kF32Dense: return pick_g<HD, kF32Dense>(G, prod);
+    case kI8Dense: return pick_g<HD, kI8Dense>(G, prod);
+    case kF32Ring: return pick_g<HD, kF32Ring>(G, prod);
+    case kI8Ring: return pick_g<HD, kI8Ring>(G, prod);
     default: return nullptr;
   }
 }
 
-void* pick_kernel(int hd, int kind, int G) {
-  if (hd == 64) return pick_kind<64>(kind, G);
-  if (hd == 128) return pick_kind<128>(kind, G);
+void* pick_kernel(int hd, int kind, int G, bool prod = false) {
+  if (hd == 64) return pick_kind<64>(kind, G, prod);
+  if (hd == 128) return pick_kind<128>(kind, G, prod);
   return nullptr;
 }
 
@@ -1308,7 +1475,9 @@ size_t attention_workspace_need(const KvGeom& g, const AttnCall& c) {
 hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, const AttnCall& c,
                             hipStream_t st) {
   const int G = c.n_heads / g.nkv;
-  void* fn = pick_kernel(g.hd, kind_of(g), G);
+  const bool prod = c.rows == 1 && (c.q_bias != nullptr || c.k_bias != nullptr ||
+                                    c.v_bias != nullptr || c.rope_row != nullptr);
+  void* fn = pick_kernel(g.hd, kind_of(g), G, prod);
   if (fn == nullptr || !g.tiled) return hipErrorNotSupported;
   AttnParams p{};
   const size_t layer_heads = static_cast<size_t>(c.layer) * g.nkv;
@@ -1352,6 +1521,10 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
   p.direct = pl.merge ? 0 : 1;
   p.chunks_per_split = pl.chunks_per_split;
   p.qscale = c.scale * kLog2e;
+  if (c.rows == 1) {
+    p.qb = c.q_bias;
+    p.qcs = c.rope_row;
+  }
   AppendArgs a{};
   a.slot = -1;
   if (c.app_slot >= 0 && c.app_k != nullptr && c.app_v != nullptr && c.rows == 1) {
@@ -1359,6 +1532,10 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
     a.v = c.app_v;
     a.slot = c.app_slot;
     a.pos = c.app_pos;
+    a.kb = c.k_bias;
+    a.vb = c.v_bias;
+    a.kcs = c.rope_row;
+    a.prod = c.k_bias != nullptr || c.v_bias != nullptr || c.rope_row != nullptr;
     a.nkv = g.nkv;
     a.n_sink = g.n_sink;
     a.capg = g.capg;

@@ -146,6 +146,13 @@ struct AttnCall {
   const float* app_v = nullptr;
   int app_slot = -1;
   int app_pos = 0;
+  // decode from raw projections (rows == 1): q is the raw q and app_k/app_v
+  // the raw k/v; each bias (or null) is added, and with rope_row (the
+  // (cos, sin) row of the position, dense layouts) q and k are roped
+  const float* q_bias = nullptr;
+  const float* k_bias = nullptr;
+  const float* v_bias = nullptr;
+  const double2* rope_row = nullptr;
 };
 
 // Launchers (return a hipError_t of the launch).

@@ -157,3 +157,60 @@ def test_split_merge_is_stable_under_load(dtype):
         bad = [r for r in range(1, rounds) if not torch.equal(out[r], first)]
         assert not bad, f"rounds differing from the first: {bad[:10]}"
         kv.close()
+
+
+@pytest.mark.parametrize("dtype,n_sink,window,bias", [(INT8, 4, 0, False), (F32, 0, 0, True),
+                                                      (INT8, 4, 64, True)])
+def test_producer_step_graph_replay(dtype, n_sink, window, bias):
+    """dbi_kv_decode_qkv_async (raw projections; bias and rope inside the
+    attention launch) captured for every layer: each replay, with eager work
+    in between, equals the eager step bit for bit."""
+    torch = pytest.importorskip("torch")
+    L, nh, nkv, hd, ctx = 2, 24, 8, 128, 1200
+    P, pos = nkv * hd, ctx - 1
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(13)
+        K = torch.randn(L, ctx, P, device="cuda", generator=g)
+        V = torch.randn(L, ctx, P, device="cuda", generator=g)
+        q = torch.randn(L, nh * hd, device="cuda", generator=g)
+        b = torch.randn(L, nh * hd + 2 * P, device="cuda", generator=g)
+        kv = HipKV(L, ctx, nkv, hd, n_sink, window, dtype, 1e6)
+        kv.set_stream(stream.cuda_stream)
+        for l in range(L):
+            kv.append_async(l, 0, pos, K[l].data_ptr(), V[l].data_ptr())
+        out = torch.zeros(L, nh * hd, device="cuda")
+
+        def bp(l):
+            if not bias:
+                return [None] * 3
+            return [b[l, :nh * hd].data_ptr(), b[l, nh * hd:nh * hd + P].data_ptr(),
+                    b[l, nh * hd + P:].data_ptr()]
+
+        def step():
+            for l in range(L):
+                kv.decode_qkv_async(l, pos, nh, scale, q[l].data_ptr(), K[l, pos].data_ptr(),
+                                    V[l, pos].data_ptr(), *bp(l), out[l].data_ptr())
+
+        step()  # the first producer call builds the rope table (not under capture)
+        torch.cuda.synchronize()
+        eager = out.clone()
+        graph = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(stream)
+        with torch.cuda.graph(graph, stream=cap):
+            kv.set_stream(cap.cuda_stream)
+            step()
+        kv.set_stream(stream.cuda_stream)
+        torch.cuda.synchronize()
+        for r in range(4):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {r}"
+            other = torch.empty_like(out)
+            kv.attend_async(0, pos, nh, scale, q[1].data_ptr(), other[0].data_ptr())
+            torch.cuda.synchronize()
+        kv.close()

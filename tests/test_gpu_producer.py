@@ -194,6 +194,36 @@ def test_qkv_async_matches_host_calls():
     b.close()
 
 
+def test_decode_qkv_unaligned_inputs_take_the_producer_kernel():
+    """Rows that are not 16-byte aligned go through the producer kernel and
+    the plain fused step; the result is the same bits as the one-launch path."""
+    torch = pytest.importorskip("torch")
+    nh, nkv, hd, theta, steps = 24, 8, 128, 5e5, 6
+    P, Q = nkv * hd, nh * hd
+    a = HipKV(1, 64, nkv, hd, 4, 0, INT8, theta)
+    b = HipKV(1, 64, nkv, hd, 4, 0, INT8, theta)
+    qb, kb, vb = normal(650, Q), normal(651, P), normal(652, P)
+    q, k, v = normal(653, steps, Q), normal(654, steps, P), normal(655, steps, P)
+    sc = float(scale_of(hd))
+    # one extra float in front of every array: device pointers 4 bytes past alignment
+    T = lambda x: torch.from_numpy(np.concatenate([[0.0], x.reshape(-1)]).astype(np.float32)).cuda()  # noqa: E731
+    tq, tk, tv, tqb, tkb, tvb = T(q), T(k), T(v), T(qb), T(kb), T(vb)
+    out = torch.zeros(Q, device="cuda")
+    torch.cuda.synchronize()
+    f = 4  # bytes to the first real element
+    for t in range(steps):
+        want = a.decode_qkv(0, t, q[t], k[t], v[t], nh, sc, qb, kb, vb)
+        b.decode_qkv_async(0, t, nh, sc, tq.data_ptr() + f + 4 * Q * t, tk.data_ptr() + f + 4 * P * t,
+                           tv.data_ptr() + f + 4 * P * t, tqb.data_ptr() + f, tkb.data_ptr() + f,
+                           tvb.data_ptr() + f, out.data_ptr())
+        b.sync()
+        same_bits(out.cpu().numpy(), want, f"unaligned step {t}")
+    for name in store_names(INT8, 0, 4):
+        same_bits(b.export(name, 0), a.export(name, 0), f"store {name}")
+    a.close()
+    b.close()
+
+
 def test_qkv_errors_leave_state():
     nh, nkv, hd = 8, 2, 64
     P, Q = nkv * hd, nh * hd
