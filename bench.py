@@ -352,6 +352,63 @@ def run_configs(torch, HipKV, F32, INT8, args):
         print(json.dumps(res), flush=True)
 
 
+def run_ctx_sweep(torch, HipKV, F32, INT8, args):
+    """Config 3's shape over the target context range (8k-32k): one JSON line
+    per (context, KV dtype) with the fused decode step and the attention-only
+    call per layer (graph replay over all 28 layers), their algorithmic GB/s
+    and the fraction of the 8 TB/s HBM peak."""
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(HD)))
+    P = NKV * HD
+    for ctx in (8192, 16384, 32768):
+        for name, code in (("int8", INT8), ("f32", F32)):
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                g = torch.Generator(device="cuda")
+                g.manual_seed(ctx)
+                kv = HipKV(L, ctx, NKV, HD, n_sink=NSINK, dtype=code)
+                kv.set_stream(stream.cuda_stream)
+                rows = []
+                for layer in range(L):  # one layer's K/V at a time (32k fp32: 268 MB each)
+                    K = torch.randn(ctx, P, device="cuda", generator=g)
+                    V = torch.randn(ctx, P, device="cuda", generator=g)
+                    kv.append_async(layer, 0, ctx, K.data_ptr(), V.data_ptr())
+                    rows.append((K[ctx - 1].clone(), V[ctx - 1].clone()))
+                    torch.cuda.synchronize()
+                    del K, V
+                q = torch.randn(L, NH * HD, device="cuda", generator=g)
+                out = torch.empty_like(q)
+                pos = ctx - 1
+
+                def full(s):
+                    kv.set_stream(s.cuda_stream)
+                    for layer in range(L):
+                        kv.decode_async(layer, pos, rows[layer][0].data_ptr(),
+                                        rows[layer][1].data_ptr(), NH, scale,
+                                        q[layer].data_ptr(), out[layer].data_ptr())
+
+                def attn(s):
+                    kv.set_stream(s.cuda_stream)
+                    for layer in range(L):
+                        kv.attend_async(layer, pos, NH, scale, q[layer].data_ptr(),
+                                        out[layer].data_ptr())
+
+                res = {"sweep": "config 3 shape", "ctx": ctx, "kv": name,
+                       "bytes_per_call": attn_bytes(name, ctx)}
+                for key, fn in (("step", full), ("attn", attn)):
+                    gr = capture(torch, fn)
+                    for _ in range(5):
+                        gr.replay()
+                    us = 1000.0 * time_graph(torch, gr, args.config_steps) / L
+                    gbs = attn_bytes(name, ctx) / (us * 1e-6) / 1e9
+                    res.update({f"{key}_us_per_layer": round(us, 3), f"{key}_GBs": round(gbs, 1),
+                                f"{key}_frac_of_peak": round(gbs / PEAK_GBS, 4)})
+                    del gr
+                kv.close()
+                del rows, q, out
+            torch.cuda.synchronize()
+            print(json.dumps(res), flush=True)
+
+
 def prefix_io(HipKV, F32, kv, L_, cap, nkv, hd, n_tok):
     """Config 5's prefix cache: save the first n_tok positions of every layer
     as a DBKVCACH v1 file, then load it into a fresh cache (model.cpp
@@ -443,6 +500,8 @@ def main():
     ap.add_argument("--config-steps", type=int, default=30)
     ap.add_argument("--configs-cpu", action="store_true",
                     help="with --configs: also time the CPU oracle on one layer of each config")
+    ap.add_argument("--ctx-sweep", action="store_true",
+                    help="instead of the bench line, config 3's shape at ctx 8k, 16k, 32k")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (PMC calibration)")
     args = ap.parse_args()
@@ -467,6 +526,9 @@ def main():
         return
     if args.configs:
         run_configs(torch, HipKV, F32, INT8, args)
+        return
+    if args.ctx_sweep:
+        run_ctx_sweep(torch, HipKV, F32, INT8, args)
         return
     scale = float(np.float32(1.0) / np.sqrt(np.float32(HD)))
     # every launch and event goes on one non-default stream (the kernels'
