@@ -321,8 +321,9 @@ def run_configs(torch, HipKV, F32, INT8, args):
             res.update({"producer_us_per_token_layer": round(usp, 3),
                         "producer_bias": bias is not None})
             del gp
-            if name.startswith("C5") and dt == "f32":
-                res["prefix_io"] = prefix_io(HipKV, F32, kv, L_, pos + 1, nkv, hd, 2048)
+            if name.startswith("C5"):  # fp32: DBKVCACH v1; int8: v2
+                res["prefix_io"] = prefix_io(HipKV, INT8 if dt == "int8" else F32, ns, kv, L_,
+                                             pos + 1, nkv, hd, 2048)
             if rows:
                 pos0 = 1792 if rows == 256 else pos + 1 - rows
                 kv.truncate(pos0 + rows)
@@ -409,10 +410,11 @@ def run_ctx_sweep(torch, HipKV, F32, INT8, args):
             print(json.dumps(res), flush=True)
 
 
-def prefix_io(HipKV, F32, kv, L_, cap, nkv, hd, n_tok):
+def prefix_io(HipKV, code, n_sink, kv, L_, cap, nkv, hd, n_tok):
     """Config 5's prefix cache: save the first n_tok positions of every layer
-    as a DBKVCACH v1 file, then load it into a fresh cache (model.cpp
-    :1023-1156), timed end to end (device pack, PCIe, file)."""
+    (fp32: a DBKVCACH v1 file, model.cpp:1023-1156; int8: the v2 file of
+    codes, scales and sinks), then load it into a fresh cache of the same
+    layout, timed end to end (device pack, PCIe, file)."""
     import tempfile
 
     tokens = np.arange(n_tok, dtype=np.int32)
@@ -422,7 +424,7 @@ def prefix_io(HipKV, F32, kv, L_, cap, nkv, hd, n_tok):
         kv.save_prefix(path, tokens)
         save_s = time.perf_counter() - t
         size = os.path.getsize(path)
-        fresh = HipKV(L_, cap, nkv, hd, 0, 0, F32, 1e6)
+        fresh = HipKV(L_, cap, nkv, hd, n_sink, 0, code, 1e6)
         t = time.perf_counter()
         n = fresh.load_prefix(path, tokens)
         load_s = time.perf_counter() - t

@@ -777,38 +777,108 @@ dbi_status dbi_kv_chunk_qkv_async(dbi_kv* kv, uint32_t layer, uint32_t pos0, uin
 // [L][len][nkv][hd], fp32 V in the same layout.
 
 static const unsigned char kMagic[8] = {'D', 'B', 'K', 'V', 'C', 'A', 'C', 'H'};
-static const uint32_t kVersion = 1;
+static const uint32_t kVersion = 1;      // model.cpp:1033: dense fp32 K then V
+static const uint32_t kVersionInt8 = 2;  // dense int8 (this library; v1 is fp32-only)
+
+namespace {
+
+// v2 payload of a dense int8 cache's first len positions, in file order:
+// K codes, V codes (int8 [L][len][nkv][hd], signed), V block scales
+// [L][len][nkv][nb], K channel scales of the groups covering len
+// [L][ceil(len/32)][nkv][hd], the raw K rows of a partial last group
+// [L][len % 32][nkv][hd], K sinks then V sinks [L][min(n_sink, len)][nkv][hd]
+// (all fp32 but the codes).
+struct Int8Payload {
+  size_t codes, vsc, ksc, raw, sinks;  // bytes per code array; floats per section
+  int ngl, w, ns;
+  size_t bytes() const { return 2 * codes + 4 * (vsc + ksc + raw + 2 * sinks); }
+};
+
+Int8Payload int8_payload(const dbi::KvGeom& g, uint32_t len) {
+  Int8Payload p{};
+  const size_t L = g.n_layers, P = size_t(g.nkv) * g.hd;
+  p.ngl = static_cast<int>((len + dbi::kKGroup - 1) / dbi::kKGroup);
+  p.w = static_cast<int>(len % dbi::kKGroup);
+  p.ns = static_cast<int>(len < uint32_t(g.n_sink) ? len : uint32_t(g.n_sink));
+  p.codes = L * len * P;
+  p.vsc = L * len * g.nkv * g.nb;
+  p.ksc = L * size_t(p.ngl) * P;
+  p.raw = L * size_t(p.w) * P;
+  p.sinks = L * size_t(p.ns) * P;
+  return p;
+}
+
+// every v2 section between the store and a device buffer in file order
+// (unpack: buffer -> store)
+hipError_t int8_sections(dbi_kv* kv, unsigned char* dev, uint32_t len, bool unpack) {
+  const dbi::KvGeom& g = kv->geom;
+  dbi::KvStore& s = kv->store;
+  const Int8Payload p = int8_payload(g, len);
+  const int n = static_cast<int>(len), L = g.n_layers, P = g.nkv * g.hd;
+  int8_t* kc = reinterpret_cast<int8_t*>(dev);
+  int8_t* vc = kc + p.codes;
+  float* f = reinterpret_cast<float*>(dev + 2 * p.codes);
+  hipError_t e = dbi::launch_prefix_codes(g, s.k8, kc, n, true, unpack, kv->stream);
+  if (e == hipSuccess) e = dbi::launch_prefix_codes(g, s.v8, vc, n, false, unpack, kv->stream);
+  float* at = f;
+  auto rows = [&](float* store, int nkv, int dev_rows, int r, int inner, size_t count) {
+    if (e == hipSuccess)
+      e = dbi::launch_rows_pack(store, at, L, nkv, dev_rows, r, inner, unpack, kv->stream);
+    at += count;
+  };
+  rows(s.v_scale, g.nkv, g.capg, n, g.nb, p.vsc);
+  rows(s.k_scale, g.nkv, g.ngroups, p.ngl, g.hd, p.ksc);
+  rows(s.k_raw, 1, dbi::kKGroup, p.w, P, p.raw);
+  rows(s.k_sink, g.nkv, g.n_sink, p.ns, g.hd, p.sinks);
+  rows(s.v_sink, g.nkv, g.n_sink, p.ns, g.hd, p.sinks);
+  return e;
+}
+
+}  // namespace
 
 dbi_status dbi_kv_prefix_save(dbi_kv* kv, const char* path, const int32_t* tokens,
                               uint32_t len) {
   if (kv == nullptr || path == nullptr) return fail(DBI_ERR_INVALID, "null argument");
-  // checks in the order of model.cpp:1074-1079
-  if (kv->geom.ring || kv->geom.int8)
+  // checks in the order of model.cpp:1074-1079; a dense int8 cache writes v2
+  if (kv->geom.ring)
     return fail(DBI_ERR_UNSUPPORTED, "kv prefix cache supports only the dense fp32 cache");
   if (len == 0) return fail(DBI_ERR_INVALID, "kv prefix is empty");
   if (tokens == nullptr) return fail(DBI_ERR_INVALID, "null tokens");
   if (kv->n_seen < len) return fail(DBI_ERR_INVALID, "cache holds fewer positions than the prefix");
-
   const dbi::KvGeom& g = kv->geom;
+  // an int8 group that later appends extended was requantized with their
+  // rows: only a prefix ending on a group boundary, or at n_seen, is the
+  // state those len appends left
+  if (g.int8 && len % dbi::kKGroup != 0 && len != kv->n_seen)
+    return fail(DBI_ERR_INVALID,
+                "an int8 kv prefix must end on a 32-token group boundary or at n_seen");
+
   const size_t elems = size_t(g.n_layers) * len * g.nkv * g.hd;
   if (dbi_status st = need_pinned(kv)) return st;
-  std::vector<unsigned char> hdr(8 + 5 * 4 + size_t(len) * 4);
+  const uint32_t version = g.int8 ? kVersionInt8 : kVersion;
+  const size_t nh = g.int8 ? 7 : 5;
+  std::vector<unsigned char> hdr(8 + nh * 4 + size_t(len) * 4);
   std::memcpy(hdr.data(), kMagic, 8);
-  const uint32_t h[5] = {kVersion, kv->cfg.n_layers, kv->cfg.n_kv_heads, kv->cfg.head_dim, len};
-  std::memcpy(hdr.data() + 8, h, sizeof h);
-  std::memcpy(hdr.data() + 28, tokens, size_t(len) * 4);
+  const uint32_t h[7] = {version, kv->cfg.n_layers, kv->cfg.n_kv_heads, kv->cfg.head_dim, len,
+                         DBI_KV_INT8, kv->cfg.n_sink};
+  std::memcpy(hdr.data() + 8, h, nh * 4);
+  std::memcpy(hdr.data() + 8 + nh * 4, tokens, size_t(len) * 4);
 
-  // K then V packed into [L][len][nkv][hd] on the device, then streamed out
+  // the payload packed on the device in file order, then streamed out
   unsigned char* dev = nullptr;
-  const size_t payload = 2 * elems * sizeof(float);
+  const size_t payload = g.int8 ? int8_payload(g, len).bytes() : 2 * elems * sizeof(float);
   if (hipMalloc(reinterpret_cast<void**>(&dev), payload) != hipSuccess)
     return fail(DBI_ERR_NOMEM, "prefix staging allocation failed");
-  float* devf = reinterpret_cast<float*>(dev);
-  hipError_t e =
-      dbi::launch_prefix_pack(g, kv->store.k, devf, static_cast<int>(len), true, kv->stream);
-  if (e == hipSuccess)
-    e = dbi::launch_prefix_pack(g, kv->store.v, devf + elems, static_cast<int>(len), false,
-                                kv->stream);
+  hipError_t e = hipSuccess;
+  if (g.int8) {
+    e = int8_sections(kv, dev, len, false);
+  } else {
+    float* devf = reinterpret_cast<float*>(dev);
+    e = dbi::launch_prefix_pack(g, kv->store.k, devf, static_cast<int>(len), true, kv->stream);
+    if (e == hipSuccess)
+      e = dbi::launch_prefix_pack(g, kv->store.v, devf + elems, static_cast<int>(len), false,
+                                  kv->stream);
+  }
   std::FILE* f = nullptr;
   if (e == hipSuccess) {
     f = std::fopen(path, "wb");
@@ -837,7 +907,7 @@ dbi_status dbi_kv_prefix_save(dbi_kv* kv, const char* path, const int32_t* token
 dbi_status dbi_kv_prefix_load(dbi_kv* kv, const char* path, const int32_t* tokens,
                               uint32_t n_tokens, uint32_t* out_len) {
   if (kv == nullptr || path == nullptr) return fail(DBI_ERR_INVALID, "null argument");
-  if (kv->geom.ring || kv->geom.int8)
+  if (kv->geom.ring)
     return fail(DBI_ERR_UNSUPPORTED, "kv prefix cache supports only the dense fp32 cache");
   std::FILE* f = std::fopen(path, "rb");
   if (f == nullptr) return fail(DBI_ERR_IO, std::string("cannot open kv prefix cache ") + path);
@@ -861,27 +931,38 @@ dbi_status dbi_kv_prefix_load(dbi_kv* kv, const char* path, const int32_t* token
   };
   auto io_fail = [&] { return fail(DBI_ERR_IO, std::string("read error on kv prefix cache ") + path); };
 
-  // validation in the order of model.cpp:1117-1148
+  // validation in the order of model.cpp:1117-1148; v2 adds its layout
+  // fields after the hyperparameters
   for (int i = 0; i < 8; ++i) {
     if (!need(1)) return fail(DBI_ERR_FORMAT, "kv prefix cache truncated");
     unsigned char ch;
     if (!take(&ch, 1)) return io_fail();
     if (ch != kMagic[i]) return fail(DBI_ERR_FORMAT, "kv prefix cache bad magic");
   }
-  uint32_t u[5];
-  for (int i = 0; i < 5; ++i) {
+  uint32_t u[7] = {};
+  int nh = 5;
+  for (int i = 0; i < nh; ++i) {
     if (!need(4)) return fail(DBI_ERR_FORMAT, "kv prefix cache truncated");
     if (!take(&u[i], 4)) return io_fail();
-    if (i == 0 && u[0] != kVersion)
-      return fail(DBI_ERR_FORMAT,
-                  "kv prefix cache version " + std::to_string(u[0]) + " unsupported");
+    if (i == 0) {
+      if (u[0] != kVersion && u[0] != kVersionInt8)
+        return fail(DBI_ERR_FORMAT,
+                    "kv prefix cache version " + std::to_string(u[0]) + " unsupported");
+      if (u[0] == kVersionInt8) nh = 7;
+    }
   }
+  const bool v2 = u[0] == kVersionInt8;
   const uint32_t n_layers = u[1], n_kv = u[2], hd = u[3], prefix_len = u[4];
+  const dbi::KvGeom& g = kv->geom;
   if (n_layers != kv->cfg.n_layers || n_kv != kv->cfg.n_kv_heads || hd != kv->cfg.head_dim)
     return fail(DBI_ERR_FORMAT, "kv prefix cache hyperparams do not match this model");
+  if (v2 && !g.int8)
+    return fail(DBI_ERR_FORMAT, "kv prefix cache holds an int8 cache; this cache is dense fp32");
+  if (v2 && (u[5] != DBI_KV_INT8 || u[6] != kv->cfg.n_sink))
+    return fail(DBI_ERR_FORMAT, "kv prefix cache int8 layout does not match this cache");
   if (prefix_len == 0) return fail(DBI_ERR_FORMAT, "kv prefix cache has a zero-length prefix");
   if (prefix_len > n_tokens) return fail(DBI_ERR_FORMAT, "kv prefix is longer than the prompt");
-  if (prefix_len > static_cast<uint32_t>(kv->geom.cap))
+  if (prefix_len > static_cast<uint32_t>(g.cap))
     return fail(DBI_ERR_FORMAT, "kv prefix exceeds cache capacity");
   if (tokens == nullptr) return fail(DBI_ERR_INVALID, "null tokens");
   for (uint32_t i = 0; i < prefix_len; ++i) {
@@ -892,9 +973,9 @@ dbi_status dbi_kv_prefix_load(dbi_kv* kv, const char* path, const int32_t* token
       return fail(DBI_ERR_FORMAT,
                   "prompt prefix differs from saved cache at token " + std::to_string(i));
   }
-  const dbi::KvGeom& g = kv->geom;
-  const size_t elems = size_t(g.n_layers) * prefix_len * g.nkv * g.hd;
-  const size_t payload = 2 * elems * sizeof(float);
+  const size_t P = size_t(g.nkv) * g.hd;
+  const size_t elems = size_t(g.n_layers) * prefix_len * P;
+  const size_t payload = v2 ? int8_payload(g, prefix_len).bytes() : 2 * elems * sizeof(float);
   if (p + payload != total) return fail(DBI_ERR_FORMAT, "kv prefix cache payload size mismatch");
   if (dbi_status st = need_pinned(kv)) return st;
 
@@ -912,12 +993,22 @@ dbi_status dbi_kv_prefix_load(dbi_kv* kv, const char* path, const int32_t* token
     if (ok && e == hipSuccess) e = hipStreamSynchronize(kv->stream);
   }
   const float* devf = reinterpret_cast<const float*>(dev);
-  if (ok && e == hipSuccess)
-    e = dbi::launch_prefix_unpack(g, devf, kv->store.k, static_cast<int>(prefix_len), true,
-                                  kv->stream);
-  if (ok && e == hipSuccess)
-    e = dbi::launch_prefix_unpack(g, devf + elems, kv->store.v, static_cast<int>(prefix_len),
-                                  false, kv->stream);
+  const int n = static_cast<int>(prefix_len);
+  if (ok && e == hipSuccess) {
+    if (v2) {
+      e = int8_sections(kv, dev, prefix_len, true);
+    } else if (g.int8) {
+      // a v1 (fp32) prefix into an int8 cache: the prefix's appends,
+      // quantized on append exactly as KVCache::append would
+      for (int l = 0; l < g.n_layers && e == hipSuccess; ++l)
+        e = dbi::launch_append(g, kv->store, l, 0, n, devf + size_t(l) * n * P,
+                               devf + elems + size_t(l) * n * P, kv->stream);
+    } else {
+      e = dbi::launch_prefix_unpack(g, devf, kv->store.k, n, true, kv->stream);
+      if (e == hipSuccess)
+        e = dbi::launch_prefix_unpack(g, devf + elems, kv->store.v, n, false, kv->stream);
+    }
+  }
   if (ok && e == hipSuccess) e = hipStreamSynchronize(kv->stream);
   if (e != hipSuccess) (void)hipStreamSynchronize(kv->stream);
   (void)hipFree(dev);

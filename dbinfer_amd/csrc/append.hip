@@ -176,9 +176,9 @@ int grid_for(size_t work) {
 }
 
 // [L][len][nkv][hd] <-> the head-major K (is_k) or V store
-__global__ __launch_bounds__(kThreads) void prefix_pack_kernel(KvGeom g, const float* store,
-                                                               float* dst, int len, int unpack,
-                                                               int is_k) {
+template <typename T>
+__global__ __launch_bounds__(kThreads) void prefix_pack_kernel(KvGeom g, const T* store, T* dst,
+                                                               int len, int unpack, int is_k) {
   const size_t P = static_cast<size_t>(g.nkv) * g.hd;
   const size_t total = static_cast<size_t>(g.n_layers) * len * P;
   for (size_t idx = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; idx < total;
@@ -191,10 +191,39 @@ __global__ __launch_bounds__(kThreads) void prefix_pack_kernel(KvGeom g, const f
     const size_t st = (l * g.nkv + kh) * head_elems(g) +
                       (is_k ? k_off(g, static_cast<int>(p), static_cast<int>(i))
                             : v_off(g, static_cast<int>(p), static_cast<int>(i)));
+    if constexpr (sizeof(T) == 1) {  // int8 codes: stored biased (code + 128), filed signed
+      if (unpack)
+        const_cast<T*>(store)[st] = static_cast<T>(dst[idx] ^ 0x80);
+      else
+        dst[idx] = static_cast<T>(store[st] ^ 0x80);
+    } else {
+      if (unpack)
+        const_cast<T*>(store)[st] = dst[idx];
+      else
+        dst[idx] = store[st];
+    }
+  }
+}
+
+// Row-major per-head arrays: store [L][nkv][dev_rows][inner] <-> file
+// [L][rows][nkv][inner], the first `rows` rows of every head.
+__global__ __launch_bounds__(kThreads) void rows_pack_kernel(const float* store, float* file,
+                                                             int n_layers, int nkv, int dev_rows,
+                                                             int rows, int inner, int unpack) {
+  const size_t per_layer = static_cast<size_t>(rows) * nkv * inner;
+  const size_t total = static_cast<size_t>(n_layers) * per_layer;
+  for (size_t idx = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; idx < total;
+       idx += static_cast<size_t>(gridDim.x) * kThreads) {
+    const size_t l = idx / per_layer;
+    const size_t rem = idx % per_layer;
+    const size_t r = rem / (static_cast<size_t>(nkv) * inner);
+    const size_t kh = (rem / inner) % nkv;
+    const size_t i = rem % inner;
+    const size_t st = ((l * nkv + kh) * dev_rows + r) * inner + i;
     if (unpack)
-      const_cast<float*>(store)[st] = dst[idx];
+      const_cast<float*>(store)[st] = file[idx];
     else
-      dst[idx] = store[st];
+      file[idx] = store[st];
   }
 }
 
@@ -229,7 +258,7 @@ hipError_t launch_append(const KvGeom& g, const KvStore& s, int layer, int pos0,
 hipError_t launch_prefix_pack(const KvGeom& g, const float* src_store, float* dst, int len,
                               bool is_k, hipStream_t st) {
   const size_t total = static_cast<size_t>(g.n_layers) * len * g.nkv * g.hd;
-  hipLaunchKernelGGL(prefix_pack_kernel, dim3(grid_for(total)), dim3(kThreads), 0, st, g,
+  hipLaunchKernelGGL(prefix_pack_kernel<float>, dim3(grid_for(total)), dim3(kThreads), 0, st, g,
                      src_store, dst, len, 0, is_k ? 1 : 0);
   return hipGetLastError();
 }
@@ -237,8 +266,27 @@ hipError_t launch_prefix_pack(const KvGeom& g, const float* src_store, float* ds
 hipError_t launch_prefix_unpack(const KvGeom& g, const float* src, float* dst_store, int len,
                                 bool is_k, hipStream_t st) {
   const size_t total = static_cast<size_t>(g.n_layers) * len * g.nkv * g.hd;
-  hipLaunchKernelGGL(prefix_pack_kernel, dim3(grid_for(total)), dim3(kThreads), 0, st, g,
+  hipLaunchKernelGGL(prefix_pack_kernel<float>, dim3(grid_for(total)), dim3(kThreads), 0, st, g,
                      dst_store, const_cast<float*>(src), len, 1, is_k ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefix_codes(const KvGeom& g, int8_t* store, int8_t* file, int len, bool is_k,
+                               bool unpack, hipStream_t st) {
+  const size_t total = static_cast<size_t>(g.n_layers) * len * g.nkv * g.hd;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(prefix_pack_kernel<uint8_t>, dim3(grid_for(total)), dim3(kThreads), 0, st,
+                     g, reinterpret_cast<const uint8_t*>(store),
+                     reinterpret_cast<uint8_t*>(file), len, unpack ? 1 : 0, is_k ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_rows_pack(float* store, float* file, int n_layers, int nkv, int dev_rows,
+                            int rows, int inner, bool unpack, hipStream_t st) {
+  const size_t total = static_cast<size_t>(n_layers) * rows * nkv * inner;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(rows_pack_kernel, dim3(grid_for(total)), dim3(kThreads), 0, st, store, file,
+                     n_layers, nkv, dev_rows, rows, inner, unpack ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -206,5 +206,12 @@ hipError_t launch_prefix_pack(const KvGeom& g, const float* src_store, float* ds
                               bool is_k, hipStream_t st);
 hipError_t launch_prefix_unpack(const KvGeom& g, const float* src, float* dst_store, int len,
                                 bool is_k, hipStream_t st);
+// int8 codes between the biased granule store and the file's signed
+// [L][len][nkv][hd] (both directions; unpack = file -> store)
+hipError_t launch_prefix_codes(const KvGeom& g, int8_t* store, int8_t* file, int len, bool is_k,
+                               bool unpack, hipStream_t st);
+// store [L][nkv][dev_rows][inner] <-> file [L][rows][nkv][inner] (first rows)
+hipError_t launch_rows_pack(float* store, float* file, int n_layers, int nkv, int dev_rows,
+                            int rows, int inner, bool unpack, hipStream_t st);
 
 }  // namespace dbi

@@ -186,13 +186,28 @@ dbi_status dbi_kv_chunk_qkv_async(dbi_kv* kv, uint32_t layer, uint32_t pos0, uin
                                   const float* v_bias_dev, float* out_dev);
 
 /* Model::save_kv_prefix (model.hpp:292-293, model.cpp:1072-1107): writes the
- * DBKVCACH v1 file of positions [0, len) with the token ids. Dense fp32 only. */
+ * DBKVCACH v1 file of positions [0, len) with the token ids from a dense
+ * fp32 cache. A dense int8 cache writes version 2, which has no counterpart
+ * in the reference (its v1 is dense-fp32-only, model.cpp:1074-1075):
+ *   header  "DBKVCACH", u32 2, n_layers, n_kv_heads, head_dim, len,
+ *           u32 dtype (1 = int8), u32 n_sink, i32 tokens[len];
+ *   payload K codes, V codes   int8 [L][len][n_kv_heads][head_dim] (signed);
+ *           V block scales     f32 [L][len][n_kv_heads][head_dim/32];
+ *           K channel scales   f32 [L][ceil(len/32)][n_kv_heads][head_dim];
+ *           raw K rows of a partial last group f32 [L][len % 32][n_kv_heads][head_dim];
+ *           K sinks, V sinks   f32 [L][min(n_sink, len)][n_kv_heads][head_dim].
+ * An int8 prefix must end on a 32-token group boundary or at n_seen (a group
+ * that later appends extended was requantized with their rows). Rings have
+ * no prefix files. */
 dbi_status dbi_kv_prefix_save(dbi_kv* kv, const char* path, const int32_t* tokens,
                               uint32_t len);
 /* Model::load_kv_prefix (model.hpp:298-299, model.cpp:1109-1156): validates
  * magic, version, hyperparameters, length, token ids and exact size in the
  * reference's order, then restores K/V and sets n_seen = prefix length
- * (written to *out_len). Leaves the cache untouched on any error. */
+ * (written to *out_len). Leaves the cache untouched on any error. A v1 file
+ * loads into a dense fp32 cache, or into a dense int8 cache as the
+ * quantize-on-append of its rows; a v2 file into a dense int8 cache with the
+ * same n_sink, restoring its codes, scales, raw rows and sinks exactly. */
 dbi_status dbi_kv_prefix_load(dbi_kv* kv, const char* path, const int32_t* tokens,
                               uint32_t n_tokens, uint32_t* out_len);
 

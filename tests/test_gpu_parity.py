@@ -361,7 +361,8 @@ def test_abi_errors_leave_state():
     with pytest.raises(DbiError):
         g.residents()  # dense cache has no ring mapping
     assert g.n_seen == 4
-    i8 = HipKV(1, 16, 1, 64, dtype=INT8)
+    ring = HipKV(1, 0, 1, 64, 0, 8, INT8, 1e4)  # rings have no prefix files
+    ring.append(0, 0, normal(3, 64), normal(4, 64))
     with pytest.raises(DbiError) as e:
-        i8.save_prefix("/tmp/never.kv", [1])
+        ring.save_prefix("/tmp/never.kv", [1])
     assert "dense fp32" in e.value.message
