@@ -359,7 +359,7 @@ template <int HD, int G, bool PROD>
 __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs& A, int kh,
                                            int qrow, int wave, int lane, const float* qw) {
   constexpr int DPL = HD / 64;
-  constexpr int kSinkBatch = 8;
+  constexpr int kSinkBatch = 4;  // the usual n_sink: one batch, no idle reductions
   constexpr int kSC1 = 16;  // cache policy: agent-coherent load
   if (wave >= G) return;
   const int g = wave;
@@ -380,10 +380,17 @@ __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs
   float ov[kMergeBatch][DPL];
   auto load_batch = [&](int sp0) {
 #pragma unroll
-    for (int sp = 0; sp < kMergeBatch; ++sp)
-#pragma unroll
-      for (int e = 0; e < DPL; ++e)
-        ov[sp][e] = ld(min(sp0 + sp, P.nsplit - 1) * rec_floats + g * HD + lane * DPL + e);
+    for (int sp = 0; sp < kMergeBatch; ++sp) {
+      const int idx = min(sp0 + sp, P.nsplit - 1) * rec_floats + g * HD + lane * DPL;
+      if constexpr (DPL == 2) {  // the lane's two dims in one 8-byte load
+        const float2 t = __builtin_bit_cast(
+            float2, __builtin_amdgcn_raw_buffer_load_b64(rr, idx * 4, 0, kSC1));
+        ov[sp][0] = t.x;
+        ov[sp][1] = t.y;
+      } else {
+        ov[sp][0] = ld(idx);
+      }
+    }
   };
   load_batch(0);
   const int ns = min(P.n_sink, P.pos0 + qrow + 1);
@@ -450,7 +457,8 @@ __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs
       float dot = 0.0f;
 #pragma unroll
       for (int e = 0; e < DPL; ++e) dot += qd[e] * kd[b][e];
-      sc[b] = p0 + b < ns ? wave_sum(dot) : -INFINITY;
+      sc[b] = -INFINITY;
+      if (p0 + b < ns) sc[b] = wave_sum(dot);  // uniform
       bm = fmaxf(bm, sc[b]);
     }
     const float f = fast_exp2(M - bm);
