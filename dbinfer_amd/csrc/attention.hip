@@ -377,22 +377,28 @@ __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs
   const int r0 = min(lane, P.nsplit - 1) * rec_floats;
   const float m = ld(r0 + G * HD + g);
   const float l = ld(r0 + G * HD + G + g);
-  float ov[kMergeBatch][DPL];
-  auto load_batch = [&](int sp0) {
+  // up to kMaxSplits = 2 kMergeBatch records, both batches in the first
+  // round (every record read is a round trip to the device-coherent level)
+  static_assert(kMaxSplits <= 2 * kMergeBatch, "merge batches");
+  float ov[2][kMergeBatch][DPL];
+  auto load_batch = [&](int b) {
 #pragma unroll
     for (int sp = 0; sp < kMergeBatch; ++sp) {
-      const int idx = min(sp0 + sp, P.nsplit - 1) * rec_floats + g * HD + lane * DPL;
+      const int idx =
+          min(b * kMergeBatch + sp, P.nsplit - 1) * rec_floats + g * HD + lane * DPL;
       if constexpr (DPL == 2) {  // the lane's two dims in one 8-byte load
         const float2 t = __builtin_bit_cast(
             float2, __builtin_amdgcn_raw_buffer_load_b64(rr, idx * 4, 0, kSC1));
-        ov[sp][0] = t.x;
-        ov[sp][1] = t.y;
+        ov[b][sp][0] = t.x;
+        ov[b][sp][1] = t.y;
       } else {
-        ov[sp][0] = ld(idx);
+        ov[b][sp][0] = ld(idx);
       }
     }
   };
   load_batch(0);
+  const bool two = P.nsplit > kMergeBatch;  // uniform
+  if (two) load_batch(1);
   const int ns = min(P.n_sink, P.pos0 + qrow + 1);
   const size_t h = static_cast<size_t>(qrow) * P.n_heads + kh * G + g;
   float qd[DPL], kd[kSinkBatch][DPL], vd[kSinkBatch][DPL];
@@ -436,15 +442,16 @@ __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs
   const float w = on ? fast_exp2(m - M) : 0.0f;
   float L = wave_sum(on ? l * w : 0.0f);
   float O[DPL] = {};
-  for (int sp0 = 0; sp0 < P.nsplit; sp0 += kMergeBatch) {  // uniform
-    if (sp0 > 0) load_batch(sp0);
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    if (b == 1 && !two) break;
 #pragma unroll
     for (int sp = 0; sp < kMergeBatch; ++sp) {
       // lanes past nsplit hold weight 0 (and clamped records)
       const float ws = __builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), min(sp0 + sp, 63)));
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), b * kMergeBatch + sp));
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) O[e] += ws * ov[sp][e];
+      for (int e = 0; e < DPL; ++e) O[e] += ws * ov[b][sp][e];
     }
   }
   // sinks as further entries, a batch at a time with a running max
