@@ -73,6 +73,43 @@ __device__ __forceinline__ float4 lds4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
 
+// Lane-group exchanges of the softmax through the gfx950 permlane swaps
+// (VALU, no LDS round trip like a bpermute). After v_permlane16_swap of
+// (x, x), a lane holds its own x and the x of lane ^ 16 (one in each
+// register); v_permlane32_swap does the same for lane ^ 32. Emitted through
+// asm: the compiler's builtins fold the two results into one when both are
+// used.
+__device__ __forceinline__ float xmax16(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float xmax32(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float xsum16(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+__device__ __forceinline__ float xsum32(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+
+// Stage buffers hold the cache's granule layout with its 16-byte units
+// swizzled inside every aligned run of 64 units: unit u sits at
+// u ^ ((u >> 3) & 7). A K operand read has lanes of eight position rows
+// (units 8 apart, one bank group in the plain layout) in one LDS pass; the
+// swizzle spreads them over eight bank groups. The map is its own inverse.
+__device__ __forceinline__ int swz(int o) {  // float offset in a stage array
+  const int u = o >> 2;
+  return ((u ^ ((u >> 3) & 7)) << 2) | (o & 3);
+}
+
 template <int HD>
 struct Stage {
   static constexpr int SK = HD == 64 ? 64 : 32;                // keys per stage
@@ -122,14 +159,16 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
   const float* kbase = P.kf + head_el;
   const float* vbase = P.vf + head_el;
 
-  // stage copy: K then V, contiguous, 16 bytes per lane per instruction
+  // stage copy: K then V, 16 bytes per lane per instruction; each lane
+  // fetches the unit that the swizzle puts at its LDS slot
+  const int src_lane = lane ^ ((lane >> 3) & 7);
   auto copy_stage = [&](int st, float* dst) {
     const size_t off = static_cast<size_t>(st) * FL;
 #pragma unroll
     for (int m = 0; m < NDMA; ++m) {
       const int e = (m * kPThreads + wave * 64) * 4;  // this wave's KiB of the copy
-      lds_copy16(kbase + off + e + lane * 4, dst + e);
-      lds_copy16(vbase + off + e + lane * 4, dst + FL + e);
+      lds_copy16(kbase + off + e + src_lane * 4, dst + e);
+      lds_copy16(vbase + off + e + src_lane * 4, dst + FL + e);
     }
   };
 
@@ -165,10 +204,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
       for (int c = 0; c < 4; ++c) sc[c] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int h = 0; h < NH; ++h) {
-        const float* kp = sk + k_off_tiled(HD, false, 16 * t + vec, 16 * gq + 64 * h);
+        const int ko = static_cast<int>(k_off_tiled(HD, false, 16 * t + vec, 16 * gq + 64 * h));
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4) {
-          const float4 x = lds4(kp + 4 * s4);
+          const float4 x = lds4(sk + swz(ko + 4 * s4));
           const int i = 16 * h + 4 * s4;
           sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, qv[i + 0], sc[0], 0, 0, 0);
           sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, qv[i + 1], sc[1], 0, 0, 0);
@@ -187,8 +226,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
         sv4[v] = key <= limit ? s[v] : -INFINITY;
         mx = fmaxf(mx, sv4[v]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = xmax32(xmax16(mx));
       const float mn = fmaxf(m_run, mx);
       const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
       float pv[4], ls = 0.0f;
@@ -197,8 +235,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
         pv[v] = __builtin_amdgcn_exp2f(sv4[v] - mn);
         ls += pv[v];
       }
-      ls += __shfl_xor(ls, 16);
-      ls += __shfl_xor(ls, 32);
+      ls = xsum32(xsum16(ls));
       l_run = l_run * alpha + ls;
       m_run = mn;
 #pragma unroll
@@ -209,11 +246,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int key = kb + 4 * gq + j;
-        const float* vp = sv + v_off_tiled(HD, false, 16 * t + 4 * gq + j, VD * vec);
+        const int vo = static_cast<int>(v_off_tiled(HD, false, 16 * t + 4 * gq + j, VD * vec));
         float vd[VD];
 #pragma unroll
         for (int u = 0; u < VD / 4; ++u) {
-          const float4 x = lds4(vp + 256 * u);
+          const float4 x = lds4(sv + swz(vo + 256 * u));
           vd[4 * u + 0] = key <= last_key ? x.x : 0.0f;
           vd[4 * u + 1] = key <= last_key ? x.y : 0.0f;
           vd[4 * u + 2] = key <= last_key ? x.z : 0.0f;
