@@ -158,12 +158,6 @@ __device__ __forceinline__ float swap16_sum(float a, float b) {
 // output tolerance, so the denormal-range handling of exp2f is not needed.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Workgroup barrier that waits for this wave's LDS operations only (no
-// wait on outstanding vector-memory loads, which __syncthreads would add).
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // tensor::rope's fp64 NeoX rotation of one pair (ops.cpp:31-34): products
 // and sums rounded one by one, as the reference's scalar code does
 __device__ __forceinline__ void rope_pair(float& a, float& b, double2 cs) {
@@ -421,10 +415,16 @@ __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs
       } else {
         const float* kr = fresh ? A.k + kh * HD + lane * DPL : P.ksink + at;
         const float* vr = fresh ? A.v + kh * HD + lane * DPL : P.vsink + at;
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) {
-          kd[b][e] = kr[e];
-          vd[b][e] = vr[e];
+        if constexpr (DPL == 2) {  // 8-byte aligned pairs: one load each
+          const float2 k2 = *reinterpret_cast<const float2*>(kr);
+          const float2 v2 = *reinterpret_cast<const float2*>(vr);
+          kd[b][0] = k2.x;
+          kd[b][1] = k2.y;
+          vd[b][0] = v2.x;
+          vd[b][1] = v2.y;
+        } else {
+          kd[b][0] = kr[0];
+          vd[b][0] = vr[0];
         }
       }
     }
@@ -432,9 +432,9 @@ __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs
   if (ns > 0) {
 #pragma unroll
     for (int e = 0; e < DPL; ++e)
-      // raw projections: the produced, scaled q row kept in LDS (qw, the
-      // same bits as q * qscale); otherwise q itself
-      qd[e] = PROD ? qw[lane * DPL + e] : P.q[h * HD + lane * DPL + e] * P.qscale;
+      // the scaled q row the workgroup keeps in LDS (only dense int8 has
+      // sinks; the same bits as q * qscale, produced q in PROD)
+      qd[e] = qw[lane * DPL + e];
     sink_rows(0);
   }
 
