@@ -378,6 +378,11 @@ __device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs
   auto load_batch = [&](int b) {
 #pragma unroll
     for (int sp = 0; sp < kMergeBatch; ++sp) {
+      if (b > 0 && b * kMergeBatch + sp >= P.nsplit) {  // uniform: no such record
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) ov[b][sp][e] = 0.0f;
+        continue;
+      }
       const int idx =
           min(b * kMergeBatch + sp, P.nsplit - 1) * rec_floats + g * HD + lane * DPL;
       if constexpr (DPL == 2) {  // the lane's two dims in one 8-byte load
