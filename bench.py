@@ -345,12 +345,62 @@ def run_configs(torch, HipKV, F32, INT8, args):
                             "chunk_us_per_token_layer": round(usc / rows, 3),
                             "chunk_TFLOPs": round(flops / (usc * 1e-6) / 1e12, 3)})
                 del gc
+                if rows == 5:
+                    res["verify_tokens"] = verify_tokens(torch, kv, rows - 1, g, args)
             kv.close()
             if args.configs_cpu:
                 res["cpu"] = config_cpu(K, V, q, name, nh, nkv, hd, dt, ns, win, pos, rows, scale)
             del K, V, q, out
         torch.cuda.synchronize()
         print(json.dumps(res), flush=True)
+
+
+VOCAB_QWEN3 = 151936
+
+
+def verify_tokens(torch, kv, k, gen, args):
+    """C5's verify round, token side: the argmax of the k+1 logit rows over
+    Qwen3's vocabulary and the merge against the draft, one
+    dbi_spec_verify_async launch (16 per graph replay); its algorithmic GB/s
+    (the logits read once). With --configs-cpu, the oracle's argmax + merge of the
+    same rows on the host beside it."""
+    vocab = VOCAB_QWEN3
+    logits = torch.randn(k + 1, vocab, device="cuda", generator=gen)
+    draft = torch.zeros(k, dtype=torch.int32, device="cuda")
+    ver = torch.zeros(k + 1, dtype=torch.int32, device="cuda")
+    acc = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    per_graph = 16  # back-to-back calls per replay: the launch of one graph is not timed
+
+    def call(s_):
+        kv.set_stream(s_.cuda_stream)
+        for _ in range(per_graph):
+            kv.spec_verify_async(k, vocab, logits.data_ptr(), draft.data_ptr(), ver.data_ptr(),
+                                 acc.data_ptr())
+
+    gv = capture(torch, call)
+    for _ in range(5):
+        gv.replay()
+    us = 1000.0 * time_graph(torch, gv, args.config_steps) / per_graph
+    del gv
+    byts = (k + 1) * vocab * 4
+    res = {"k": k, "vocab": vocab, "us": round(us, 3), "bytes": byts,
+           "GBs": round(byts / (us * 1e-6) / 1e9, 1)}
+    if args.configs_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pyoracle  # checker / baseline only
+
+        host = logits.cpu().numpy()
+        d = draft.cpu().numpy()
+        times = []
+        for _ in range(20):
+            t = time.perf_counter()
+            want = [pyoracle.argmax(r) for r in host]
+            pyoracle.spec_merge(d, want)
+            times.append(time.perf_counter() - t)
+        res["cpu_us"] = round(1e6 * statistics.median(times), 1)
+        res["cpu_threads"] = 1
+    return res
 
 
 def run_ctx_sweep(torch, HipKV, F32, INT8, args):

@@ -75,6 +75,8 @@ SIGNATURES = {
     "dbi_kv_decode_qkv_async": (_st, [_vp, _u32, _u32, _u32, _f32] + [_vp] * 7),
     "dbi_kv_chunk_qkv": (_st, [_vp, _u32, _u32, _u32, _u32, _f32] + [_vp] * 7),
     "dbi_kv_chunk_qkv_async": (_st, [_vp, _u32, _u32, _u32, _u32, _f32] + [_vp] * 7),
+    "dbi_spec_verify_async": (_st, [_vp, _u32, _u32, _vp, _vp, _vp, _vp]),
+    "dbi_kv_verify_commit": (_st, [_vp, _u32, _u32, _u32, _vp, _vp, _vp, _vp]),
     "dbi_kv_prefix_save": (_st, [_vp, ctypes.c_char_p, _vp, _u32]),
     "dbi_kv_prefix_load": (_st, [_vp, ctypes.c_char_p, _vp, _u32, ctypes.POINTER(_u32)]),
     "dbi_kv_export_bytes": (ctypes.c_size_t, [_vp, _u32]),

@@ -67,6 +67,7 @@ void free_ws(dbi::Workspace& w) {
   if (w.counters) (void)hipFree(w.counters);
   if (w.staging) (void)hipFree(w.staging);
   if (w.prod) (void)hipFree(w.prod);
+  if (w.verify) (void)hipFree(w.verify);
   w = dbi::Workspace{};
 }
 
@@ -780,6 +781,8 @@ static const unsigned char kMagic[8] = {'D', 'B', 'K', 'V', 'C', 'A', 'C', 'H'};
 static const uint32_t kVersion = 1;      // model.cpp:1033: dense fp32 K then V
 static const uint32_t kVersionInt8 = 2;  // dense int8 (this library; v1 is fp32-only)
 
+}  // extern "C"
+
 namespace {
 
 // v2 payload of a dense int8 cache's first len positions, in file order:
@@ -835,6 +838,8 @@ hipError_t int8_sections(dbi_kv* kv, unsigned char* dev, uint32_t len, bool unpa
 }
 
 }  // namespace
+
+extern "C" {
 
 dbi_status dbi_kv_prefix_save(dbi_kv* kv, const char* path, const int32_t* tokens,
                               uint32_t len) {
@@ -1110,6 +1115,115 @@ dbi_status dbi_kv_export(dbi_kv* kv, uint32_t what, uint32_t layer, void* dst, s
         else
           std::memcpy(out + to * 4, tmp.data() + at * 4, 4);
       }
+  return DBI_OK;
+}
+
+/* ------------------------------------------------------------------ */
+/* speculative verify round, token side                                */
+/* ------------------------------------------------------------------ */
+
+}  // extern "C"
+
+namespace {
+
+// verify workspace: slice keys, then the arrival counter, then int32 staging
+// for the host variant (draft, verified argmaxes, accepted count)
+constexpr size_t kVerifyKeysBytes =
+    size_t(dbi::kMaxVerifyRows) * dbi::kMaxVerifySlices * sizeof(unsigned long long);
+constexpr size_t kVerifyCounterAt = kVerifyKeysBytes;
+constexpr size_t kVerifyIntsAt = kVerifyCounterAt + 256;
+constexpr size_t kVerifyBytes =
+    kVerifyIntsAt + sizeof(int32_t) * (dbi::kMaxVerifyDraft + dbi::kMaxVerifyRows + 1);
+
+dbi_status ensure_verify(dbi_kv* kv) {
+  if (kv->ws.verify != nullptr) return DBI_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(kv->stream, &cap), "capture status");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(DBI_ERR_INVALID,
+                "the first verify call of a handle allocates its workspace and cannot be "
+                "captured; make one call before capturing");
+  unsigned char* w = nullptr;
+  if (hipMalloc(reinterpret_cast<void**>(&w), kVerifyBytes) != hipSuccess)
+    return fail(DBI_ERR_NOMEM, "verify workspace allocation failed");
+  // the kernel leaves the counter at zero; a fresh one starts there
+  hipError_t e = hipMemsetAsync(w + kVerifyCounterAt, 0, sizeof(unsigned), kv->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(kv->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(w);
+    return hip_fail(e, "verify counter clear");
+  }
+  kv->ws.verify = w;
+  return DBI_OK;
+}
+
+dbi_status check_verify(const dbi_kv* kv, uint32_t k, uint32_t vocab) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (k == 0 || k > uint32_t(dbi::kMaxVerifyDraft))
+    return fail(DBI_ERR_INVALID, "verify needs 1 <= k <= " +
+                                     std::to_string(dbi::kMaxVerifyDraft) + " draft tokens");
+  if (vocab == 0 || vocab > (uint32_t(1) << 30))
+    return fail(DBI_ERR_INVALID, "verify needs 1 <= vocab <= 2^30");
+  return DBI_OK;
+}
+
+dbi_status verify_impl(dbi_kv* kv, uint32_t k, uint32_t vocab, const float* logits_dev,
+                       const int32_t* draft_dev, int32_t* verified_dev, int32_t* accepted_dev) {
+  if (dbi_status st = ensure_verify(kv)) return st;
+  dbi::VerifyCall c{};
+  c.logits = logits_dev;
+  c.draft = draft_dev;
+  c.verified = verified_dev;
+  c.accepted = accepted_dev;
+  c.keys = reinterpret_cast<unsigned long long*>(kv->ws.verify);
+  c.counter = reinterpret_cast<unsigned*>(kv->ws.verify + kVerifyCounterAt);
+  c.rows = static_cast<int>(k) + 1;
+  c.vocab = static_cast<int>(vocab);
+  HIP_TRY(dbi::launch_verify(c, kv->stream), "verify launch");
+  return DBI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+dbi_status dbi_spec_verify_async(dbi_kv* kv, uint32_t k, uint32_t vocab, const float* logits_dev,
+                                 const int32_t* draft_dev, int32_t* verified_dev,
+                                 int32_t* accepted_dev) {
+  if (dbi_status st = check_verify(kv, k, vocab)) return st;
+  if (logits_dev == nullptr || draft_dev == nullptr || verified_dev == nullptr ||
+      accepted_dev == nullptr)
+    return fail(DBI_ERR_INVALID, "null verify argument");
+  return verify_impl(kv, k, vocab, logits_dev, draft_dev, verified_dev, accepted_dev);
+}
+
+dbi_status dbi_kv_verify_commit(dbi_kv* kv, uint32_t pos, uint32_t k, uint32_t vocab,
+                                const float* logits_dev, const int32_t* draft, int32_t* merged,
+                                uint32_t* accepted) {
+  if (dbi_status st = check_verify(kv, k, vocab)) return st;
+  if (logits_dev == nullptr || draft == nullptr || merged == nullptr || accepted == nullptr)
+    return fail(DBI_ERR_INVALID, "null verify argument");
+  if (uint64_t(pos) + k + 1 > kv->n_seen)
+    return fail(DBI_ERR_INVALID,
+                "verify commit needs the round's k+1 rows in the cache (pos + k + 1 <= n_seen)");
+  if (dbi_status st = ensure_verify(kv)) return st;
+  int32_t* ints = reinterpret_cast<int32_t*>(kv->ws.verify + kVerifyIntsAt);
+  int32_t* d_draft = ints;
+  int32_t* d_ver = ints + dbi::kMaxVerifyDraft;
+  int32_t* d_acc = d_ver + dbi::kMaxVerifyRows;
+  HIP_TRY(hipMemcpyAsync(d_draft, draft, k * sizeof(int32_t), hipMemcpyHostToDevice, kv->stream),
+          "copy draft");
+  if (dbi_status st = verify_impl(kv, k, vocab, logits_dev, d_draft, d_ver, d_acc)) return st;
+  // verified and the count are adjacent: one readback
+  int32_t back[dbi::kMaxVerifyRows + 1];
+  HIP_TRY(hipMemcpyAsync(back, d_ver, (dbi::kMaxVerifyRows + 1) * sizeof(int32_t),
+                         hipMemcpyDeviceToHost, kv->stream),
+          "copy verified");
+  HIP_TRY(hipStreamSynchronize(kv->stream), "verify sync");
+  const uint32_t acc = static_cast<uint32_t>(back[dbi::kMaxVerifyRows]);
+  for (uint32_t i = 0; i <= acc; ++i) merged[i] = back[i];
+  *accepted = acc;
+  kv->n_seen = pos + acc + 1;
   return DBI_OK;
 }
 

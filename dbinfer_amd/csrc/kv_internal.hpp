@@ -120,6 +120,9 @@ struct Workspace {
   size_t staging_floats = 0;
   float* prod = nullptr;  // producer output: roped q, roped k, biased v rows
   size_t prod_floats = 0;
+  // verify round: slice keys, arrival counter and the host variant's token
+  // staging, one fixed-size allocation made on first use
+  unsigned char* verify = nullptr;
 };
 
 // Ring state of one attention call (resident set of n_seen = pos + 1).
@@ -213,5 +216,21 @@ hipError_t launch_prefix_codes(const KvGeom& g, int8_t* store, int8_t* file, int
 // store [L][nkv][dev_rows][inner] <-> file [L][rows][nkv][inner] (first rows)
 hipError_t launch_rows_pack(float* store, float* file, int n_layers, int nkv, int dev_rows,
                             int rows, int inner, bool unpack, hipStream_t st);
+
+// Speculative verify round, token side (verify.hip): argmax of each of the
+// rows = k+1 logit rows, then the merge against the k draft tokens.
+constexpr int kMaxVerifyDraft = 64;
+constexpr int kMaxVerifyRows = kMaxVerifyDraft + 1;
+constexpr int kMaxVerifySlices = 64;  // workgroups per row
+struct VerifyCall {
+  const float* logits;   // device [rows][vocab]
+  const int32_t* draft;  // device [rows - 1]
+  int32_t* verified;     // device [rows]
+  int32_t* accepted;     // device [1]
+  unsigned long long* keys;  // device [kMaxVerifyRows * kMaxVerifySlices]
+  unsigned* counter;     // device, zero between calls (the kernel resets it)
+  int rows, vocab;
+};
+hipError_t launch_verify(const VerifyCall& c, hipStream_t st);
 
 }  // namespace dbi

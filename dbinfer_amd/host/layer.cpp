@@ -117,4 +117,21 @@ std::int32_t speculative_commit(KVCache& kv, std::int32_t pos, std::size_t accep
   return next;
 }
 
+Result<std::size_t> speculative_verify(KVCache& kv, std::int32_t pos, std::size_t vocab,
+                                       const float* logits_dev,
+                                       std::span<const std::int32_t> draft,
+                                       std::vector<std::int32_t>& merged) {
+  merged.assign(draft.size() + 1, 0);
+  std::uint32_t accepted = 0;
+  const dbi_status st = dbi_kv_verify_commit(
+      kv.handle(), static_cast<std::uint32_t>(pos), static_cast<std::uint32_t>(draft.size()),
+      static_cast<std::uint32_t>(vocab), logits_dev, draft.data(), merged.data(), &accepted);
+  if (st != DBI_OK) {
+    merged.clear();
+    return Error{dbi_last_error(), "", 0};
+  }
+  merged.resize(accepted + 1);
+  return static_cast<std::size_t>(accepted);
+}
+
 }  // namespace dbinfer_amd::model

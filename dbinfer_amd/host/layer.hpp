@@ -106,6 +106,18 @@ std::size_t speculative_merge(std::span<const std::int32_t> draft,
 // keeps pos + accepted + 1 positions. Returns the new pos.
 std::int32_t speculative_commit(KVCache& kv, std::int32_t pos, std::size_t accepted);
 
+// A verify round's token side plus its commit, with the argmax of the
+// target's k+1 logit rows and the merge on the device (dbi_kv_verify_commit;
+// speculative.cpp:69-82 with sample::argmax): logits_dev is device memory
+// [draft.size()+1][vocab] and never leaves it. merged is cleared, then
+// receives what speculative_merge emits (the accepted draft prefix, then the
+// correction or the bonus token); the cache keeps pos + accepted + 1
+// positions. Returns the accepted count.
+Result<std::size_t> speculative_verify(KVCache& kv, std::int32_t pos, std::size_t vocab,
+                                       const float* logits_dev,
+                                       std::span<const std::int32_t> draft,
+                                       std::vector<std::int32_t>& merged);
+
 }  // namespace dbinfer_amd::model
 
 #endif  // DBINFER_AMD_HOST_LAYER_HPP

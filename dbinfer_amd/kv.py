@@ -236,6 +236,22 @@ class HipKV:
             self._h, layer, pos0, n, n_heads, scale, q_dev, k_dev, v_dev, q_bias_dev,
             k_bias_dev, v_bias_dev, out_dev))
 
+    # ---- speculative verify round (token side)
+    def spec_verify_async(self, k: int, vocab: int, logits_dev: int, draft_dev: int,
+                          verified_dev: int, accepted_dev: int) -> None:
+        _check(self._lib, self._lib.dbi_spec_verify_async(
+            self._h, k, vocab, logits_dev, draft_dev, verified_dev, accepted_dev))
+
+    def verify_commit(self, pos: int, k: int, vocab: int, logits_dev: int, draft):
+        """(accepted, merged tokens); the cache keeps pos + accepted + 1 positions."""
+        d = np.ascontiguousarray(draft, dtype=np.int32)
+        assert d.size == k
+        merged = np.zeros(k + 1, np.int32)
+        acc = ctypes.c_uint32()
+        _check(self._lib, self._lib.dbi_kv_verify_commit(
+            self._h, pos, k, vocab, logits_dev, _ptr(d), _ptr(merged), ctypes.byref(acc)))
+        return int(acc.value), merged[: acc.value + 1].tolist()
+
     # ---- prefix cache
     def save_prefix(self, path: str, tokens) -> None:
         t = np.ascontiguousarray(tokens, dtype=np.int32)

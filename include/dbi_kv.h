@@ -185,6 +185,36 @@ dbi_status dbi_kv_chunk_qkv_async(dbi_kv* kv, uint32_t layer, uint32_t pos0, uin
                                   const float* q_bias_dev, const float* k_bias_dev,
                                   const float* v_bias_dev, float* out_dev);
 
+/* Token side of one speculative verify round, on the device. Replaces the
+ * host loop of speculative_generate (speculative.cpp:69-76): sample::argmax
+ * of each of the k+1 chunk rows (sample.cpp:11-28), then speculative_merge of
+ * the k draft proposals against them (speculative.cpp:10-23).
+ * logits_dev: device [k+1][vocab] fp32, the target model's rows for the chunk
+ * [last, draft...]; draft_dev: device [k] int32.
+ * Writes verified_dev[0..k], the argmax of every row (the first maximum wins;
+ * NaNs never win, and a NaN in slot 0 gives 0, as the reference's strict >
+ * scan does), and *accepted_dev = j, the length of the accepted draft prefix.
+ * The merged tokens are verified_dev[0..j] (the draft prefix equals them).
+ * 1 <= k <= 64, 1 <= vocab <= 2^30. Ordered on the handle's stream; the
+ * handle's small verify workspace is allocated on its first verify call, so
+ * make one call before capturing a graph. Verify calls on one handle must not
+ * overlap (they share an arrival counter). */
+dbi_status dbi_spec_verify_async(dbi_kv* kv, uint32_t k, uint32_t vocab, const float* logits_dev,
+                                 const int32_t* draft_dev, int32_t* verified_dev,
+                                 int32_t* accepted_dev);
+
+/* A verify round with the cache commit, blocking: dbi_spec_verify_async on a
+ * device copy of the host draft[k], then the argmaxes and the count copied
+ * back (4(k+2) bytes; the logits stay in HBM), then the cache truncated to
+ * pos + accepted + 1. The round appended its k+1 rows at pos..pos+k (the
+ * chunk of speculative.cpp:69); speculative.cpp:82 moves pos past the accepted
+ * tokens and the correction, and the next round's rows overwrite the rest.
+ * merged receives accepted + 1 tokens (room for k+1). Needs
+ * pos + k + 1 <= n_seen. */
+dbi_status dbi_kv_verify_commit(dbi_kv* kv, uint32_t pos, uint32_t k, uint32_t vocab,
+                                const float* logits_dev, const int32_t* draft, int32_t* merged,
+                                uint32_t* accepted);
+
 /* Model::save_kv_prefix (model.hpp:292-293, model.cpp:1072-1107): writes the
  * DBKVCACH v1 file of positions [0, len) with the token ids from a dense
  * fp32 cache. A dense int8 cache writes version 2, which has no counterpart

@@ -748,3 +748,22 @@ size_t ok_spec_merge(const int32_t* draft, size_t k, const int32_t* target, int3
   if (n_out) *n_out = n;
   return j;
 }
+
+/* ------------------------------------------------------------------ */
+/* greedy argmax (sample.cpp:11-28)                                    */
+/* ------------------------------------------------------------------ */
+
+/* A scan that replaces the best only on a strictly greater value: ties keep
+ * the earlier index, a NaN never replaces (every comparison with it is
+ * false), and a NaN in slot 0 is never replaced either, so the answer is 0. */
+int32_t ok_argmax(const float* logits, size_t n) {
+  int32_t best = 0;
+  float bestv = logits[0];
+  for (size_t i = 1; i < n; ++i) {
+    if (logits[i] > bestv) {
+      bestv = logits[i];
+      best = (int32_t)i;
+    }
+  }
+  return best;
+}

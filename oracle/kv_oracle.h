@@ -31,6 +31,8 @@
  *                      chunk == per-row decode, int8 vs fp32 rel-L2 bound
  *   prefix save/load   byte-level format check, round trip, every error path
  *   ok_spec_merge      speculative_test merge vectors
+ *   ok_argmax          sample_test argmax vectors, plus NaN / signed-zero /
+ *                      infinity cases whose answer the strict-greater scan fixes
  */
 #ifndef DBI_KV_ORACLE_H
 #define DBI_KV_ORACLE_H
@@ -140,6 +142,9 @@ int okv_prefix_load(okv* kv, const char* path, const int32_t* tokens, size_t n_t
 /* speculative.cpp:10-23. out must hold k+1 entries. returns accepted count. */
 size_t ok_spec_merge(const int32_t* draft, size_t k, const int32_t* target, int32_t* out,
                      size_t* n_out);
+
+/* sample.cpp:11-28: greedy argmax, first maximum wins (strict >), n >= 1. */
+int32_t ok_argmax(const float* logits, size_t n);
 
 #ifdef __cplusplus
 }

@@ -64,6 +64,7 @@ _SIGS = {
     "okv_prefix_load": (ctypes.c_int, [_P, ctypes.c_char_p, _vp, _sz, ctypes.POINTER(_sz),
                                        ctypes.c_char_p, _sz]),
     "ok_spec_merge": (_sz, [_vp, _sz, _vp, _vp, ctypes.POINTER(_sz)]),
+    "ok_argmax": (ctypes.c_int32, [_vp, _sz]),
 }
 
 _LIB = None
@@ -131,6 +132,12 @@ def spec_merge(draft, target) -> tuple[int, list[int]]:
     acc = load().ok_spec_merge(d.ctypes.data, d.size, t.ctypes.data, out.ctypes.data,
                                ctypes.byref(n))
     return int(acc), out[: n.value].tolist()
+
+
+def argmax(logits) -> int:
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    assert x.size >= 1
+    return int(load().ok_argmax(x.ctypes.data, x.size))
 
 
 class OracleError(RuntimeError):

@@ -16,6 +16,8 @@
 #include <string>
 #include <vector>
 
+#include <hip/hip_runtime_api.h>
+
 #include "kv_cache.hpp"
 #include "kv_oracle.h"
 #include "layer.hpp"
@@ -403,6 +405,49 @@ void test_speculative_rollback() {
         "next round after rollback == cache without the rejected rows (bitwise)");
 }
 
+void test_speculative_verify() {
+  // a verify round's tokens on the device: argmax of the k+1 logit rows
+  // (ties planted), merge against a draft that diverges at 2, then commit
+  const std::size_t cap = 64, pos = 30, k = 4, vocab = 50000, kn = 2 * 64;
+  KVCache kv(1, cap, 2, 64);
+  Lcg rng{0x7e57};
+  std::vector<float> kk((pos + k + 1) * kn), vv((pos + k + 1) * kn);
+  for (auto& x : kk) x = rng.next();
+  for (auto& x : vv) x = rng.next();
+  kv.append_n(0, 0, pos + k + 1, kk.data(), vv.data());
+  std::vector<float> logits((k + 1) * vocab);
+  for (auto& x : logits) x = rng.next();
+  std::vector<std::int32_t> want(k + 1);
+  for (std::size_t r = 0; r <= k; ++r) {
+    logits[r * vocab + 4000 + r] = 3.0f;  // tied maximum: the earlier index wins
+    logits[r * vocab + 30000 + r] = 3.0f;
+    want[r] = ok_argmax(logits.data() + r * vocab, vocab);
+  }
+  const std::vector<std::int32_t> draft = {want[0], want[1], want[2] + 1, want[3]};
+  std::vector<std::int32_t> out(k + 1);
+  std::size_t n_out = 0;
+  const std::size_t acc = ok_spec_merge(draft.data(), k, want.data(), out.data(), &n_out);
+  out.resize(n_out);
+  float* d = nullptr;
+  const bool dev = hipMalloc(reinterpret_cast<void**>(&d), logits.size() * sizeof(float)) ==
+                       hipSuccess &&
+                   hipMemcpy(d, logits.data(), logits.size() * sizeof(float),
+                             hipMemcpyHostToDevice) == hipSuccess;
+  check(dev, "verify: device logits");
+  if (!dev) return;
+  std::vector<std::int32_t> merged;
+  const auto r = dbinfer_amd::model::speculative_verify(kv, static_cast<std::int32_t>(pos), vocab,
+                                                        d, draft, merged);
+  check(want[0] == 4000 && acc == 2, "verify: oracle argmax keeps the first of a tie");
+  check(r && *r == acc && merged == out && kv.n_seen() == pos + acc + 1,
+        "verify: device argmax + merge == oracle, cache keeps pos + accepted + 1");
+  const auto e = dbinfer_amd::model::speculative_verify(kv, static_cast<std::int32_t>(pos), vocab,
+                                                        d, draft, merged);
+  check(!e && merged.empty() && kv.n_seen() == pos + acc + 1,
+        "verify: a round whose rows are not in the cache is refused, cache unchanged");
+  (void)hipFree(d);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -426,6 +471,7 @@ int main(int argc, char** argv) {
     test_producer_parity({4, 16, KvDtype::F32}, {28, 4, 128, 1e6f}, 30, "ring fp32 gqa7 hd128");
     test_prefix_cache();
     test_speculative_rollback();
+    test_speculative_verify();
   }
   std::printf("---\n%d checks failed\n", g_failures);
   return g_failures == 0 ? 0 : 1;

@@ -8,6 +8,8 @@
 2. Writes kv_ring_cases.json: the case matrix of tests/kv_ring_test.cpp:90-97.
 3. Writes spec_merge_cases.json: the direct merge vectors of
    tests/speculative_test.cpp:104-133.
+4. Writes argmax_cases.json: the greedy argmax vectors of
+   tests/sample_test.cpp:38-50.
 
 Run from the repository root with the reference checkout mounted:
     python tests/golden/make_fixtures.py [/root/reference]
@@ -42,6 +44,13 @@ SPEC_MERGE_CASES = [  # speculative_test.cpp:104-133: draft, target, accepted, m
     {"draft": [5, 6], "target": [9, 8, 7], "accepted": 0, "out": [9]},
 ]
 
+ARGMAX_CASES = [  # sample_test.cpp:38-50: logits, expected index
+    {"logits": [0.1, 0.9, 0.3, -1.0], "index": 1},
+    {"logits": [5.0, 1.0, 5.0, 5.0], "index": 0},
+    {"logits": [-3.0, -2.0, -2.0], "index": 1},
+    {"logits": [42.0], "index": 0},
+]
+
 
 def main(ref: str) -> None:
     src = os.path.join(ref, "tests", "golden")
@@ -62,6 +71,8 @@ def main(ref: str) -> None:
     json.dump({"cases": KV_RING_CASES}, open(os.path.join(HERE, "kv_ring_cases.json"), "w"))
     json.dump({"cases": SPEC_MERGE_CASES},
               open(os.path.join(HERE, "spec_merge_cases.json"), "w"), indent=1)
+    json.dump({"cases": ARGMAX_CASES}, open(os.path.join(HERE, "argmax_cases.json"), "w"),
+              indent=1)
     print("fixtures written to", HERE)
 
 

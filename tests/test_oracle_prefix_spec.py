@@ -1,5 +1,5 @@
-"""Pins the oracle's prefix cache (model.cpp:1023-1156) and speculative merge
-(speculative.cpp:10-23).
+"""Pins the oracle's prefix cache (model.cpp:1023-1156), speculative merge
+(speculative.cpp:10-23) and greedy argmax (sample.cpp:11-28).
 
 Prefix: the byte layout of DBKVCACH v1 is checked field by field with
 struct/numpy (independent of the writer), load(save(x)) restores K/V bitwise
@@ -7,6 +7,11 @@ and sets n_seen, and every validation error of model.cpp:1117-1148 is hit in
 the reference's order with its message, leaving the cache untouched.
 Merge: the direct vectors of tests/speculative_test.cpp:104-133 and the
 synthetic oracle-greedy stream property of :136-149.
+Argmax: the vectors of tests/sample_test.cpp:38-50; the cases whose answer a
+strict-greater scan fixes (NaN in slot 0 or later, signed zeros, infinities);
+on NaN-free rows with many ties, numpy's argmax (first occurrence of the
+maximum); and on rows with NaNs, the characterisation "the earliest index whose
+value equals the maximum of the non-NaN values, or 0 when slot 0 is NaN".
 """
 import json
 import os
@@ -191,3 +196,48 @@ def test_spec_stream_equals_greedy(seed, k, wrong):
         last = merged[-1]
         gen.extend(merged)
     assert gen[:n] == greedy
+
+
+ARGMAX = json.load(open(os.path.join(GOLDEN, "argmax_cases.json")))["cases"]
+
+
+@pytest.mark.parametrize("case", ARGMAX)
+def test_argmax_vectors(case):
+    assert pyoracle.argmax(case["logits"]) == case["index"]
+
+
+NAN, INF = float("nan"), float("inf")
+
+
+@pytest.mark.parametrize("row,want", [
+    ([NAN, 1.0, 2.0], 0),        # a NaN best is never replaced
+    ([1.0, NAN, 2.0], 2),        # a later NaN is skipped
+    ([NAN, NAN, NAN], 0),
+    ([-0.0, 0.0, -0.0], 0),      # 0.0 > -0.0 is false: equal values
+    ([0.0, -0.0], 0),
+    ([-INF, -INF], 0),
+    ([-INF, NAN, -1.0], 2),
+    ([3.0, INF, INF], 1),
+    ([-1.0, -INF, -0.5, NAN], 2),
+])
+def test_argmax_special_values(row, want):
+    assert pyoracle.argmax(row) == want
+
+
+def _first_max(x):
+    if np.isnan(x[0]):
+        return 0
+    ok = ~np.isnan(x)
+    m = x[ok].max()
+    return int(np.flatnonzero(ok & (x == m))[0])
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_argmax_random_rows(seed):
+    rng = np.random.default_rng(seed)
+    for n in (1, 2, 7, 64, 1000, 4097):
+        x = rng.integers(-4, 5, n).astype(np.float32)  # many ties
+        assert pyoracle.argmax(x) == int(np.argmax(x))
+        y = rng.standard_normal(n).astype(np.float32)
+        y[rng.random(n) < 0.1] = np.nan
+        assert pyoracle.argmax(y) == _first_max(y)
