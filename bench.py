@@ -552,6 +552,8 @@ def main():
     ap.add_argument("--config-steps", type=int, default=30)
     ap.add_argument("--configs-cpu", action="store_true",
                     help="with --configs: also time the CPU oracle on one layer of each config")
+    ap.add_argument("--verify", action="store_true",
+                    help="time the verify round's token side (argmax + merge) at C5's shape")
     ap.add_argument("--ctx-sweep", action="store_true",
                     help="instead of the bench line, config 3's shape at ctx 8k, 16k, 32k")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -581,6 +583,16 @@ def main():
         return
     if args.ctx_sweep:
         run_ctx_sweep(torch, HipKV, F32, INT8, args)
+        return
+    if args.verify:
+        # C5's verify round, token side, at k = 4 and 8 (Qwen3's vocabulary)
+        kv = HipKV(1, 64, 1, 64)
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(5)
+        for k in (4, 8):
+            print(json.dumps({"config": "C5 verify tokens", **verify_tokens(torch, kv, k, gen,
+                                                                             args)}), flush=True)
+        kv.close()
         return
     scale = float(np.float32(1.0) / np.sqrt(np.float32(HD)))
     # every launch and event goes on one non-default stream (the kernels'
