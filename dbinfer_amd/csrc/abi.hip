@@ -470,6 +470,11 @@ dbi_status dbi_kv_create(const dbi_kv_config* cfg, dbi_kv** out) {
     return fail(DBI_ERR_INVALID, "unknown dtype");
   const uint64_t cap = cfg->window > 0 ? uint64_t(cfg->n_sink) + cfg->window : cfg->max_seq;
   if (cap == 0 || cap > 0x7fffffffull) return fail(DBI_ERR_INVALID, "capacity out of range");
+  // kernels address one kv head's K or V array with 32-bit byte offsets
+  const uint64_t capg = (cap + dbi::kCapAlign - 1) / dbi::kCapAlign * dbi::kCapAlign;
+  if (capg * cfg->head_dim * (cfg->dtype == DBI_KV_INT8 ? 1 : 4) > 0x7fffffffull)
+    return fail(DBI_ERR_INVALID,
+                "capacity too large: one kv head's K or V array must stay below 2 GiB");
   if (cfg->window > 0 && !(cfg->rope_theta > 0.0f))
     return fail(DBI_ERR_INVALID, "ring cache needs rope_theta > 0");
 

@@ -4,8 +4,9 @@
  * This is the drop-in boundary for the reference engine's KV cache
  * (src/model/model.hpp:102-214, src/model/model.cpp:258-474), its three
  * single-query attention kernels and the causal chunk attention
- * (model.cpp:567-728, 956-981), and its prefix cache I/O
- * (model.cpp:1023-1156). Plain C types only; no exceptions cross it.
+ * (model.cpp:567-728, 956-981), its prefix cache I/O
+ * (model.cpp:1023-1156), and the token side of a speculative verify round
+ * (speculative.cpp:64-82). Plain C types only; no exceptions cross it.
  *
  * Conventions
  *  - Every entry point returns a dbi_status. On failure the handle's state is
@@ -68,7 +69,9 @@ const char* dbi_last_error(void);
 
 /* KVCache::KVCache (model.hpp:119-120, model.cpp:258-297) and
  * Model::configure_kv (model.hpp:284). Allocates and zero-fills all device
- * storage on the current HIP device. */
+ * storage on the current HIP device. One kv head's K (or V) array, capacity
+ * rounded up to 64 x head_dim x element size, must stay below 2 GiB (e.g.
+ * up to ~4M positions at head_dim 128 fp32). */
 dbi_status dbi_kv_create(const dbi_kv_config* cfg, dbi_kv** out);
 void dbi_kv_destroy(dbi_kv* kv);
 dbi_status dbi_kv_get_config(const dbi_kv* kv, dbi_kv_config* out);

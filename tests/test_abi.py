@@ -50,6 +50,10 @@ def test_create_rejects_bad_config_without_gpu():
     cfg = _lib.KvConfig(1, 16, 1, 64, 0, 0, 7, 1e4)
     assert lib.dbi_kv_create(ctypes.byref(cfg), ctypes.byref(h)) == _lib.DBI_ERR_INVALID
     assert lib.dbi_kv_create(None, ctypes.byref(h)) == _lib.DBI_ERR_INVALID
+    # one head's fp32 K array at 2^22 positions x hd 128 is 2 GiB: refused
+    cfg = _lib.KvConfig(1, 1 << 22, 1, 128, 0, 0, 0, 1e4)
+    assert lib.dbi_kv_create(ctypes.byref(cfg), ctypes.byref(h)) == _lib.DBI_ERR_INVALID
+    assert b"below 2 GiB" in lib.dbi_last_error()
 
 
 def test_no_oracle_in_product_library():
