@@ -30,8 +30,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kPerThread = 32;   // loads in flight per thread (one batch)
-constexpr int kSliceTarget = 32;  // elements per thread a slice aims for
+constexpr int kPerThread = 32;  // loads in flight per thread (one batch)
 
 using u64 = unsigned long long;
 
@@ -166,9 +165,10 @@ hipError_t launch_verify(const VerifyCall& c, hipStream_t st) {
   a.counter = c.counter;
   a.rows = c.rows;
   a.vocab = c.vocab;
-  // small slices spread a row over many CUs; a slice of up to
-  // kThreads * kPerThread elements is one load batch
-  const long per = static_cast<long>(kThreads) * kSliceTarget;
+  // slices of one load batch (kThreads * kPerThread elements) while a row
+  // fits in kMaxVerifySlices of them, longer slices past that; halving the
+  // slice (twice the workgroups and arrivals) measured slower
+  const long per = static_cast<long>(kThreads) * kPerThread;
   long nb = (static_cast<long>(c.vocab) + per - 1) / per;
   nb = nb < 1 ? 1 : (nb > kMaxVerifySlices ? kMaxVerifySlices : nb);
   a.span = static_cast<int>((c.vocab + nb - 1) / nb);
