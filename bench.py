@@ -403,6 +403,47 @@ def verify_tokens(torch, kv, k, gen, args):
     return res
 
 
+# (config, dim, n_heads * head_dim) of the output projection after attention
+OPROJ_SHAPES = [("C1 TinyLlama", 2048, 2048), ("C3 Llama-3.2-3B", 3072, 3072),
+                ("C4 Qwen2.5-7B", 3584, 3584), ("C5 Qwen3-8B", 4096, 4096)]
+
+
+def run_oproj(torch, HipKV, args):
+    """decode_layer's step after attention (model.cpp:773-774): the output
+    projection of the attention row plus the residual add, fp32 and f16
+    weights, one call per layer with the layer's own weights (graph replay),
+    and its GB/s against the HBM peak (the weights are read once)."""
+    from dbinfer_amd.kv import W_F16, W_F32
+
+    kv = HipKV(1, 64, 1, 64)
+    for name, dim, n_in in OPROJ_SHAPES:
+        L_ = 16  # distinct weight matrices, so no call reads another's from cache
+        for wname, wtype, dt, esz in (("f32", W_F32, torch.float32, 4),
+                                      ("f16", W_F16, torch.float16, 2)):
+            w = (torch.randn(L_, dim, n_in, device="cuda") * 0.05).to(dt)
+            attn = torch.randn(L_, n_in, device="cuda")
+            x = torch.zeros(L_, dim, device="cuda")
+
+            def call(s_):
+                kv.set_stream(s_.cuda_stream)
+                for layer in range(L_):
+                    kv.oproj_residual_async(wtype, w[layer].data_ptr(), attn[layer].data_ptr(),
+                                            x[layer].data_ptr(), dim, n_in)
+
+            g = capture(torch, call)
+            for _ in range(3):
+                g.replay()
+            us = 1000.0 * time_graph(torch, g, args.config_steps) / L_
+            byts = dim * n_in * esz
+            print(json.dumps({"oproj": name, "weights": wname, "dim": dim, "in": n_in,
+                              "us": round(us, 3), "weight_bytes": byts,
+                              "GBs": round(byts / (us * 1e-6) / 1e9, 1),
+                              "frac_of_peak": round(byts / (us * 1e-6) / 1e9 / PEAK_GBS, 4)}),
+                  flush=True)
+            del g, w, attn, x
+    kv.close()
+
+
 def run_ctx_sweep(torch, HipKV, F32, INT8, args):
     """Config 3's shape over the target context range (8k-32k): one JSON line
     per (context, KV dtype) with the fused decode step and the attention-only
@@ -552,6 +593,8 @@ def main():
     ap.add_argument("--config-steps", type=int, default=30)
     ap.add_argument("--configs-cpu", action="store_true",
                     help="with --configs: also time the CPU oracle on one layer of each config")
+    ap.add_argument("--oproj", action="store_true",
+                    help="time the output projection + residual add at the configs' shapes")
     ap.add_argument("--verify", action="store_true",
                     help="time the verify round's token side (argmax + merge) at C5's shape")
     ap.add_argument("--ctx-sweep", action="store_true",
@@ -583,6 +626,9 @@ def main():
         return
     if args.ctx_sweep:
         run_ctx_sweep(torch, HipKV, F32, INT8, args)
+        return
+    if args.oproj:
+        run_oproj(torch, HipKV, args)
         return
     if args.verify:
         # C5's verify round, token side, at k = 4 and 8 (Qwen3's vocabulary)

@@ -24,6 +24,7 @@ DBI_ERR_FORMAT = 6
 
 DBI_KV_F32 = 0
 DBI_KV_INT8 = 1
+DBI_W_F32, DBI_W_F16 = 0, 1
 
 EXPORT = {
     "k": 0, "v": 1, "k8": 2, "v8": 3, "k_scale": 4, "v_scale": 5,
@@ -77,6 +78,7 @@ SIGNATURES = {
     "dbi_kv_chunk_qkv_async": (_st, [_vp, _u32, _u32, _u32, _u32, _f32] + [_vp] * 7),
     "dbi_spec_verify_async": (_st, [_vp, _u32, _u32, _vp, _vp, _vp, _vp]),
     "dbi_kv_verify_commit": (_st, [_vp, _u32, _u32, _u32, _vp, _vp, _vp, _vp]),
+    "dbi_oproj_residual_async": (_st, [_vp, _u32, _vp, _vp, _vp, _u32, _u32]),
     "dbi_kv_prefix_save": (_st, [_vp, ctypes.c_char_p, _vp, _u32]),
     "dbi_kv_prefix_load": (_st, [_vp, ctypes.c_char_p, _vp, _u32, ctypes.POINTER(_u32)]),
     "dbi_kv_export_bytes": (ctypes.c_size_t, [_vp, _u32]),

@@ -1232,4 +1232,33 @@ dbi_status dbi_kv_verify_commit(dbi_kv* kv, uint32_t pos, uint32_t k, uint32_t v
   return DBI_OK;
 }
 
+/* ------------------------------------------------------------------ */
+/* output projection + residual add                                    */
+/* ------------------------------------------------------------------ */
+
+dbi_status dbi_oproj_residual_async(dbi_kv* kv, uint32_t wtype, const void* w_dev,
+                                    const float* attn_dev, float* x_dev, uint32_t dim,
+                                    uint32_t in) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (w_dev == nullptr || attn_dev == nullptr || x_dev == nullptr)
+    return fail(DBI_ERR_INVALID, "null output-projection argument");
+  if (wtype != DBI_W_F32 && wtype != DBI_W_F16)
+    return fail(DBI_ERR_UNSUPPORTED, "output projection serves fp32 and f16 weights only");
+  if (dim == 0 || in == 0 || in % 8 != 0 || dim > (uint32_t(1) << 30) || in > (uint32_t(1) << 24))
+    return fail(DBI_ERR_INVALID,
+                "output projection needs dim in [1, 2^30] and in a positive multiple of 8 "
+                "(at most 2^24)");
+  if (((reinterpret_cast<uintptr_t>(w_dev) | reinterpret_cast<uintptr_t>(attn_dev)) & 15) != 0)
+    return fail(DBI_ERR_INVALID, "output projection needs 16-byte aligned weights and attn");
+  dbi::OprojCall c{};
+  c.w = w_dev;
+  c.attn = attn_dev;
+  c.x = x_dev;
+  c.dim = static_cast<int>(dim);
+  c.in = static_cast<int>(in);
+  c.f16 = wtype == DBI_W_F16;
+  HIP_TRY(dbi::launch_oproj(c, kv->stream), "output projection launch");
+  return DBI_OK;
+}
+
 }  // extern "C"

@@ -233,4 +233,15 @@ struct VerifyCall {
 };
 hipError_t launch_verify(const VerifyCall& c, hipStream_t st);
 
+// Output projection + residual add of decode_layer (oproj.hip):
+// x[o] += sum_i w[o][i] * attn[i], w fp32 or f16 [dim][in], in % 8 == 0.
+struct OprojCall {
+  const void* w;
+  const float* attn;
+  float* x;
+  int dim, in;
+  bool f16;
+};
+hipError_t launch_oproj(const OprojCall& c, hipStream_t st);
+
 }  // namespace dbi

@@ -19,6 +19,8 @@ from . import _lib
 
 F32 = _lib.DBI_KV_F32
 INT8 = _lib.DBI_KV_INT8
+W_F32 = _lib.DBI_W_F32
+W_F16 = _lib.DBI_W_F16
 
 
 class DbiError(RuntimeError):
@@ -251,6 +253,12 @@ class HipKV:
         _check(self._lib, self._lib.dbi_kv_verify_commit(
             self._h, pos, k, vocab, logits_dev, _ptr(d), _ptr(merged), ctypes.byref(acc)))
         return int(acc.value), merged[: acc.value + 1].tolist()
+
+    # ---- output projection + residual (decode_layer's step after attention)
+    def oproj_residual_async(self, wtype: int, w_dev: int, attn_dev: int, x_dev: int, dim: int,
+                             n_in: int) -> None:
+        _check(self._lib, self._lib.dbi_oproj_residual_async(self._h, wtype, w_dev, attn_dev,
+                                                             x_dev, dim, n_in))
 
     # ---- prefix cache
     def save_prefix(self, path: str, tokens) -> None:

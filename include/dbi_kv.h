@@ -5,8 +5,10 @@
  * (src/model/model.hpp:102-214, src/model/model.cpp:258-474), its three
  * single-query attention kernels and the causal chunk attention
  * (model.cpp:567-728, 956-981), its prefix cache I/O
- * (model.cpp:1023-1156), and the token side of a speculative verify round
- * (speculative.cpp:64-82). Plain C types only; no exceptions cross it.
+ * (model.cpp:1023-1156), the token side of a speculative verify round
+ * (speculative.cpp:64-82), and the output projection + residual add that
+ * follows attention (model.cpp:773-774). Plain C types only; no exceptions
+ * cross it.
  *
  * Conventions
  *  - Every entry point returns a dbi_status. On failure the handle's state is
@@ -217,6 +219,24 @@ dbi_status dbi_spec_verify_async(dbi_kv* kv, uint32_t k, uint32_t vocab, const f
 dbi_status dbi_kv_verify_commit(dbi_kv* kv, uint32_t pos, uint32_t k, uint32_t vocab,
                                 const float* logits_dev, const int32_t* draft, int32_t* merged,
                                 uint32_t* accepted);
+
+/* Weight element types of dbi_oproj_residual_async (GgmlType F32 / F16). */
+enum { DBI_W_F32 = 0, DBI_W_F16 = 1 };
+
+/* The step after attention in Model::decode_layer (model.cpp:773-774):
+ * matvec_quant(attn_output, attn, proj, dim, nh*hd) then x[i] += proj[i],
+ * for unquantized weights: fp32 (tensor::matvec, matmul.cpp:36-43) or f16
+ * (tensor::matvec_f16, matmul.cpp:45-54). w_dev: device [dim][in] row-major;
+ * attn_dev: device [in] (the attention row, in = n_heads*head_dim); x_dev:
+ * device [dim], the residual stream, updated in place. in must be a multiple
+ * of 8, and w_dev and attn_dev 16-byte aligned. The lanes of a row sum in a
+ * tree, so proj agrees with the reference's sequential sum to the rounding
+ * of a dot product, not bit for bit. GGUF block types (Q8_0, Q4_K, ...)
+ * return DBI_ERR_UNSUPPORTED. Ordered on the handle's stream; allocates
+ * nothing. */
+dbi_status dbi_oproj_residual_async(dbi_kv* kv, uint32_t wtype, const void* w_dev,
+                                    const float* attn_dev, float* x_dev, uint32_t dim,
+                                    uint32_t in);
 
 /* Model::save_kv_prefix (model.hpp:292-293, model.cpp:1072-1107): writes the
  * DBKVCACH v1 file of positions [0, len) with the token ids from a dense

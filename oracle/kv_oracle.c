@@ -767,3 +767,41 @@ int32_t ok_argmax(const float* logits, size_t n) {
   }
   return best;
 }
+
+/* ------------------------------------------------------------------ */
+/* output projection + residual (model.cpp:773-774)                    */
+/* ------------------------------------------------------------------ */
+
+/* sign, 5-bit exponent, 10-bit mantissa; subnormals are man * 2^-24 */
+float ok_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  uint32_t bits;
+  if (e == 0) {
+    const float v = ldexpf((float)m, -24);
+    memcpy(&bits, &v, 4);
+    bits |= sign;
+  } else if (e == 31) {
+    bits = sign | 0x7f800000u | (m << 13);
+  } else {
+    bits = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+void ok_oproj_residual(const void* w, int f16, const float* attn, float* x, size_t dim,
+                       size_t in) {
+  for (size_t o = 0; o < dim; ++o) {
+    float acc = 0.0f;
+    if (f16) {
+      const uint16_t* row = (const uint16_t*)w + o * in;
+      for (size_t i = 0; i < in; ++i) acc = fmaf(ok_f16_to_f32(row[i]), attn[i], acc);
+    } else {
+      const float* row = (const float*)w + o * in;
+      for (size_t i = 0; i < in; ++i) acc += row[i] * attn[i];
+    }
+    x[o] += acc;
+  }
+}

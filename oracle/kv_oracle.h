@@ -33,6 +33,10 @@
  *   ok_spec_merge      speculative_test merge vectors
  *   ok_argmax          sample_test argmax vectors, plus NaN / signed-zero /
  *                      infinity cases whose answer the strict-greater scan fixes
+ *   ok_f16_to_f32      all 65536 half values against numpy's float16 -> float32
+ *   ok_oproj_residual  exact on small-integer data (every partial sum is an
+ *                      integer below 2^24, so any order is exact); fp64 dot
+ *                      product within the sequential-sum rounding bound
  */
 #ifndef DBI_KV_ORACLE_H
 #define DBI_KV_ORACLE_H
@@ -145,6 +149,14 @@ size_t ok_spec_merge(const int32_t* draft, size_t k, const int32_t* target, int3
 
 /* sample.cpp:11-28: greedy argmax, first maximum wins (strict >), n >= 1. */
 int32_t ok_argmax(const float* logits, size_t n);
+
+/* dequant.cpp:14: IEEE half to float (exact). */
+float ok_f16_to_f32(uint16_t h);
+/* model.cpp:773-774 with tensor::matvec (matmul.cpp:36-43, f16 = 0) or
+ * tensor::matvec_f16 (matmul.cpp:45-54, f16 = 1): proj[o] = sequential
+ * sum over i of w[o][i] * attn[i], then x[o] += proj[o]. */
+void ok_oproj_residual(const void* w, int f16, const float* attn, float* x, size_t dim,
+                       size_t in);
 
 #ifdef __cplusplus
 }

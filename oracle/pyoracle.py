@@ -65,6 +65,8 @@ _SIGS = {
                                        ctypes.c_char_p, _sz]),
     "ok_spec_merge": (_sz, [_vp, _sz, _vp, _vp, ctypes.POINTER(_sz)]),
     "ok_argmax": (ctypes.c_int32, [_vp, _sz]),
+    "ok_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+    "ok_oproj_residual": (None, [_vp, ctypes.c_int, _vp, _vp, _sz, _sz]),
 }
 
 _LIB = None
@@ -138,6 +140,22 @@ def argmax(logits) -> int:
     x = np.ascontiguousarray(logits, dtype=np.float32)
     assert x.size >= 1
     return int(load().ok_argmax(x.ctypes.data, x.size))
+
+
+def f16_to_f32(h: int) -> float:
+    return float(load().ok_f16_to_f32(h))
+
+
+def oproj_residual(w, attn, x):
+    """x + w @ attn with the reference's sequential sums; w fp32 or float16
+    [dim][in] (float16 passed as its bits)."""
+    f16 = np.asarray(w).dtype == np.float16
+    wc = np.ascontiguousarray(w)
+    a = np.ascontiguousarray(attn, dtype=np.float32)
+    out = np.array(x, dtype=np.float32, copy=True)
+    dim, n_in = wc.shape
+    load().ok_oproj_residual(wc.ctypes.data, int(f16), a.ctypes.data, out.ctypes.data, dim, n_in)
+    return out
 
 
 class OracleError(RuntimeError):

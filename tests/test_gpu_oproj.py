@@ -1,0 +1,116 @@
+"""Output projection + residual add on the device (`dbi_oproj_residual_async`,
+model.cpp:773-774) against the oracle (`ok_oproj_residual`: tensor::matvec /
+matvec_f16 sequential sums, then x += proj).
+
+Tolerance: the device sums a row's products in a tree, the reference in
+sequence, so the two agree to the rounding of a dot product:
+    |a - b| <= 1e-5 + 1e-4 |b| + 2 * n * 2^-24 * sum_i |w_i x_i|
+(each order is within n * 2^-24 * sum|w_i x_i| of the exact value). On
+small-integer data every partial sum is exact, so there the results must be
+bit-identical.
+"""
+import numpy as np
+import pytest
+
+import pyoracle
+from dbinfer_amd.kv import W_F16, W_F32, DbiError, HipKV
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(2048, 2048), (3072, 3072), (3584, 3584), (4096, 4096),  # C1/C2, C3, C4, C5
+          (5, 8), (70, 520), (1, 4096), (300, 14336)]
+
+
+@pytest.fixture(scope="module")
+def torch():
+    return pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def kv():
+    h = HipKV(1, 64, 1, 64)
+    yield h
+    h.close()
+
+
+def run(torch, kv, w, a, x):
+    wt = torch.from_numpy(np.ascontiguousarray(w).view(np.uint16) if w.dtype == np.float16
+                          else np.ascontiguousarray(w)).cuda()
+    at = torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    xt = torch.from_numpy(np.array(x, np.float32)).cuda()
+    kv.set_stream(torch.cuda.current_stream().cuda_stream)
+    kv.oproj_residual_async(W_F16 if w.dtype == np.float16 else W_F32, wt.data_ptr(),
+                            at.data_ptr(), xt.data_ptr(), w.shape[0], w.shape[1])
+    torch.cuda.synchronize()
+    return xt.cpu().numpy()
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("dim,n_in", SHAPES)
+def test_integer_data_bit_exact(torch, kv, f16, dim, n_in):
+    rng = np.random.default_rng(dim + n_in)
+    w = rng.integers(-8, 9, (dim, n_in)).astype(np.float16 if f16 else np.float32)
+    a = rng.integers(-8, 9, n_in).astype(np.float32)
+    x = rng.integers(-100, 101, dim).astype(np.float32)
+    got = run(torch, kv, w, a, x)
+    want = pyoracle.oproj_residual(w, a, x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("dim,n_in", SHAPES)
+def test_random_data_within_dot_tolerance(torch, kv, f16, dim, n_in):
+    rng = np.random.default_rng(3 * dim + n_in)
+    w = (rng.standard_normal((dim, n_in)) * 0.05).astype(np.float16 if f16 else np.float32)
+    a = rng.standard_normal(n_in).astype(np.float32)
+    x = rng.standard_normal(dim).astype(np.float32)
+    got = run(torch, kv, w, a, x).astype(np.float64)
+    want = pyoracle.oproj_residual(w, a, x).astype(np.float64)
+    mag = np.abs(w.astype(np.float64)) @ np.abs(a.astype(np.float64))
+    bound = 1e-5 + 1e-4 * np.abs(want) + 2 * n_in * 2.0 ** -24 * mag
+    err = np.abs(got - want)
+    assert np.all(err <= bound), f"worst {float((err - bound).max()):.3e}"
+
+
+def test_oproj_errors(torch, kv):
+    w = torch.zeros(64, 64, device="cuda")
+    a = torch.zeros(64, device="cuda")
+    x = torch.zeros(64, device="cuda")
+    for args, msg in [((W_F32, w.data_ptr(), a.data_ptr(), x.data_ptr(), 64, 60), "multiple of 8"),
+                      ((W_F32, w.data_ptr(), a.data_ptr(), x.data_ptr(), 0, 64), "dim"),
+                      ((2, w.data_ptr(), a.data_ptr(), x.data_ptr(), 64, 64), "fp32 and f16"),
+                      ((W_F32, w.data_ptr() + 4, a.data_ptr(), x.data_ptr(), 8, 56), "aligned"),
+                      ((W_F32, 0, a.data_ptr(), x.data_ptr(), 64, 64), "null")]:
+        with pytest.raises(DbiError) as e:
+            kv.oproj_residual_async(*args)
+        assert msg in e.value.message
+
+
+def test_oproj_graph_replay(torch):
+    """Captured once; each replay reads the attention row written since and
+    accumulates into the residual, checked against the oracle every time."""
+    dim, n_in = 3072, 3072
+    rng = np.random.default_rng(11)
+    w = rng.integers(-4, 5, (dim, n_in)).astype(np.float32)
+    kv = HipKV(1, 64, 1, 64)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        wt = torch.from_numpy(w).cuda()
+        at = torch.zeros(n_in, device="cuda")
+        xt = torch.zeros(dim, device="cuda")
+        kv.set_stream(s.cuda_stream)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            kv.oproj_residual_async(W_F32, wt.data_ptr(), at.data_ptr(), xt.data_ptr(), dim, n_in)
+    torch.cuda.synchronize()
+    x = np.zeros(dim, np.float32)
+    for rep in range(4):
+        a = rng.integers(-4, 5, n_in).astype(np.float32)
+        at.copy_(torch.from_numpy(a))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        x = pyoracle.oproj_residual(w, a, x)
+        assert np.array_equal(xt.cpu().numpy(), x), f"replay {rep}"
+        _ = (at * 2).sum()
+    kv.close()
