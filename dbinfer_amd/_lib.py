@@ -24,7 +24,7 @@ DBI_ERR_FORMAT = 6
 
 DBI_KV_F32 = 0
 DBI_KV_INT8 = 1
-DBI_W_F32, DBI_W_F16 = 0, 1
+DBI_W_F32, DBI_W_F16, DBI_W_Q8_0 = 0, 1, 8
 
 EXPORT = {
     "k": 0, "v": 1, "k8": 2, "v8": 3, "k_scale": 4, "v_scale": 5,

@@ -1242,14 +1242,22 @@ dbi_status dbi_oproj_residual_async(dbi_kv* kv, uint32_t wtype, const void* w_de
   if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
   if (w_dev == nullptr || attn_dev == nullptr || x_dev == nullptr)
     return fail(DBI_ERR_INVALID, "null output-projection argument");
-  if (wtype != DBI_W_F32 && wtype != DBI_W_F16)
-    return fail(DBI_ERR_UNSUPPORTED, "output projection serves fp32 and f16 weights only");
-  if (dim == 0 || in == 0 || in % 8 != 0 || dim > (uint32_t(1) << 30) || in > (uint32_t(1) << 24))
+  if (wtype != DBI_W_F32 && wtype != DBI_W_F16 && wtype != DBI_W_Q8_0)
+    return fail(DBI_ERR_UNSUPPORTED,
+                "output projection serves fp32, f16 and Q8_0 weights only");
+  // Q8_0 keeps the quantized activation row in LDS (36 bytes per 32 floats)
+  const uint32_t mult = wtype == DBI_W_Q8_0 ? 32 : 8;
+  const uint32_t max_in = wtype == DBI_W_Q8_0 ? (uint32_t(1) << 16) : (uint32_t(1) << 24);
+  if (dim == 0 || in == 0 || in % mult != 0 || dim > (uint32_t(1) << 30) || in > max_in)
     return fail(DBI_ERR_INVALID,
-                "output projection needs dim in [1, 2^30] and in a positive multiple of 8 "
-                "(at most 2^24)");
-  if (((reinterpret_cast<uintptr_t>(w_dev) | reinterpret_cast<uintptr_t>(attn_dev)) & 15) != 0)
-    return fail(DBI_ERR_INVALID, "output projection needs 16-byte aligned weights and attn");
+                "output projection needs dim in [1, 2^30] and in a positive multiple of " +
+                    std::to_string(mult) + " (at most " + std::to_string(max_in) + ")");
+  const uintptr_t walign = wtype == DBI_W_Q8_0 ? 3 : 15;
+  if ((reinterpret_cast<uintptr_t>(w_dev) & walign) != 0 ||
+      (reinterpret_cast<uintptr_t>(attn_dev) & 15) != 0)
+    return fail(DBI_ERR_INVALID,
+                "output projection needs aligned weights (16 bytes; Q8_0: 4) and a 16-byte "
+                "aligned attn");
   dbi::OprojCall c{};
   c.w = w_dev;
   c.attn = attn_dev;
@@ -1257,6 +1265,7 @@ dbi_status dbi_oproj_residual_async(dbi_kv* kv, uint32_t wtype, const void* w_de
   c.dim = static_cast<int>(dim);
   c.in = static_cast<int>(in);
   c.f16 = wtype == DBI_W_F16;
+  c.q8 = wtype == DBI_W_Q8_0;
   HIP_TRY(dbi::launch_oproj(c, kv->stream), "output projection launch");
   return DBI_OK;
 }

@@ -234,13 +234,14 @@ struct VerifyCall {
 hipError_t launch_verify(const VerifyCall& c, hipStream_t st);
 
 // Output projection + residual add of decode_layer (oproj.hip):
-// x[o] += sum_i w[o][i] * attn[i], w fp32 or f16 [dim][in], in % 8 == 0.
+// x[o] += sum_i w[o][i] * attn[i], w fp32 or f16 [dim][in] (in % 8 == 0) or
+// Q8_0 blocks [dim][in/32] (in % 32 == 0).
 struct OprojCall {
   const void* w;
   const float* attn;
   float* x;
   int dim, in;
-  bool f16;
+  bool f16, q8;
 };
 hipError_t launch_oproj(const OprojCall& c, hipStream_t st);
 

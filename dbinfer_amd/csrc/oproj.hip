@@ -2,10 +2,12 @@
 // projection of the attention row and the residual add,
 //   proj = W_o · attn   (tensor::matvec_quant, [dim][in] row-major weights)
 //   x[o] += proj[o]
-// for unquantized weights: fp32 (tensor::matvec, matmul.cpp:36-43) and f16
+// for fp32 weights (tensor::matvec, matmul.cpp:36-43), f16 weights
 // (tensor::matvec_f16, matmul.cpp:45-54; every f16 weight converts exactly to
-// fp32 and is fused-multiply-added). The GGUF block formats (Q8_0, Q4_K, ...)
-// are not served.
+// fp32 and is fused-multiply-added) and Q8_0 blocks (matvec_q8_0_scalar,
+// matmul.cpp:56-75, with the activation row quantized to Q8_0 first,
+// quantize_row_q8_0, dequant.cpp:80-97). The other GGUF block formats are not
+// served.
 //
 // One wave per output row: each lane accumulates its share of the row with
 // fused multiply-adds, the wave sums the lanes, and lane 0 adds the result to
@@ -16,6 +18,7 @@
 // The reduction order differs from the reference's sequential sum, so results
 // agree to the rounding of a dot product, not bit for bit.
 #include "kv_internal.hpp"
+#include "quant.hpp"
 
 namespace dbi {
 namespace {
@@ -96,6 +99,97 @@ __global__ __launch_bounds__(kThreads) void oproj_kernel(OprojArgs a) {
   if (lane == 0) a.x[row] = a.x[row] + proj;
 }
 
+// Q8_0: a block is an f16 scale then 32 int8 codes (34 bytes). Each
+// workgroup first quantizes the activation row into LDS with
+// quantize_row_q8_0's arithmetic (amax over the block, d = amax / 127,
+// id = 1 / d, the stored scale f16(d), codes clamp(lround(x * id), +-127)),
+// one thread per block. Then each wave takes kQRows rows; lane l owns blocks
+// l, l + 64, ... of a row. Per block the integer dot product is exact
+// (v_dot4_i32_i8) and its term is (f16(dw) * f16(dx)) * sumi in fp32, the
+// reference's expression; the terms are then summed in a tree. A block's 34
+// bytes are read as the 9 aligned dwords around them (the weights start
+// 4-byte aligned, so the first of them never precedes the matrix; the last
+// can reach 2 bytes past it, inside the same aligned dword).
+constexpr int kQBlocks = 2;  // blocks per lane in flight
+constexpr int kQRows = 2;    // rows per wave
+constexpr int kQStride = 9;  // LDS dwords per activation block: 8 code dwords, the scale
+
+__device__ inline uint32_t pack4(int8_t a, int8_t b, int8_t c, int8_t d) {
+  return static_cast<uint32_t>(static_cast<uint8_t>(a)) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(b)) << 8) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(c)) << 16) |
+         (static_cast<uint32_t>(static_cast<uint8_t>(d)) << 24);
+}
+
+__global__ __launch_bounds__(kThreads) void oproj_q8_kernel(OprojArgs a) {
+  extern __shared__ uint32_t s_xq[];  // [nbk][kQStride]
+  const int nbk = a.in / 32;
+  for (int b = threadIdx.x; b < nbk; b += kThreads) {
+    const float4* xb = reinterpret_cast<const float4*>(a.attn + static_cast<size_t>(b) * 32);
+    float x[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 t = xb[i];
+      x[4 * i] = t.x;
+      x[4 * i + 1] = t.y;
+      x[4 * i + 2] = t.z;
+      x[4 * i + 3] = t.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = max_f(amax, fabsf(x[i]));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      s_xq[b * kQStride + i] = pack4(quant_code(x[4 * i], id), quant_code(x[4 * i + 1], id),
+                                     quant_code(x[4 * i + 2], id), quant_code(x[4 * i + 3], id));
+    s_xq[b * kQStride + 8] = __float_as_uint(static_cast<float>(static_cast<_Float16>(d)));
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) * kQRows;
+  for (int rr = 0; rr < kQRows; ++rr) {
+    const int row = row0 + rr;
+    if (row >= a.dim) break;  // wave-uniform
+    const uintptr_t wrow =
+        reinterpret_cast<uintptr_t>(a.w) + static_cast<size_t>(row) * nbk * 34;
+    float acc = 0.0f;
+    for (int b0 = lane; b0 < nbk; b0 += 64 * kQBlocks) {
+      uint32_t wd[kQBlocks][9];
+      uint32_t off[kQBlocks];
+#pragma unroll
+      for (int q = 0; q < kQBlocks; ++q) {
+        const int b = min(b0 + 64 * q, nbk - 1);
+        const uintptr_t p = wrow + static_cast<size_t>(b) * 34;
+        off[q] = static_cast<uint32_t>(p & 2);
+        const uint32_t* base = reinterpret_cast<const uint32_t*>(p & ~static_cast<uintptr_t>(3));
+#pragma unroll
+        for (int i = 0; i < 9; ++i) wd[q][i] = base[i];
+      }
+#pragma unroll
+      for (int q = 0; q < kQBlocks; ++q) {
+        const int b = min(b0 + 64 * q, nbk - 1);
+        const uint32_t* xq = s_xq + b * kQStride;
+        const bool hi = off[q] != 0;  // block starts 2 bytes into its first dword
+        const uint16_t dbits = static_cast<uint16_t>(hi ? wd[q][0] >> 16 : wd[q][0] & 0xffffu);
+        const float dw = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
+        int sumi = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t wc = hi ? wd[q][i + 1] : ((wd[q][i] >> 16) | (wd[q][i + 1] << 16));
+          sumi = __builtin_amdgcn_sdot4(static_cast<int>(wc), static_cast<int>(xq[i]), sumi,
+                                        false);
+        }
+        const float term = (dw * __uint_as_float(xq[8])) * static_cast<float>(sumi);
+        acc = b0 + 64 * q < nbk ? acc + term : acc;
+      }
+    }
+    const float proj = wave_sum64(acc);
+    if (lane == 0) a.x[row] = a.x[row] + proj;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_oproj(const OprojCall& c, hipStream_t st) {
@@ -106,7 +200,12 @@ hipError_t launch_oproj(const OprojCall& c, hipStream_t st) {
   a.dim = c.dim;
   a.in = c.in;
   const dim3 grid((c.dim + kRowsPerBlock - 1) / kRowsPerBlock);
-  if (c.f16)
+  if (c.q8) {
+    const int rows_per_block = kRowsPerBlock * kQRows;
+    const size_t lds = static_cast<size_t>(c.in / 32) * kQStride * sizeof(uint32_t);
+    hipLaunchKernelGGL(oproj_q8_kernel, dim3((c.dim + rows_per_block - 1) / rows_per_block),
+                       dim3(kThreads), lds, st, a);
+  } else if (c.f16)
     hipLaunchKernelGGL(oproj_kernel<true>, grid, dim3(kThreads), 0, st, a);
   else
     hipLaunchKernelGGL(oproj_kernel<false>, grid, dim3(kThreads), 0, st, a);

@@ -21,6 +21,7 @@ F32 = _lib.DBI_KV_F32
 INT8 = _lib.DBI_KV_INT8
 W_F32 = _lib.DBI_W_F32
 W_F16 = _lib.DBI_W_F16
+W_Q8_0 = _lib.DBI_W_Q8_0
 
 
 class DbiError(RuntimeError):

@@ -220,20 +220,24 @@ dbi_status dbi_kv_verify_commit(dbi_kv* kv, uint32_t pos, uint32_t k, uint32_t v
                                 const float* logits_dev, const int32_t* draft, int32_t* merged,
                                 uint32_t* accepted);
 
-/* Weight element types of dbi_oproj_residual_async (GgmlType F32 / F16). */
-enum { DBI_W_F32 = 0, DBI_W_F16 = 1 };
+/* Weight types of dbi_oproj_residual_async, numbered as GgmlType. */
+enum { DBI_W_F32 = 0, DBI_W_F16 = 1, DBI_W_Q8_0 = 8 };
 
 /* The step after attention in Model::decode_layer (model.cpp:773-774):
  * matvec_quant(attn_output, attn, proj, dim, nh*hd) then x[i] += proj[i],
- * for unquantized weights: fp32 (tensor::matvec, matmul.cpp:36-43) or f16
- * (tensor::matvec_f16, matmul.cpp:45-54). w_dev: device [dim][in] row-major;
- * attn_dev: device [in] (the attention row, in = n_heads*head_dim); x_dev:
- * device [dim], the residual stream, updated in place. in must be a multiple
- * of 8, and w_dev and attn_dev 16-byte aligned. The lanes of a row sum in a
- * tree, so proj agrees with the reference's sequential sum to the rounding
- * of a dot product, not bit for bit. GGUF block types (Q8_0, Q4_K, ...)
- * return DBI_ERR_UNSUPPORTED. Ordered on the handle's stream; allocates
- * nothing. */
+ * for fp32 weights (tensor::matvec, matmul.cpp:36-43), f16 weights
+ * (tensor::matvec_f16, matmul.cpp:45-54) and Q8_0 blocks
+ * (matvec_q8_0_scalar, matmul.cpp:56-75, after quantize_row_q8_0 of attn,
+ * dequant.cpp:80-97). w_dev: device [dim][in] row-major (Q8_0: [dim][in/32]
+ * blocks of an f16 scale and 32 int8 codes, 34 bytes); attn_dev: device [in]
+ * (the attention row, in = n_heads*head_dim); x_dev: device [dim], the
+ * residual stream, updated in place. in must be a multiple of 8, at most
+ * 2^24 (Q8_0: a multiple of 32, at most 65536);
+ * w_dev 16-byte aligned (Q8_0: 4), attn_dev 16-byte aligned. Each row's terms
+ * are summed in a tree, so proj agrees with the reference's sequential sum
+ * to the rounding of a dot product, not bit for bit (the Q8_0 codes and
+ * per-block integer sums are exact). Other GGUF block types return
+ * DBI_ERR_UNSUPPORTED. Ordered on the handle's stream; allocates nothing. */
 dbi_status dbi_oproj_residual_async(dbi_kv* kv, uint32_t wtype, const void* w_dev,
                                     const float* attn_dev, float* x_dev, uint32_t dim,
                                     uint32_t in);

@@ -791,17 +791,84 @@ float ok_f16_to_f32(uint16_t h) {
   return f;
 }
 
-void ok_oproj_residual(const void* w, int f16, const float* attn, float* x, size_t dim,
+/* sign, exponent rebiased 127 -> 15; mantissa rounded to 10 bits, to
+ * nearest with ties to even; below the normal range the implicit one is
+ * shifted into a subnormal, above it the result is infinity */
+uint16_t ok_f32_to_f16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  const uint32_t eb = (x >> 23) & 0xffu;
+  uint32_t m = x & 0x7fffffu;
+  if (eb == 0xffu) return (uint16_t)(sign | (m != 0 ? 0x7e00u : 0x7c00u));
+  const int32_t e = (int32_t)eb - 127 + 15;
+  if (e >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return sign;
+    m |= 0x800000u;
+    const int32_t sh = 14 - e;
+    uint32_t q = m >> sh;
+    const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (q & 1u))) ++q;
+    return (uint16_t)(sign | q);
+  }
+  uint32_t q = ((uint32_t)e << 10) | (m >> 13);
+  const uint32_t rem = m & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ++q;  /* a carry may reach inf */
+  return (uint16_t)(sign | q);
+}
+
+void ok_quantize_row_q8_0(const float* x, size_t n, uint8_t* out) {
+  for (size_t b = 0; b < n / 32; ++b) {
+    const float* xb = x + b * 32;
+    float amax = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+      const float a = fabsf(xb[i]);
+      if (amax < a) amax = a;  /* std::max(amax, a): a NaN never replaces */
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t db = ok_f32_to_f16(d);
+    uint8_t* blk = out + b * 34;
+    memcpy(blk, &db, 2);
+    for (int i = 0; i < 32; ++i) {
+      long q = lround(xb[i] * id);
+      if (q < -127) q = -127;
+      if (q > 127) q = 127;
+      blk[2 + i] = (uint8_t)(int8_t)q;
+    }
+  }
+}
+
+void ok_oproj_residual(const void* w, int wtype, const float* attn, float* x, size_t dim,
                        size_t in) {
+  uint8_t* xq = NULL;
+  if (wtype == 8) {
+    xq = (uint8_t*)malloc(in / 32 * 34);
+    ok_quantize_row_q8_0(attn, in, xq);
+  }
   for (size_t o = 0; o < dim; ++o) {
     float acc = 0.0f;
-    if (f16) {
+    if (wtype == 1) {
       const uint16_t* row = (const uint16_t*)w + o * in;
       for (size_t i = 0; i < in; ++i) acc = fmaf(ok_f16_to_f32(row[i]), attn[i], acc);
+    } else if (wtype == 8) {
+      const uint8_t* row = (const uint8_t*)w + o * (in / 32) * 34;
+      for (size_t b = 0; b < in / 32; ++b) {
+        const uint8_t* wb = row + b * 34;
+        const uint8_t* ab = xq + b * 34;
+        uint16_t dw, dx;
+        memcpy(&dw, wb, 2);
+        memcpy(&dx, ab, 2);
+        int32_t sumi = 0;
+        for (int i = 0; i < 32; ++i) sumi += (int32_t)(int8_t)wb[2 + i] * (int32_t)(int8_t)ab[2 + i];
+        acc += ok_f16_to_f32(dw) * ok_f16_to_f32(dx) * (float)sumi;
+      }
     } else {
       const float* row = (const float*)w + o * in;
       for (size_t i = 0; i < in; ++i) acc += row[i] * attn[i];
     }
     x[o] += acc;
   }
+  free(xq);
 }

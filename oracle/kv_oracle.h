@@ -34,6 +34,10 @@
  *   ok_argmax          sample_test argmax vectors, plus NaN / signed-zero /
  *                      infinity cases whose answer the strict-greater scan fixes
  *   ok_f16_to_f32      all 65536 half values against numpy's float16 -> float32
+ *   ok_f32_to_f16      numpy's float32 -> float16 (round to nearest even) on
+ *                      random, tie, subnormal, overflow and special values
+ *   ok_quantize_row_q8_0  closed-form properties: |code| <= 127, the block max
+ *                      maps to +-127, codes reconstruct x within d/2
  *   ok_oproj_residual  exact on small-integer data (every partial sum is an
  *                      integer below 2^24, so any order is exact); fp64 dot
  *                      product within the sequential-sum rounding bound
@@ -152,10 +156,17 @@ int32_t ok_argmax(const float* logits, size_t n);
 
 /* dequant.cpp:14: IEEE half to float (exact). */
 float ok_f16_to_f32(uint16_t h);
-/* model.cpp:773-774 with tensor::matvec (matmul.cpp:36-43, f16 = 0) or
- * tensor::matvec_f16 (matmul.cpp:45-54, f16 = 1): proj[o] = sequential
- * sum over i of w[o][i] * attn[i], then x[o] += proj[o]. */
-void ok_oproj_residual(const void* w, int f16, const float* attn, float* x, size_t dim,
+/* dequant.cpp:36: float to IEEE half, round to nearest even. */
+uint16_t ok_f32_to_f16(float f);
+/* dequant.cpp:80-97: one row of n floats (n % 32 == 0) to Q8_0 blocks of
+ * 34 bytes (f16 scale, 32 int8 codes). */
+void ok_quantize_row_q8_0(const float* x, size_t n, uint8_t* out);
+/* model.cpp:773-774 with matvec_quant's weight types (wtype numbered as
+ * GgmlType): 0 fp32 (tensor::matvec, matmul.cpp:36-43), 1 f16
+ * (tensor::matvec_f16, :45-54), 8 Q8_0 (attn quantized by
+ * ok_quantize_row_q8_0, then matvec_q8_0_scalar, :56-75): proj[o] is a
+ * sequential sum over the row, then x[o] += proj[o]. */
+void ok_oproj_residual(const void* w, int wtype, const float* attn, float* x, size_t dim,
                        size_t in);
 
 #ifdef __cplusplus

@@ -67,6 +67,8 @@ _SIGS = {
     "ok_argmax": (ctypes.c_int32, [_vp, _sz]),
     "ok_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
     "ok_oproj_residual": (None, [_vp, ctypes.c_int, _vp, _vp, _sz, _sz]),
+    "ok_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+    "ok_quantize_row_q8_0": (None, [_vp, _sz, _vp]),
 }
 
 _LIB = None
@@ -146,15 +148,26 @@ def f16_to_f32(h: int) -> float:
     return float(load().ok_f16_to_f32(h))
 
 
-def oproj_residual(w, attn, x):
-    """x + w @ attn with the reference's sequential sums; w fp32 or float16
-    [dim][in] (float16 passed as its bits)."""
-    f16 = np.asarray(w).dtype == np.float16
+def f32_to_f16(f: float) -> int:
+    return int(load().ok_f32_to_f16(f))
+
+
+def quantize_row_q8_0(x) -> np.ndarray:
+    xa = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(xa.size // 32 * 34, np.uint8)
+    load().ok_quantize_row_q8_0(xa.ctypes.data, xa.size, out.ctypes.data)
+    return out
+
+
+def oproj_residual(w, attn, x, q8_0: bool = False):
+    """x + w @ attn with the reference's sequential sums. w: float32 or
+    float16 [dim][in], or (q8_0) uint8 [dim][in/32*34] Q8_0 blocks."""
     wc = np.ascontiguousarray(w)
     a = np.ascontiguousarray(attn, dtype=np.float32)
     out = np.array(x, dtype=np.float32, copy=True)
-    dim, n_in = wc.shape
-    load().ok_oproj_residual(wc.ctypes.data, int(f16), a.ctypes.data, out.ctypes.data, dim, n_in)
+    wtype = 8 if q8_0 else (1 if wc.dtype == np.float16 else 0)
+    load().ok_oproj_residual(wc.ctypes.data, wtype, a.ctypes.data, out.ctypes.data, out.size,
+                             a.size)
     return out
 
 

@@ -7,13 +7,16 @@ sequence, so the two agree to the rounding of a dot product:
     |a - b| <= 1e-5 + 1e-4 |b| + 2 * n * 2^-24 * sum_i |w_i x_i|
 (each order is within n * 2^-24 * sum|w_i x_i| of the exact value). On
 small-integer data every partial sum is exact, so there the results must be
-bit-identical.
+bit-identical. Q8_0 (matvec_q8_0_scalar after quantize_row_q8_0): the same
+bound over the block terms, sum_b |dw_b * dx_b * sumi_b|; with unit scales
+and activation blocks that quantize to themselves, bit-identical.
 """
 import numpy as np
 import pytest
 
 import pyoracle
-from dbinfer_amd.kv import W_F16, W_F32, DbiError, HipKV
+from dbinfer_amd.kv import W_F16, W_F32, W_Q8_0, DbiError, HipKV
+from test_oracle_oproj import q8_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -78,7 +81,7 @@ def test_oproj_errors(torch, kv):
     x = torch.zeros(64, device="cuda")
     for args, msg in [((W_F32, w.data_ptr(), a.data_ptr(), x.data_ptr(), 64, 60), "multiple of 8"),
                       ((W_F32, w.data_ptr(), a.data_ptr(), x.data_ptr(), 0, 64), "dim"),
-                      ((2, w.data_ptr(), a.data_ptr(), x.data_ptr(), 64, 64), "fp32 and f16"),
+                      ((2, w.data_ptr(), a.data_ptr(), x.data_ptr(), 64, 64), "fp32, f16"),
                       ((W_F32, w.data_ptr() + 4, a.data_ptr(), x.data_ptr(), 8, 56), "aligned"),
                       ((W_F32, 0, a.data_ptr(), x.data_ptr(), 64, 64), "null")]:
         with pytest.raises(DbiError) as e:
@@ -114,3 +117,69 @@ def test_oproj_graph_replay(torch):
         assert np.array_equal(xt.cpu().numpy(), x), f"replay {rep}"
         _ = (at * 2).sum()
     kv.close()
+
+
+def run_q8(torch, kv, w, a, x, dim, n_in):
+    wt = torch.from_numpy(np.ascontiguousarray(w)).cuda()
+    at = torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    xt = torch.from_numpy(np.array(x, np.float32)).cuda()
+    kv.set_stream(torch.cuda.current_stream().cuda_stream)
+    kv.oproj_residual_async(W_Q8_0, wt.data_ptr(), at.data_ptr(), xt.data_ptr(), dim, n_in)
+    torch.cuda.synchronize()
+    return xt.cpu().numpy()
+
+
+Q8_SHAPES = [(2048, 2048), (3072, 3072), (3584, 3584), (4096, 4096), (5, 32), (70, 8192),
+             (3, 96)]
+
+
+@pytest.mark.parametrize("dim,n_in", Q8_SHAPES)
+def test_q8_0_integer_data_bit_exact(torch, kv, dim, n_in):
+    rng = np.random.default_rng(dim * 7 + n_in)
+    nb = n_in // 32
+    a = rng.integers(-127, 128, n_in)
+    a[::32] = -127  # every activation block's max is 127: d = 1, codes = values
+    codes = rng.integers(-8, 9, (dim, nb, 32))  # |sum| <= 256 * 32 * 8 * 127 < 2^24
+    w = q8_blocks(codes, np.ones((dim, nb), np.float32))
+    x = rng.integers(-100, 101, dim).astype(np.float32)
+    got = run_q8(torch, kv, w, a.astype(np.float32), x, dim, n_in)
+    want = pyoracle.oproj_residual(w, a.astype(np.float32), x, q8_0=True)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("dim,n_in", Q8_SHAPES)
+def test_q8_0_random_within_dot_tolerance(torch, kv, dim, n_in):
+    rng = np.random.default_rng(dim * 11 + n_in)
+    nb = n_in // 32
+    a = rng.standard_normal(n_in).astype(np.float32)
+    a[7] = 0.0
+    codes = rng.integers(-127, 128, (dim, nb, 32))
+    scales = np.exp(rng.uniform(-9, -4, (dim, nb))).astype(np.float32)
+    w = q8_blocks(codes, scales)
+    x = rng.standard_normal(dim).astype(np.float32)
+    got = run_q8(torch, kv, w, a, x, dim, n_in).astype(np.float64)
+    want = pyoracle.oproj_residual(w, a, x, q8_0=True).astype(np.float64)
+    aq = pyoracle.quantize_row_q8_0(a).reshape(nb, 34)
+    dx = aq[:, :2].copy().view(np.float16).astype(np.float64).ravel()
+    xc = aq[:, 2:].view(np.int8).astype(np.int64)
+    dw = scales.astype(np.float16).astype(np.float64)
+    sumi = np.einsum("dbi,bi->db", codes, xc)
+    mag = np.abs(dw * dx[None, :] * sumi).sum(axis=1)
+    bound = 1e-5 + 1e-4 * np.abs(want) + 2 * nb * 2.0 ** -24 * mag
+    err = np.abs(got - want)
+    assert np.all(err <= bound), f"worst {float((err - bound).max()):.3e}"
+
+
+def test_q8_0_errors(torch, kv):
+    w = torch.zeros(64 * 34, dtype=torch.uint8, device="cuda")
+    a = torch.zeros(64, device="cuda")
+    x = torch.zeros(64, device="cuda")
+    with pytest.raises(DbiError) as e:
+        kv.oproj_residual_async(W_Q8_0, w.data_ptr(), a.data_ptr(), x.data_ptr(), 2, 48)
+    assert "multiple of 32" in e.value.message
+    with pytest.raises(DbiError) as e:
+        kv.oproj_residual_async(W_Q8_0, w.data_ptr() + 2, a.data_ptr(), x.data_ptr(), 2, 32)
+    assert "aligned" in e.value.message
+    with pytest.raises(DbiError) as e:
+        kv.oproj_residual_async(2, w.data_ptr(), a.data_ptr(), x.data_ptr(), 2, 32)
+    assert "Q8_0 weights only" in e.value.message

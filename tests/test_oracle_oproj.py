@@ -52,3 +52,68 @@ def test_random_within_dot_bound(f16):
     got = pyoracle.oproj_residual(w, a, x).astype(np.float64)
     bound = n_in * 2.0 ** -24 * (np.abs(wf) @ np.abs(a)) + 2.0 ** -23 * np.abs(exact)
     assert np.all(np.abs(got - exact) <= bound)
+
+
+def test_f32_to_f16_against_numpy():
+    rng = np.random.default_rng(5)
+    mags = np.exp(rng.uniform(np.log(1e-9), np.log(7e4), 20000)).astype(np.float32)
+    vals = np.concatenate([mags, -mags])
+    # halfway cases between adjacent halves (ties to even), subnormal halves,
+    # the overflow edge and specials
+    h = np.arange(0, 0x7bff, 37, dtype=np.uint16).view(np.float16).astype(np.float64)
+    h_next = (np.arange(0, 0x7bff, 37, dtype=np.uint16) + 1).view(np.float16).astype(np.float64)
+    ties = ((h + h_next) / 2).astype(np.float32)
+    edge = np.array([65504, 65519, 65519.996, 65520, 65536, 1e9, 2.0 ** -24, 2.0 ** -25,
+                     2.0 ** -25 * 1.0000001, 2.0 ** -26, 0.0, -0.0, np.inf, -np.inf],
+                    np.float32)
+    allv = np.concatenate([vals, ties, edge]).astype(np.float32)
+    with np.errstate(over="ignore"):  # the overflow edge rounds to infinity
+        want = allv.astype(np.float16).view(np.uint16)
+    got = np.array([pyoracle.f32_to_f16(float(v)) for v in allv], np.uint16)
+    assert np.array_equal(got, want)
+    assert pyoracle.f32_to_f16(float("nan")) & 0x7c00 == 0x7c00
+
+
+def test_quantize_row_q8_0_properties():
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal(32 * 64).astype(np.float32) * np.repeat(
+        np.exp(rng.uniform(-8, 8, 64)), 32).astype(np.float32)
+    x[32 * 5: 32 * 6] = 0.0  # an all-zero block: scale 0, codes 0
+    q = pyoracle.quantize_row_q8_0(x).reshape(64, 34)
+    d_bits = q[:, :2].copy().view(np.uint16).ravel()
+    codes = q[:, 2:].view(np.int8).astype(np.int64)
+    xb = x.reshape(64, 32)
+    amax = np.abs(xb).max(axis=1)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    assert np.array_equal(d_bits, d.astype(np.float16).view(np.uint16))
+    assert np.all(np.abs(codes) <= 127)
+    nz = amax > 0
+    assert np.all(np.abs(codes[nz]).max(axis=1) == 127)
+    assert np.all(codes[~nz] == 0)
+    err = np.abs(xb[nz].astype(np.float64) - codes[nz] * d[nz, None].astype(np.float64))
+    assert np.all(err <= 0.5 * d[nz, None] * (1 + 1e-6))
+
+
+def q8_blocks(codes, scales):
+    """Q8_0 rows [dim][nb*34] from int8 codes [dim][nb][32] and f32 scales [dim][nb]."""
+    dim, nb, _ = codes.shape
+    blk = np.zeros((dim, nb, 34), np.uint8)
+    blk[:, :, :2] = scales.astype(np.float16).view(np.uint8).reshape(dim, nb, 2)
+    blk[:, :, 2:] = codes.astype(np.int8).view(np.uint8)
+    return blk.reshape(dim, nb * 34)
+
+
+@pytest.mark.parametrize("dim,n_in", [(1, 32), (9, 256), (40, 4096)])
+def test_q8_0_integer_data_exact(dim, n_in):
+    """Activation blocks whose max is 127 quantize to themselves (d = 1), and
+    weight scales of 1 make every term an exact integer."""
+    rng = np.random.default_rng(dim + n_in)
+    nb = n_in // 32
+    a = rng.integers(-127, 128, n_in)
+    a[::32] = 127
+    codes = rng.integers(-8, 9, (dim, nb, 32))  # |sum| <= 256 * 32 * 8 * 127 < 2^24
+    w = q8_blocks(codes, np.ones((dim, nb), np.float32))
+    x = rng.integers(-100, 101, dim).astype(np.float32)
+    want = (codes.reshape(dim, n_in) @ a + x.astype(np.int64)).astype(np.float32)
+    got = pyoracle.oproj_residual(w, a.astype(np.float32), x, q8_0=True)
+    assert np.array_equal(got, want)
