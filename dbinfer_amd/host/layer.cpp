@@ -117,6 +117,13 @@ std::int32_t speculative_commit(KVCache& kv, std::int32_t pos, std::size_t accep
   return next;
 }
 
+bool output_projection(KVCache& kv, std::uint32_t wtype, const void* w_dev,
+                       const float* attn_dev, float* x_dev, std::size_t dim, std::size_t in) {
+  return kv.check(dbi_oproj_residual_async(kv.handle(), wtype, w_dev, attn_dev, x_dev,
+                                           static_cast<std::uint32_t>(dim),
+                                           static_cast<std::uint32_t>(in)));
+}
+
 Result<std::size_t> speculative_verify(KVCache& kv, std::int32_t pos, std::size_t vocab,
                                        const float* logits_dev,
                                        std::span<const std::int32_t> draft,

@@ -89,6 +89,15 @@ bool chunk_attention_qkv(KVCache& kv, const Config& cfg, std::size_t layer, std:
                          std::size_t n, const float* q, const float* k, const float* v,
                          const AttnBias& bias, float* attn_out);
 
+// The step after attention in decode_layer (model.cpp:773-774): x += W_o ·
+// attn on the device (dbi_oproj_residual_async, on the cache handle's
+// stream). w_dev is W_o [dim][in] in device memory as fp32, f16 or Q8_0
+// blocks (wtype DBI_W_F32 / DBI_W_F16 / DBI_W_Q8_0); attn_dev [in] and x_dev
+// [dim] are device memory, x_dev updated in place. Returns false on an
+// argument or device error (kv.error() has the message).
+bool output_projection(KVCache& kv, std::uint32_t wtype, const void* w_dev,
+                       const float* attn_dev, float* x_dev, std::size_t dim, std::size_t in);
+
 // Model::save_kv_prefix / load_kv_prefix (model.hpp:292-299).
 Result<Unit> save_kv_prefix(const KVCache& kv, const std::string& path,
                             std::span<const std::int32_t> prefix_tokens);

@@ -448,6 +448,67 @@ void test_speculative_verify() {
   (void)hipFree(d);
 }
 
+void test_output_projection() {
+  // x += W_o · attn on the device for fp32, f16 and Q8_0 weights; integer
+  // data (Q8_0: unit block scales, activation blocks whose max is 127) keeps
+  // every partial sum exact, so the device equals the oracle bit for bit
+  const std::size_t dim = 64, in = 256, nb = in / 32;
+  KVCache kv(1, 16, 1, 64);
+  Lcg rng{0x0b0e};
+  auto small = [&](int range) {
+    return static_cast<float>(static_cast<int>((rng.next() + 1.0f) * 0.5f * (2 * range + 1)) - range);
+  };
+  std::vector<float> attn(in), x(dim), wf(dim * in);
+  for (std::size_t i = 0; i < in; ++i) attn[i] = i % 32 == 0 ? 127.0f : small(127);
+  for (auto& v : x) v = small(100);
+  for (auto& v : wf) v = small(8);
+  std::vector<std::uint16_t> wh(dim * in);
+  for (std::size_t i = 0; i < wf.size(); ++i) wh[i] = ok_f32_to_f16(wf[i]);
+  std::vector<std::uint8_t> wq(dim * nb * 34);
+  const std::uint16_t one = ok_f32_to_f16(1.0f);
+  for (std::size_t o = 0; o < dim; ++o)
+    for (std::size_t b = 0; b < nb; ++b) {
+      std::uint8_t* blk = wq.data() + (o * nb + b) * 34;
+      std::memcpy(blk, &one, 2);
+      for (int i = 0; i < 32; ++i)
+        blk[2 + i] = static_cast<std::uint8_t>(static_cast<std::int8_t>(wf[o * in + b * 32 + i]));
+    }
+  struct Case {
+    std::uint32_t wtype;
+    int oracle_type;
+    const void* host;
+    std::size_t bytes;
+    const char* name;
+  } cases[] = {{DBI_W_F32, 0, wf.data(), wf.size() * 4, "fp32"},
+               {DBI_W_F16, 1, wh.data(), wh.size() * 2, "f16"},
+               {DBI_W_Q8_0, 8, wq.data(), wq.size(), "Q8_0"}};
+  void *dw = nullptr, *da = nullptr, *dx = nullptr;
+  bool ok = hipMalloc(&dw, wf.size() * 4) == hipSuccess && hipMalloc(&da, in * 4) == hipSuccess &&
+            hipMalloc(&dx, dim * 4) == hipSuccess &&
+            hipMemcpy(da, attn.data(), in * 4, hipMemcpyHostToDevice) == hipSuccess;
+  check(ok, "output projection: device buffers");
+  for (const Case& c : cases) {
+    if (!ok) break;
+    std::vector<float> want = x, got(dim);
+    ok_oproj_residual(c.host, c.oracle_type, attn.data(), want.data(), dim, in);
+    const bool up = hipMemcpy(dw, c.host, c.bytes, hipMemcpyHostToDevice) == hipSuccess &&
+                    hipMemcpy(dx, x.data(), dim * 4, hipMemcpyHostToDevice) == hipSuccess;
+    const bool ran = up && dbinfer_amd::model::output_projection(
+                               kv, c.wtype, dw, static_cast<const float*>(da),
+                               static_cast<float*>(dx), dim, in);
+    const bool back = ran && dbi_kv_sync(kv.handle()) == DBI_OK &&
+                      hipMemcpy(got.data(), dx, dim * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    check(back && std::memcmp(got.data(), want.data(), dim * 4) == 0,
+          std::string("output projection ") + c.name + ": device == oracle (bitwise)");
+  }
+  check(!dbinfer_amd::model::output_projection(kv, 5, dw, static_cast<const float*>(da),
+                                               static_cast<float*>(dx), dim, in),
+        "output projection: an unserved weight type is refused");
+  (void)hipFree(dw);
+  (void)hipFree(da);
+  (void)hipFree(dx);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -472,6 +533,7 @@ int main(int argc, char** argv) {
     test_prefix_cache();
     test_speculative_rollback();
     test_speculative_verify();
+    test_output_projection();
   }
   std::printf("---\n%d checks failed\n", g_failures);
   return g_failures == 0 ? 0 : 1;
