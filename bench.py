@@ -230,7 +230,7 @@ def _profiled_traffic():
     return None
 
 
-# SURVEY 8(d) workloads, one decode step (and, where the config has them, the
+# The five benchmark configurations, one decode step (and, where the config has them, the
 # prefill chunk / verify round) per config; bench.py --configs
 CONFIGS = [
     # name, layers, nh, nkv, hd, dtype, n_sink, window, position decoded, chunk rows
@@ -596,7 +596,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--configs", action="store_true",
-                    help="instead of the bench line, one JSON line per SURVEY config (C1-C5)")
+                    help="instead of the bench line, one JSON line per benchmark config (C1-C5)")
     ap.add_argument("--config-steps", type=int, default=30)
     ap.add_argument("--configs-cpu", action="store_true",
                     help="with --configs: also time the CPU oracle on one layer of each config")
@@ -611,7 +611,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards by kv head with no exchange, see DESIGN.md)", file=sys.stderr)
+              "(the path shards by kv head with no exchange)", file=sys.stderr)
         sys.exit(2)
 
     import torch
