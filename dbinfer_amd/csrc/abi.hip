@@ -1245,9 +1245,10 @@ dbi_status dbi_oproj_residual_async(dbi_kv* kv, uint32_t wtype, const void* w_de
   if (wtype != DBI_W_F32 && wtype != DBI_W_F16 && wtype != DBI_W_Q8_0)
     return fail(DBI_ERR_UNSUPPORTED,
                 "output projection serves fp32, f16 and Q8_0 weights only");
-  // Q8_0 keeps the quantized activation row in LDS (36 bytes per 32 floats)
+  // Q8_0 keeps the quantized activation row in LDS (36 bytes per 32 floats):
+  // at most 36 KB, within a launch's default dynamic LDS
   const uint32_t mult = wtype == DBI_W_Q8_0 ? 32 : 8;
-  const uint32_t max_in = wtype == DBI_W_Q8_0 ? (uint32_t(1) << 16) : (uint32_t(1) << 24);
+  const uint32_t max_in = wtype == DBI_W_Q8_0 ? (uint32_t(1) << 15) : (uint32_t(1) << 24);
   if (dim == 0 || in == 0 || in % mult != 0 || dim > (uint32_t(1) << 30) || in > max_in)
     return fail(DBI_ERR_INVALID,
                 "output projection needs dim in [1, 2^30] and in a positive multiple of " +

@@ -232,7 +232,7 @@ enum { DBI_W_F32 = 0, DBI_W_F16 = 1, DBI_W_Q8_0 = 8 };
  * blocks of an f16 scale and 32 int8 codes, 34 bytes); attn_dev: device [in]
  * (the attention row, in = n_heads*head_dim); x_dev: device [dim], the
  * residual stream, updated in place. in must be a multiple of 8, at most
- * 2^24 (Q8_0: a multiple of 32, at most 65536);
+ * 2^24 (Q8_0: a multiple of 32, at most 32768);
  * w_dev 16-byte aligned (Q8_0: 4), attn_dev 16-byte aligned. Each row's terms
  * are summed in a tree, so proj agrees with the reference's sequential sum
  * to the rounding of a dot product, not bit for bit (the Q8_0 codes and

@@ -147,7 +147,7 @@ def test_q8_0_integer_data_bit_exact(torch, kv, dim, n_in):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("dim,n_in", Q8_SHAPES)
+@pytest.mark.parametrize("dim,n_in", Q8_SHAPES + [(2, 32768)])  # the largest LDS stage
 def test_q8_0_random_within_dot_tolerance(torch, kv, dim, n_in):
     rng = np.random.default_rng(dim * 11 + n_in)
     nb = n_in // 32
@@ -183,3 +183,6 @@ def test_q8_0_errors(torch, kv):
     with pytest.raises(DbiError) as e:
         kv.oproj_residual_async(2, w.data_ptr(), a.data_ptr(), x.data_ptr(), 2, 32)
     assert "Q8_0 weights only" in e.value.message
+    with pytest.raises(DbiError) as e:  # the quantized row must fit the LDS stage
+        kv.oproj_residual_async(W_Q8_0, w.data_ptr(), a.data_ptr(), x.data_ptr(), 1, 32800)
+    assert "at most 32768" in e.value.message
