@@ -118,8 +118,22 @@ dbi_status need_pinned(dbi_kv* kv) {
   return DBI_OK;
 }
 
+// Workspace growth syncs, frees and allocates, none of which a graph
+// capture may record: under capture a call that needs more than the handle
+// holds fails, and the caller makes that call once before capturing.
+dbi_status refuse_capture(dbi_kv* kv, const char* what) {
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(kv->stream, &cap), "capture status");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(DBI_ERR_INVALID, std::string(what) +
+                                     " would grow under graph capture; make the same call once "
+                                     "before capturing");
+  return DBI_OK;
+}
+
 dbi_status ensure_part(dbi_kv* kv, size_t part) {
   if (part > kv->ws.part_floats) {
+    if (dbi_status st = refuse_capture(kv, "the attention workspace")) return st;
     HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
     if (kv->ws.part) (void)hipFree(kv->ws.part);
     kv->ws.part = nullptr;
@@ -132,19 +146,11 @@ dbi_status ensure_part(dbi_kv* kv, size_t part) {
 }
 
 dbi_status ensure_workspace(dbi_kv* kv, const dbi::AttnCall& c) {
-  const size_t part = dbi::attention_workspace_need(kv->geom, c);
-  if (part > kv->ws.part_floats) {
-    HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
-    if (kv->ws.part) (void)hipFree(kv->ws.part);
-    kv->ws.part = nullptr;
-    kv->ws.part_floats = 0;
-    if (hipMalloc(reinterpret_cast<void**>(&kv->ws.part), part * sizeof(float)) != hipSuccess)
-      return fail(DBI_ERR_NOMEM, "attention workspace allocation failed");
-    kv->ws.part_floats = part;
-  }
+  if (dbi_status st = ensure_part(kv, dbi::attention_workspace_need(kv->geom, c))) return st;
   // the kernels leave the counters at zero; a fresh array starts there
   const size_t cnt = dbi::attention_counters_need(kv->geom, c);
   if (cnt > kv->ws.counters_n) {
+    if (dbi_status st = refuse_capture(kv, "the split counters")) return st;
     HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
     if (kv->ws.counters) (void)hipFree(kv->ws.counters);
     kv->ws.counters = nullptr;
@@ -333,6 +339,7 @@ dbi_status ensure_rope_table(dbi_kv* kv) {
 
 dbi_status ensure_prod(dbi_kv* kv, size_t floats) {
   if (floats <= kv->ws.prod_floats) return DBI_OK;
+  if (dbi_status st = refuse_capture(kv, "the producer workspace")) return st;
   HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
   if (kv->ws.prod) (void)hipFree(kv->ws.prod);
   kv->ws.prod = nullptr;
@@ -678,6 +685,23 @@ dbi_status dbi_attn_decode_async(dbi_kv* kv, uint32_t layer, uint32_t pos, uint3
   if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
   if (dbi_status st = check_attend(kv, layer, n_heads, q_dev, out_dev)) return st;
   return decode_impl(kv, layer, pos, n_heads, scale, q_dev, out_dev);
+}
+
+dbi_status dbi_attn_splits(const dbi_kv* kv, uint32_t pos0, uint32_t rows, uint32_t n_heads,
+                           uint32_t* n_split) {
+  if (kv == nullptr || n_split == nullptr) return fail(DBI_ERR_INVALID, "null argument");
+  if (rows == 0 || (kv->geom.ring && rows != 1))
+    return fail(DBI_ERR_INVALID, "rows must be 1 (decode) or, on a dense cache, a chunk's rows");
+  if (n_heads == 0 || n_heads % kv->cfg.n_kv_heads != 0 ||
+      !dbi::attention_supported(kv->geom, static_cast<int>(n_heads)))
+    return fail(DBI_ERR_UNSUPPORTED, "no attention kernel for this shape");
+  if (dbi_status st = check_rows(kv, pos0, rows)) return st;
+  dbi::AttnCall c = chunk_call(0, pos0, rows, n_heads, 1.0f, nullptr, nullptr);
+  if (kv->geom.ring) c.ring = ring_view(kv, pos0 + 1);
+  const bool pre = dbi::prefill_supported(kv->geom, c.n_heads, c.rows);
+  *n_split = static_cast<uint32_t>(pre ? dbi::prefill_split_count(kv->geom, c)
+                                       : dbi::attention_split_count(kv->geom, c));
+  return DBI_OK;
 }
 
 dbi_status dbi_kv_decode(dbi_kv* kv, uint32_t layer, uint32_t pos, const float* k,

@@ -1482,6 +1482,8 @@ bool attention_supported(const KvGeom& g, int n_heads) {
   return pick_kernel(g.hd, kind_of(g), n_heads / g.nkv) != nullptr;
 }
 
+int attention_split_count(const KvGeom& g, const AttnCall& c) { return plan(g, c).nsplit; }
+
 size_t attention_counters_need(const KvGeom& g, const AttnCall& c) {
   return plan(g, c).merge ? static_cast<size_t>(c.rows) * g.nkv * kCounterStride : 0;
 }

@@ -179,6 +179,9 @@ hipError_t launch_prefill(const KvGeom& g, const KvStore& s, Workspace& ws, cons
                           hipStream_t st);
 size_t attention_counters_need(const KvGeom& g, const AttnCall& c);
 bool attention_supported(const KvGeom& g, int n_heads);
+// Key splits (partial records per query row and kv head) of a call.
+int attention_split_count(const KvGeom& g, const AttnCall& c);
+int prefill_split_count(const KvGeom& g, const AttnCall& c);
 
 // One producer launch (produce.hip): rows [pos0, pos0 + rows) of raw q/k/v
 // projections (device, row-major [rows][heads*hd]) plus optional biases

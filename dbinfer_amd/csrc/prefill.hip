@@ -367,6 +367,8 @@ int prefill_splits(const KvGeom& g, const AttnCall& c) {
 
 }  // namespace
 
+int prefill_split_count(const KvGeom& g, const AttnCall& c) { return prefill_splits(g, c); }
+
 bool prefill_supported(const KvGeom& g, int n_heads, int rows) {
   if (g.int8 || g.ring || !g.tiled || rows < kPrefillMinRows || n_heads % g.nkv != 0)
     return false;

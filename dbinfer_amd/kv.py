@@ -156,6 +156,13 @@ class HipKV:
         _check(self._lib, self._lib.dbi_attn_decode_async(self._h, layer, pos, n_heads, scale,
                                                           q_dev, out_dev))
 
+    def splits(self, pos0: int, rows: int, n_heads: int) -> int:
+        """Key splits (partial records per row and kv head) of an attention call."""
+        out = ctypes.c_uint32()
+        _check(self._lib, self._lib.dbi_attn_splits(self._h, pos0, rows, n_heads,
+                                                    ctypes.byref(out)))
+        return int(out.value)
+
     def decode(self, layer: int, pos: int, k, v, q, n_heads: int, scale: float) -> np.ndarray:
         """Fused append of (k, v) at pos + attention of q at pos (one launch)."""
         k, v, q = _f32(k), _f32(v), _f32(q)

@@ -129,6 +129,14 @@ dbi_status dbi_attn_decode(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_
 dbi_status dbi_attn_decode_async(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_heads,
                                  float scale, const float* q_dev, float* out_dev);
 
+/* Key splits of an attention call: how many partial records per query row
+ * and kv head a decode (rows = 1, at pos0) or chunk call (rows rows from
+ * pos0) over the current kernels writes and merges; 1 means the call writes
+ * its output directly. A query for tests and tuning, with no counterpart in
+ * the reference (its attention is one loop per head, model.cpp:575-600). */
+dbi_status dbi_attn_splits(const dbi_kv* kv, uint32_t pos0, uint32_t rows, uint32_t n_heads,
+                           uint32_t* n_split);
+
 /* One decode step of a layer, fused: KVCache::append of position pos then
  * the single-query attention at pos, exactly as dbi_kv_append followed by
  * dbi_attn_decode (the attention half of Model::decode_layer,
