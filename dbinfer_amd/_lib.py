@@ -71,6 +71,7 @@ SIGNATURES = {
     "dbi_attn_splits": (_st, [_vp, _u32, _u32, _u32, ctypes.POINTER(_u32)]),
     "dbi_kv_decode": (_st, [_vp, _u32, _u32, _vp, _vp, _u32, _f32, _vp, _vp]),
     "dbi_kv_decode_async": (_st, [_vp, _u32, _u32, _vp, _vp, _u32, _f32, _vp, _vp]),
+    "dbi_kv_decode_noalloc_async": (_st, [_vp, _u32, _u32, _vp, _vp, _u32, _f32, _vp, _vp]),
     "dbi_attn_chunk": (_st, [_vp, _u32, _u32, _u32, _u32, _f32, _vp, _vp]),
     "dbi_attn_chunk_async": (_st, [_vp, _u32, _u32, _u32, _u32, _f32, _vp, _vp]),
     "dbi_kv_decode_qkv": (_st, [_vp, _u32, _u32, _u32, _f32] + [_vp] * 7),

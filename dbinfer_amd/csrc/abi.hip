@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -462,6 +463,61 @@ dbi_status qkv_host(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n, uint3
   return DBI_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free decode step (dbi_kv_decode_noalloc_async): its split records
+// and arrival counters live in one file-scope device array. Each GPU holds
+// its own copy until the process ends; host code reaches it only through
+// the address hipGetSymbolAddress returns on that device, taken once per
+// device when the first handle on it is created (the array's name is a host
+// stand-in, not a device address). Every call on a GPU shares the array:
+// calls that overlap on one GPU race.
+constexpr size_t kScratchRecordBytes = size_t(2) << 20;    // split records
+constexpr size_t kScratchCounterBytes = size_t(64) << 10;  // arrival counters
+constexpr size_t kScratchBytes = kScratchRecordBytes + kScratchCounterBytes;
+constexpr int kScratchDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_ptr[kScratchDevices] = {};
+std::string g_scratch_error[kScratchDevices];
+
+// With `device` current: the array's device address, and its counters
+// cleared (each launch leaves them at zero again). Synchronous; called from
+// dbi_kv_create, never under graph capture.
+void scratch_setup(int device) {
+  if (device < 0 || device >= kScratchDevices) return;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device] != nullptr) return;
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e == hipSuccess && p == nullptr) e = hipErrorInvalidSymbol;
+  if (e == hipSuccess)
+    e = hipMemset(static_cast<unsigned char*>(p) + kScratchRecordBytes, 0, kScratchCounterBytes);
+  if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+  if (e != hipSuccess) {
+    g_scratch_error[device] = std::string("scratch set-up failed: ") + hipGetErrorString(e);
+    return;
+  }
+  g_scratch_ptr[device] = static_cast<unsigned char*>(p);
+}
+
+unsigned char* scratch_ptr(int device, std::string* why) {
+  if (device < 0 || device >= kScratchDevices) {
+    *why = "device index beyond the scratch table";
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device] == nullptr)
+    *why = g_scratch_error[device].empty() ? "scratch not set up on this device"
+                                           : g_scratch_error[device];
+  return g_scratch_ptr[device];
+}
+
 }  // namespace
 
 extern "C" {
@@ -545,6 +601,7 @@ dbi_status dbi_kv_create(const dbi_kv_config* cfg, dbi_kv** out) {
     if (e == hipSuccess)
       e = hipMemcpy(s.rope_cs, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice);
   }
+  if (e == hipSuccess) scratch_setup(kv->device);
   // the fills above run on the null stream, which a non-blocking stream does
   // not wait for: finish them before any work can reach the arrays
   if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
@@ -733,6 +790,44 @@ dbi_status dbi_kv_decode_async(dbi_kv* kv, uint32_t layer, uint32_t pos, const f
   if (dbi_status st = append_check(kv, layer, pos, 1, k_dev, v_dev)) return st;
   if (dbi_status st = check_attend(kv, layer, n_heads, q_dev, out_dev)) return st;
   return decode_impl(kv, layer, pos, n_heads, scale, q_dev, out_dev, k_dev, v_dev);
+}
+
+dbi_status dbi_kv_decode_noalloc_async(dbi_kv* kv, uint32_t layer, uint32_t pos,
+                                       const float* k_dev, const float* v_dev, uint32_t n_heads,
+                                       float scale, const float* q_dev, float* out_dev) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  if (dbi_status st = append_check(kv, layer, pos, 1, k_dev, v_dev)) return st;
+  if (dbi_status st = check_attend(kv, layer, n_heads, q_dev, out_dev)) return st;
+  if (dbi_status st = check_rows(kv, pos, 1)) return st;
+  std::string why;
+  unsigned char* base = scratch_ptr(kv->device, &why);
+  if (base == nullptr) return fail(DBI_ERR_DEVICE, why);
+  // size checks come before any launch, so a refusal leaves the cache as it was
+  const dbi::AttnCall sized =
+      decode_call(kv, layer, pos, n_heads, scale, q_dev, out_dev, nullptr, nullptr);
+  const size_t rec = dbi::attention_workspace_need(kv->geom, sized) * sizeof(float);
+  const size_t cnt = dbi::attention_counters_need(kv->geom, sized) * sizeof(unsigned);
+  if (rec > kScratchRecordBytes || cnt > kScratchCounterBytes)
+    return fail(DBI_ERR_UNSUPPORTED,
+                "allocation-free decode: this call needs " + std::to_string(rec) +
+                    " bytes of split records and " + std::to_string(cnt) +
+                    " bytes of counters; the scratch holds " +
+                    std::to_string(kScratchRecordBytes) + " and " +
+                    std::to_string(kScratchCounterBytes));
+  dbi::Workspace ws{};
+  ws.part = reinterpret_cast<float*>(base);
+  ws.part_floats = kScratchRecordBytes / sizeof(float);
+  ws.counters = reinterpret_cast<unsigned*>(base + kScratchRecordBytes);
+  ws.counters_n = kScratchCounterBytes / sizeof(unsigned);
+  // rows that are not 16-byte aligned go through the append kernel first
+  if (((reinterpret_cast<uintptr_t>(k_dev) | reinterpret_cast<uintptr_t>(v_dev)) & 15) != 0) {
+    if (dbi_status st = append_impl(kv, layer, pos, 1, k_dev, v_dev)) return st;
+    k_dev = v_dev = nullptr;
+  }
+  const dbi::AttnCall c = decode_call(kv, layer, pos, n_heads, scale, q_dev, out_dev, k_dev, v_dev);
+  HIP_TRY(dbi::launch_attention(kv->geom, kv->store, ws, c, kv->stream), "attention launch");
+  kv->n_seen = pos + 1;
+  return DBI_OK;
 }
 
 dbi_status dbi_attn_chunk(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,

@@ -178,6 +178,12 @@ class HipKV:
         _check(self._lib, self._lib.dbi_kv_decode_async(self._h, layer, pos, k_dev, v_dev, n_heads,
                                                         scale, q_dev, out_dev))
 
+    def decode_noalloc_async(self, layer: int, pos: int, k_dev: int, v_dev: int, n_heads: int,
+                             scale: float, q_dev: int, out_dev: int) -> None:
+        """decode_async through the allocation-free entry point (static scratch)."""
+        _check(self._lib, self._lib.dbi_kv_decode_noalloc_async(
+            self._h, layer, pos, k_dev, v_dev, n_heads, scale, q_dev, out_dev))
+
     def attend_chunk(self, layer: int, pos0: int, q, n_heads: int, scale: float) -> np.ndarray:
         q = _f32(q)
         n = q.size // (n_heads * self.head_dim)

@@ -150,6 +150,19 @@ dbi_status dbi_kv_decode_async(dbi_kv* kv, uint32_t layer, uint32_t pos, const f
                                const float* v_dev, uint32_t n_heads, float scale,
                                const float* q_dev, float* out_dev);
 
+/* dbi_kv_decode_async for callers that cannot allocate: no counterpart in
+ * the reference, for code under HIP graph capture, tight serving loops and
+ * harnesses that forbid hipMalloc. Same arguments, kernels and results; it
+ * calls no allocating routine, ever. Its split records and arrival counters
+ * live in a static per-GPU scratch array (2 MiB of records, 64 KiB of
+ * counters), set up when the first handle on that GPU is created; a call
+ * whose split plan needs more fails with DBI_ERR_UNSUPPORTED and leaves the
+ * cache as it was. Every call on one GPU shares that array: calls that
+ * overlap on one GPU (other handles, other streams) race. */
+dbi_status dbi_kv_decode_noalloc_async(dbi_kv* kv, uint32_t layer, uint32_t pos,
+                                       const float* k_dev, const float* v_dev, uint32_t n_heads,
+                                       float scale, const float* q_dev, float* out_dev);
+
 /* Causal chunk attention of decode_layer_chunk (model.cpp:956-981): row c of
  * q [n][n_heads][head_dim] attends [0, pos0 + c] and writes row c of out.
  * Every row must have been appended first (model.cpp:933-954). Dense fp32
