@@ -570,8 +570,8 @@ dbi_status dbi_kv_create(const dbi_kv_config* cfg, dbi_kv** out) {
     A(&s.k, cells);
     A(&s.v, cells);
   } else {
-    A(&s.k8, cells, 0x80);  // biased code of 0, like the reference's zeroed storage
-    A(&s.v8, cells, 0x80);
+    A(&s.k8, cells);  // code 0, like the reference's zeroed storage
+    A(&s.v8, cells);
     A(&s.v_scale, scales);
     if (g.ring) {
       A(&s.k_scale, scales);
@@ -1180,7 +1180,7 @@ dbi_status dbi_kv_export(dbi_kv* kv, uint32_t what, uint32_t layer, void* dst, s
   const dbi::KvGeom& g = kv->geom;
   const dbi::KvStore& s = kv->store;
   // head-major device arrays -> reference [rows][nkv][inner]; K/V codes and
-  // values are read back through the granule layout, int8 codes un-biased
+  // values are read back through the granule layout
   enum Map { kRows, kKeys, kValues, kFlat };
   const void* src = nullptr;
   size_t rows = 0, inner = 0, esz = 4, dev_rows = 0;
@@ -1235,7 +1235,7 @@ dbi_status dbi_kv_export(dbi_kv* kv, uint32_t what, uint32_t layer, void* dst, s
         const size_t at = kh * he + (map == kKeys ? dbi::k_off(g, r, d) : dbi::v_off(g, r, d));
         const size_t to = (size_t(r) * g.nkv + kh) * g.hd + d;
         if (esz == 1)
-          out[to] = static_cast<unsigned char>(tmp[at] ^ 0x80u);
+          out[to] = tmp[at];
         else
           std::memcpy(out + to * 4, tmp.data() + at * 4, 4);
       }

@@ -3,8 +3,7 @@
 // (model.cpp:357-404).
 //
 // The int8 arithmetic (quant.hpp) is bit-exact with the reference; codes are
-// stored biased, as the byte code + 128, in the granule layout of
-// kv_internal.hpp.
+// stored as signed bytes in the granule layout of kv_internal.hpp.
 #include "kv_internal.hpp"
 #include "quant.hpp"
 
@@ -71,8 +70,8 @@ __global__ __launch_bounds__(kThreads) void append_i8_ring_kernel(KvGeom g, KvSt
   const size_t head = static_cast<size_t>(layer) * g.nkv + kh;
   const size_t row = head * g.capg + slot;
   if (in) {
-    s.k8[head * head_elems(g) + k_off(g, slot, i)] = biased(kc);
-    s.v8[head * head_elems(g) + v_off(g, slot, i)] = biased(vc);
+    s.k8[head * head_elems(g) + k_off(g, slot, i)] = kc;
+    s.v8[head * head_elems(g) + v_off(g, slot, i)] = vc;
   }
   if (t == 0) {
     s.k_scale[row * g.nb + b] = ks;
@@ -117,7 +116,7 @@ __global__ __launch_bounds__(kThreads) void append_i8_kgroup_kernel(KvGeom g, Kv
 #pragma unroll
   for (int w = 0; w < kKGroup; ++w)
     if (w <= within && first + w >= g.n_sink)
-      s.k8[head * head_elems(g) + k_off(g, first + w, i)] = biased(quant_code(x[w], inv));
+      s.k8[head * head_elems(g) + k_off(g, first + w, i)] = quant_code(x[w], inv);
 }
 
 // The staging rows after the batch: k_raw[w] holds the batch's last row p
@@ -166,7 +165,7 @@ __global__ __launch_bounds__(kThreads) void append_i8_dense_v_kernel(KvGeom g, K
   }
   float vs;
   const int8_t vc = quant_lane(vx, &vs);
-  if (in) s.v8[head * head_elems(g) + v_off(g, p, i)] = biased(vc);
+  if (in) s.v8[head * head_elems(g) + v_off(g, p, i)] = vc;
   if (t == 0) s.v_scale[(head * g.capg + p) * g.nb + b] = vs;
 }
 
@@ -191,17 +190,10 @@ __global__ __launch_bounds__(kThreads) void prefix_pack_kernel(KvGeom g, const T
     const size_t st = (l * g.nkv + kh) * head_elems(g) +
                       (is_k ? k_off(g, static_cast<int>(p), static_cast<int>(i))
                             : v_off(g, static_cast<int>(p), static_cast<int>(i)));
-    if constexpr (sizeof(T) == 1) {  // int8 codes: stored biased (code + 128), filed signed
-      if (unpack)
-        const_cast<T*>(store)[st] = static_cast<T>(dst[idx] ^ 0x80);
-      else
-        dst[idx] = static_cast<T>(store[st] ^ 0x80);
-    } else {
-      if (unpack)
-        const_cast<T*>(store)[st] = dst[idx];
-      else
-        dst[idx] = store[st];
-    }
+    if (unpack)
+      const_cast<T*>(store)[st] = dst[idx];
+    else
+      dst[idx] = store[st];
   }
 }
 

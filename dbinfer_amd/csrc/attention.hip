@@ -32,10 +32,9 @@
 //    writeback on this multi-XCD part) and no memset between launches.
 //  - int8 dense: a 32-position chunk is exactly one K group, so the
 //    per-channel K scale folds into q once per chunk (the reference's
-//    (q_i * ks_i) * k8_i); codes are stored biased (+128) and converted with
-//    one v_cvt_f32_ubyteN each, the bias removed through -128 * sum(q*ks) (K)
-//    and -128 * sum(w*vs) (V). The fp32 sinks (pos < n_sink) are attended
-//    in the merge as further entries.
+//    (q_i * ks_i) * k8_i); codes are signed bytes, converted with one
+//    sign-extending SDWA v_cvt_f32_i32 each. The fp32 sinks (pos < n_sink)
+//    are attended in the merge as further entries.
 //  - Fused decode step (dbi_kv_decode): the append of the new row runs
 //    inside the launch (FusedAppend), staged in LDS for the wave that
 //    attends its chunk.
@@ -207,12 +206,12 @@ __device__ __forceinline__ float4 stream_b128(rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kNT));
 }
 
-// 8 biased int8 codes -> code + 128 as float (one v_cvt_f32_ubyteN each)
+// 8 int8 codes -> float (one sign-extending SDWA v_cvt_f32_i32 each)
 __device__ __forceinline__ void cvt8(const uint2 w, float* f) {
 #pragma unroll
-  for (int b = 0; b < 4; ++b) f[b] = static_cast<float>((w.x >> (8 * b)) & 0xFFu);
+  for (int b = 0; b < 4; ++b) f[b] = static_cast<float>(static_cast<int8_t>(w.x >> (8 * b)));
 #pragma unroll
-  for (int b = 0; b < 4; ++b) f[4 + b] = static_cast<float>((w.y >> (8 * b)) & 0xFFu);
+  for (int b = 0; b < 4; ++b) f[4 + b] = static_cast<float>(static_cast<int8_t>(w.y >> (8 * b)));
 }
 
 template <int HD, int G, int KIND>
@@ -498,8 +497,8 @@ struct AppStage {
   float vs[4];                       // int8: the new row's V block scales
   float krow[128];                   // fp32: the new K row
   float vrow[128];                   // fp32: the new V row
-  uint32_t k8row[32];                // ring int8: the new K codes (biased bytes)
-  uint32_t v8row[32];                // int8: the new V codes (biased bytes)
+  uint32_t k8row[32];                // ring int8: the new K codes
+  uint32_t v8row[32];                // int8: the new V codes
 };
 
 // Dense int8: the requantized 32-token group of the fused step, shared by
@@ -675,7 +674,7 @@ struct FusedAppend {
     const int d = wave * CPW + c;
 #pragma unroll
     for (int i = 0; i < RPL; ++i)
-      kc[k_off_tiled(HD, true, rb * RPL + i, d)] = static_cast<uint8_t>(biased(quant_code(x[i], inv)));
+      kc[k_off_tiled(HD, true, rb * RPL + i, d)] = static_cast<uint8_t>(quant_code(x[i], inv));
     if (lane < CPW) kg.ks[d] = sc;
     // publish (the release orders the stage writes before the count)
     if (lane == 0) __hip_atomic_fetch_add(&kg.done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -697,8 +696,8 @@ struct FusedAppend {
   }
   __device__ __forceinline__ static uint32_t codes2(float2 x, float s) {
     const float inv = s > 0.0f ? 1.0f / s : 0.0f;
-    const uint32_t a = static_cast<uint8_t>(biased(quant_code(x.x, inv)));
-    const uint32_t b = static_cast<uint8_t>(biased(quant_code(x.y, inv)));
+    const uint32_t a = static_cast<uint8_t>(quant_code(x.x, inv));
+    const uint32_t b = static_cast<uint8_t>(quant_code(x.y, inv));
     return a | (b << 8);
   }
 
@@ -729,7 +728,7 @@ struct FusedAppend {
       }
     } else if (A.pos < A.n_sink) {
       if (on) {
-        v8s[lane] = 0x8080;  // a sink position is masked in the stream; keep the stage finite
+        v8s[lane] = 0;  // a sink position is masked in the stream; keep the stage finite
         if (d % kBlock == 0) st.vs[d / kBlock] = 0.0f;
       }
     } else {
@@ -1087,14 +1086,13 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
-  float M[GW], l[GW], o[GW][8], corr[kInt8 ? GW : 1];
+  float M[GW], l[GW], o[GW][8];
 #pragma unroll
   for (int g = 0; g < GW; ++g) {
     M[g] = kMinit;
     l[g] = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
-    if constexpr (kInt8) corr[g] = 0.0f;
   }
 
   while (ch < c_end) {
@@ -1143,7 +1141,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
     }
 
     // ---- q for this chunk: dense int8 folds the group's channel scales in
-    float qt[GW][8], qb[GW];
+    float qt[GW][8];
 #pragma unroll
     for (int g = 0; g < GW; ++g) {
       if constexpr (KIND == kI8Dense) {
@@ -1152,17 +1150,11 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
         const float4 qa4 = *reinterpret_cast<const float4*>(&s_qw[wave][g][4 * c]);
         const float4 qb4 = *reinterpret_cast<const float4*>(&s_qw[wave][g][HD / 2 + 4 * c]);
         const float q8[8] = {qa4.x, qa4.y, qa4.z, qa4.w, qb4.x, qb4.y, qb4.z, qb4.w};
-        float sum = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          qt[g][e] = q8[e] * ks8[e];
-          sum += qt[g][e];
-        }
-        qb[g] = -128.0f * sum;
+        for (int e = 0; e < 8; ++e) qt[g][e] = q8[e] * ks8[e];
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) qt[g][e] = qv[g][e];
-        qb[g] = 0.0f;
       }
     }
 
@@ -1180,7 +1172,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
           if constexpr (KIND == kI8Ring) {
             // dequantize (code * block scale, model.cpp:689-690)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) kx[e] = ksc[sl][e >> 2] * (kx[e] - 128.0f);
+            for (int e = 0; e < 8; ++e) kx[e] = ksc[sl][e >> 2] * kx[e];
           }
         } else {
           kx[0] = kf[sl][0].x; kx[1] = kf[sl][0].y; kx[2] = kf[sl][0].z; kx[3] = kf[sl][0].w;
@@ -1198,9 +1190,9 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
         }
 #pragma unroll
         for (int g = 0; g < GW; ++g) {
-          float a = qb[g];
+          float a = qt[g][0] * kx[0];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) a += qt[g][e] * kx[e];
+          for (int e = 1; e < 8; ++e) a += qt[g][e] * kx[e];
           acc[g][j] = a;
         }
       }
@@ -1237,7 +1229,6 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
       l[g] = ls;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
-      if constexpr (kInt8) corr[g] *= alpha;
     }
 
     // ---- weights to the PV mapping through this wave's LDS rows
@@ -1314,10 +1305,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
         }
         if constexpr (kInt8) {
 #pragma unroll
-          for (int g = 0; g < GW; ++g) {
-            wv[g] *= vsl;
-            corr[g] += wv[g];
-          }
+          for (int g = 0; g < GW; ++g) wv[g] *= vsl;
         }
 #pragma unroll
         for (int g = 0; g < GW; ++g)
@@ -1334,12 +1322,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
   // ---- wave epilogue: l over lanes, o over the RPW lane rows (transposing
   // permlane swaps: lane ends with values K = k + 2GW * (lane / 16), k < 2GW)
 #pragma unroll
-  for (int g = 0; g < GW; ++g) {
-    l[g] = wave_sum(l[g]) * (1.0f / C::DUP);
-    if constexpr (kInt8)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] -= 128.0f * corr[g];
-  }
+  for (int g = 0; g < GW; ++g) l[g] = wave_sum(l[g]) * (1.0f / C::DUP);
   float v1[4 * GW], v2[2 * GW];
 #pragma unroll
   for (int k = 0; k < 4 * GW; ++k)

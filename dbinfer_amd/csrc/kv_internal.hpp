@@ -5,7 +5,7 @@
 // stream for decode attention (the reference stores [slot][kv_head][hd],
 // model.hpp:108-214; dbi_kv_export converts back):
 //   fp32 (dense, ring)  k, v          [L][nkv][capg*hd]   fp32, granule layout
-//   int8                k8, v8        [L][nkv][capg*hd]   uint8 code+128, granule layout
+//   int8                k8, v8        [L][nkv][capg*hd]   int8 codes, granule layout
 //                       v_scale       [L][nkv][capg][nb]  fp32
 //   ring int8           k_scale       [L][nkv][capg][nb]  fp32 (per 32-block)
 //   dense int8          k_scale       [L][nkv][ng][hd]    fp32 (per channel, per 32-token group)
@@ -212,7 +212,7 @@ hipError_t launch_prefix_pack(const KvGeom& g, const float* src_store, float* ds
                               bool is_k, hipStream_t st);
 hipError_t launch_prefix_unpack(const KvGeom& g, const float* src, float* dst_store, int len,
                                 bool is_k, hipStream_t st);
-// int8 codes between the biased granule store and the file's signed
+// int8 codes between the granule store and the file's
 // [L][len][nkv][hd] (both directions; unpack = file -> store)
 hipError_t launch_prefix_codes(const KvGeom& g, int8_t* store, int8_t* file, int len, bool is_k,
                                bool unpack, hipStream_t st);

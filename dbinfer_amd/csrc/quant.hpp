@@ -39,8 +39,6 @@ __device__ __forceinline__ int8_t quant_lane(float x, float* scale) {
   return quant_code(x, inv);
 }
 
-// stored byte of an int8 code: code + 128
-__device__ __forceinline__ int8_t biased(int8_t code) { return static_cast<int8_t>(code ^ 0x80); }
 
 // KVCache::slot_for (model.cpp:321-324)
 __device__ __forceinline__ int slot_for(int pos, int s, int W) {
