@@ -1,1419 +1,24 @@
-// GQA attention over the three cache layouts (model.cpp:567-728) and the
-// causal chunk rows of decode_layer_chunk (model.cpp:956-981).
-//
-// Design (CDNA4, wave64):
-//  - Grid (split, kv_head, query_row), 8 waves per workgroup. A workgroup
-//    streams one contiguous range of key positions of ONE kv head and serves
-//    all G = gqa query heads of that head from the same bytes, so K/V cross
-//    HBM once per kv head (the reference re-reads them per query head,
-//    model.cpp:575-596).
-//  - A wave handles 32-position chunks (16 for the ring and for wide fp32
-//    groups), chunk t -> wave t % 8, in the granule layout of
-//    kv_internal.hpp: every load instruction reads 64 lanes x 8 elements,
-//    contiguous. A "lane row" of LPR = hd/8 lanes holds one position; RPW =
-//    64/LPR rows per instruction.
-//  - QK: each lane keeps the partial dots of its 8 dims for the NSG slots of
-//    a granule. K's slot order is permuted per lane (kslot_xor) so that the
-//    16-lane (hd 128) or 8-lane (hd 64) reduction is a transposing one: three
-//    DPP adds halve the slots and sum across lanes at once, and every lane
-//    ends up holding ONE position's full score (each position in 4 lanes).
-//    Softmax then runs once per position instead of once per lane row.
-//  - Softmax: wave-uniform running max (DPP row max, row_bcast15/31,
-//    readlane), exp2 with scale*log2(e) folded into q; weights go through a
-//    per-wave LDS buffer to the PV lane mapping (lane = 8 consecutive V dims
-//    of one position row).
-//  - Loads: K of the next chunk is issued right after QK, V of the next
-//    chunk right after PV, so one of them is always in flight.
-//  - Split-K: each split writes (o[G][HD], m[G], l[G]) of its range with
-//    agent-coherent stores, waits for them, and counts itself in a per
-//    (row, kv head) counter with one device-scope atomic. The split that
-//    arrives last merges every split (and the sinks) and resets the counter,
-//    so no second launch, no fence (an agent-scope fence is a whole-L2
-//    writeback on this multi-XCD part) and no memset between launches.
-//  - int8 dense: a 32-position chunk is exactly one K group, so the
-//    per-channel K scale folds into q once per chunk (the reference's
-//    (q_i * ks_i) * k8_i); codes are signed bytes, converted with one
-//    sign-extending SDWA v_cvt_f32_i32 each. The fp32 sinks (pos < n_sink)
-//    are attended in the merge as further entries.
-//  - Fused decode step (dbi_kv_decode): the append of the new row runs
-//    inside the launch (FusedAppend), staged in LDS for the wave that
-//    attends its chunk.
-//  - ring: keys are stored un-roped; each resident key is dequantized (int8:
-//    per-block scale) and roped at its cache-relative position from an fp32
-//    cos/sin table, q at n_res - 1 (model.cpp:662-700). K lanes hold dims d
-//    and d + hd/2 together, so the rotation is lane-local.
-#include <cmath>
-#include <cstdlib>
-#include <type_traits>
-
-#include "kv_internal.hpp"
-#include "quant.hpp"
+// Planning and launch of the GQA attention kernel (attn_kernel.hpp): the
+// split-K plan of a call, the kernel instance it needs, and its arguments.
+#include "attn_kernel.hpp"
 
 namespace dbi {
 namespace {
 
-constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / 64;
-constexpr int kMaxSplits = 64;  // one split per lane in the merge
-constexpr int kMergeBatch = 32;  // split records the merge loads per round
-// split-arrival counters sit 256 bytes apart: the atomics of different
-// (row, kv head) pairs never share a cache line
-constexpr int kCounterStride = 64;
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kMinit = -1.0e30f;  // finite: exp2(kMinit - kMinit) == 1, no NaN
-
-enum Kind { kF32Dense = 0, kI8Dense = 1, kF32Ring = 2, kI8Ring = 3 };
-
-struct AttnParams {
-  const float* kf;
-  const float* vf;
-  const uint8_t* k8;
-  const uint8_t* v8;
-  const float* ks;
-  const float* vs;
-  const float* ksink;
-  const float* vsink;
-  const float2* rope;
-  int rope_rows;
-  const float* q;
-  // decode from raw projections (rows == 1): q bias [n_heads*hd] or null, and
-  // the (cos, sin) row of the decode position for a dense rope, or null
-  const float* qb;
-  const double2* qcs;
-  float* out;
-  float* part;
-  unsigned* cnt;  // split arrivals per (row, kv head), zero between launches
-  int capg, ng, n_sink, nkv, n_heads;
-  int rows, pos0;
-  int ring_nres, ring_s, ring_W, ring_base;
-  int nsplit;  // splits (partial records) per (row, kv head)
-  int direct;  // 1: single split and no sinks, write the output directly;
-               // 0: write a partial record, the last split to arrive merges
-  int chunks_per_split;
-  float qscale;
-};
-
-// ---------------------------------------------------------------------------
-// cross-lane helpers
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
-}
-
-// DPP controls: lane ^ 8 within a 16-lane row (row_ror:8), lane ^ 7 within
-// 8 lanes (row_half_mirror), lane ^ 2 and lane ^ 1 (quad_perm).
-constexpr int kX8 = 0x128, kX7 = 0x141, kX2 = 0x4E, kX1 = 0xB1;
-
-// Row-broadcast step of a wave reduction: rows in ROWMASK combine with the
-// last lane of the row(s) before them, the other rows with `idle`.
-template <int CTRL, int ROWMASK>
-__device__ __forceinline__ float bcast(float x, float idle) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, idle), __builtin_bit_cast(int, x),
-                                         CTRL, ROWMASK, 0xF, false));
-}
-
-__device__ __forceinline__ float lane63(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-}
-
-// Wave-uniform max / sum of one value per lane.
-__device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, dpp<kX8>(v));
-  v = fmaxf(v, dpp<kX7>(v));
-  v = fmaxf(v, dpp<kX2>(v));
-  v = fmaxf(v, dpp<kX1>(v));
-  v = fmaxf(v, bcast<0x142, 0xA>(v, v));  // row_bcast:15
-  v = fmaxf(v, bcast<0x143, 0xC>(v, v));  // row_bcast:31
-  return lane63(v);
-}
-__device__ __forceinline__ float wave_sum(float v) {
-  v += dpp<kX8>(v);
-  v += dpp<kX7>(v);
-  v += dpp<kX2>(v);
-  v += dpp<kX1>(v);
-  v += bcast<0x142, 0xA>(v, 0.0f);
-  v += bcast<0x143, 0xC>(v, 0.0f);
-  return lane63(v);
-}
-
-// gfx950 permlane swaps, emitted through asm (the compiler's builtins fold
-// the two results into one when both are used). swap32(a, b): lanes 0-31
-// end with {own a, a of lane + 32}, lanes 32-63 with {b of lane - 32, own
-// b}; swap16 does the same between even and odd 16-lane rows. a + b after
-// the swap is therefore a's pair sum in the lower half and b's in the upper.
-__device__ __forceinline__ float swap32_sum(float a, float b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return a + b;
-}
-__device__ __forceinline__ float swap16_sum(float a, float b) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return a + b;
-}
-
-// Raw v_exp_f32 (2^x). Softmax weights below 2^-126 are far under the
-// output tolerance, so the denormal-range handling of exp2f is not needed.
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// tensor::rope's fp64 NeoX rotation of one pair (ops.cpp:31-34): products
-// and sums rounded one by one, as the reference's scalar code does
-__device__ __forceinline__ void rope_pair(float& a, float& b, double2 cs) {
-#pragma clang fp contract(off)
-  const double x = static_cast<double>(a) * cs.x - static_cast<double>(b) * cs.y;
-  const double y = static_cast<double>(b) * cs.x + static_cast<double>(a) * cs.y;
-  a = static_cast<float>(x);
-  b = static_cast<float>(y);
-}
-
-// Element d of one head row as the reference's host code hands it to the
-// cache (model.cpp:747-763): x + bias (one fp32 add; no add without a
-// bias), then, with a (cos, sin) row, the rope of its pair (d, d +- hd/2).
-template <int HD>
-__device__ __forceinline__ float produced(const float* x, const float* bias, const double2* cs,
-                                          int d) {
-  constexpr int H2 = HD / 2;
-  const int j = d % H2;
-  float a = x[j], b = x[j + H2];
-  if (bias != nullptr) {
-    a += bias[j];
-    b += bias[j + H2];
-  }
-  if (cs != nullptr) rope_pair(a, b, cs[j]);
-  return d < H2 ? a : b;
-}
-
-// Raw buffer resources (gfx9 descriptor word 3 = 0x00020000: 32-bit raw
-// data, bounds-checked against num_records bytes; reads past it return 0).
-using rsrc_t = __amdgpu_buffer_rsrc_t;
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), bytes,
-                                           0x00020000);
-}
-__device__ __forceinline__ float4 load_b128(rsrc_t r, int voff, int soff) {
-  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-__device__ __forceinline__ float2 load_b64(rsrc_t r, int voff, int soff) {
-  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
-}
-__device__ __forceinline__ float load_b32(rsrc_t r, int voff, int soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
-}
-// K/V rows are read once per call: non-temporal (gfx940+ cache policy NT)
-constexpr int kNT = 2;
-__device__ __forceinline__ float4 stream_b128(rsrc_t r, int voff, int soff) {
-  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kNT));
-}
-
-// 8 int8 codes -> float (one sign-extending SDWA v_cvt_f32_i32 each)
-__device__ __forceinline__ void cvt8(const uint2 w, float* f) {
-#pragma unroll
-  for (int b = 0; b < 4; ++b) f[b] = static_cast<float>(static_cast<int8_t>(w.x >> (8 * b)));
-#pragma unroll
-  for (int b = 0; b < 4; ++b) f[4 + b] = static_cast<float>(static_cast<int8_t>(w.y >> (8 * b)));
-}
-
-template <int HD, int G, int KIND>
-struct Cfg {
-  static constexpr bool kInt8 = (KIND == kI8Dense || KIND == kI8Ring);
-  static constexpr bool kRing = (KIND == kF32Ring || KIND == kI8Ring);
-  static constexpr int LPR = HD / 8;            // lanes per position row
-  static constexpr int RPW = 64 / LPR;          // rows per load instruction
-  static constexpr int NSG = kGranule / RPW;    // slots per granule
-  // granules per chunk: 2 (32 positions, one int8 K group) for dense int8;
-  // fp32 rows and the ring's rope table need the registers of a second one
-  static constexpr int NGC = KIND == kI8Dense ? 2 : 1;
-  static constexpr int CHUNK = kGranule * NGC;
-  static constexpr int NS = NSG * NGC;          // slots per chunk
-  // wide groups split their heads over two halves of the workgroup (each
-  // half streams the same chunks, the second read hitting L1/L2): a wave
-  // then holds q and o of GW <= 4 heads, which keeps them in registers
-  static constexpr int NHG = (G > 4 && (HD == 128 || KIND == kI8Dense)) ? 2 : 1;
-  static constexpr int GW = (G + NHG - 1) / NHG;  // query heads per wave
-  static constexpr int WPG = kWaves / NHG;        // waves per head group
-  static constexpr int GP = GW <= 4 ? 4 : 8;      // padded heads of an LDS weight row
-  static constexpr int DUP = LPR / NSG;         // lanes holding one position's score
-  static constexpr int NB = HD / kBlock;
-  static_assert(HD == 64 || HD == 128, "head dim");
-  static_assert(KIND != kI8Dense || CHUNK == kKGroup, "int8 chunk must be one K group");
-};
-
-// Reduces the NSG per-slot partial dots of a lane row to full scores, one
-// position per lane (lane c of the row ends with granule slot kslot_xor(c)).
-template <int HD>
-__device__ __forceinline__ float treduce(const float* a) {
-  float t;
-  if constexpr (HD == 128) {
-    const float s0 = a[0] + dpp<kX8>(a[2]);
-    const float s1 = a[1] + dpp<kX8>(a[3]);
-    t = s0 + dpp<kX7>(s1);
-  } else {
-    t = a[0] + dpp<kX7>(a[1]);
-  }
-  t += dpp<kX2>(t);
-  t += dpp<kX1>(t);
-  return t;
-}
-
-// Fused decode step (Model::decode_layer's kv.append then attend,
-// model.cpp:759-771): the row of one position, appended by the workgroup
-// whose split holds its storage chunk (FusedAppend below).
-struct AppendArgs {
-  const float* k;  // new row, device [nkv][hd]; nullptr: no append
-  const float* v;
-  // raw-projection step: the row is k + kb roped by kcs (dense) and v + vb;
-  // each may be null (no bias / no rope); prod = any of them set
-  const float* kb;
-  const float* vb;
-  const double2* kcs;
-  int prod;
-  int slot;        // storage row (dense: pos; ring: slot_for(pos)); -1: no append
-  int pos;
-  int nkv, n_sink, capg, ng;
-  float* kf;       // this layer's arrays, writable
-  float* vf;
-  uint8_t* k8;
-  uint8_t* v8;
-  float* ks;
-  float* vs;
-  float* k_raw;    // dense int8 staging [32][nkv*hd]
-  float* ksink;
-  float* vsink;
-};
-
-// Cross-wave combine of (m, l, o) in LDS, then either the final output
-// (single split) or this split's partial record. Head g was handled by the
-// WPG waves of head group g / GW, at their local head index g % GW.
-template <int HD, int G, int GW, int WPG>
-__device__ __forceinline__ void finish(const AttnParams& P, float (&s_o)[kWaves][GW][HD],
-                                       float (&s_ml)[kWaves][GW][2], float (&s_f)[G][WPG],
-                                       float (&s_M)[G], float (&s_L)[G], int split, int kh,
-                                       int qrow) {
-  __syncthreads();
-  if (static_cast<int>(threadIdx.x) < G) {
-    const int g = threadIdx.x, w0 = (g / GW) * WPG, gl = g % GW;
-    float M = kMinit;
-#pragma unroll
-    for (int i = 0; i < WPG; ++i) M = fmaxf(M, s_ml[w0 + i][gl][0]);
-    float L = 0.0f;
-#pragma unroll
-    for (int i = 0; i < WPG; ++i) {
-      const float f = fast_exp2(s_ml[w0 + i][gl][0] - M);
-      s_f[g][i] = f;
-      L += s_ml[w0 + i][gl][1] * f;
-    }
-    s_M[g] = M;
-    s_L[g] = L;
-  }
-  __syncthreads();
-
-  auto o_of = [&](int g, int d) {
-    const int w0 = (g / GW) * WPG, gl = g % GW;
-    float O = 0.0f;
-#pragma unroll
-    for (int i = 0; i < WPG; ++i) O += s_o[w0 + i][gl][d] * s_f[g][i];
-    return O;
-  };
-  const int rec_floats = G * (HD + 2);
-  const size_t head_base = static_cast<size_t>(qrow) * P.nkv + kh;
-  if (P.direct) {
-    float* out_base = P.out + (static_cast<size_t>(qrow) * P.n_heads + kh * G) * HD;
-    for (int idx = threadIdx.x; idx < G * HD; idx += kThreads) {
-      const int g = idx / HD, d = idx % HD;
-      out_base[idx] = o_of(g, d) / s_L[g];
-    }
-    return;
-  }
-  float* rec = P.part + (head_base * P.nsplit + split) * rec_floats;
-  for (int idx = threadIdx.x; idx < G * HD + 2 * G; idx += kThreads) {
-    float v;
-    if (idx < G * HD) {
-      v = o_of(idx / HD, idx % HD);
-    } else {
-      const int r = idx - G * HD;
-      v = r < G ? s_M[r] : s_L[r - G];
-    }
-    // written through to the device coherence point (the merging
-    // workgroup may run on another XCD, behind another L2)
-    __hip_atomic_store(rec + idx, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
-// The split merge of one (row, kv head), run by the workgroup whose split
-// arrived last (each split counts itself in P.cnt after its record stores
-// completed; the last one resets the count for the next launch). Wave g
-// merges query head g: the (m, l) of split s in lane s gives the split
-// weights (DPP max / sum), every lane combines its HD/64 dims of the split
-// records, then the fp32 sink positions, when the layout has them
-// (model.cpp:612-614), are attended as further entries with a running max.
-// Records are read at device coherence.
-template <int HD, int G, bool PROD>
-__device__ __forceinline__ void merge_last(const AttnParams& P, const AppendArgs& A, int kh,
-                                           int qrow, int wave, int lane, const float* qw) {
-  constexpr int DPL = HD / 64;
-  constexpr int kSinkBatch = 4;  // the usual n_sink: one batch, no idle reductions
-  constexpr int kSC1 = 16;  // cache policy: agent-coherent load
-  if (wave >= G) return;
-  const int g = wave;
-  const int rec_floats = G * (HD + 2);
-  const size_t head_base = static_cast<size_t>(qrow) * P.nkv + kh;
-  const rsrc_t rr = make_rsrc(P.part + head_base * P.nsplit * rec_floats,
-                              P.nsplit * rec_floats * 4);
-  auto ld = [&](int idx) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, idx * 4, 0, kSC1));
-  };
-  // every load of the merge in one round: (m, l) of split `lane`, this
-  // lane's dims of every split (clamped, surplus splits weighted 0), q and
-  // the first sink rows
-  const bool on = lane < P.nsplit;
-  const int r0 = min(lane, P.nsplit - 1) * rec_floats;
-  const float m = ld(r0 + G * HD + g);
-  const float l = ld(r0 + G * HD + G + g);
-  // up to kMaxSplits = 2 kMergeBatch records, both batches in the first
-  // round (every record read is a round trip to the device-coherent level)
-  static_assert(kMaxSplits <= 2 * kMergeBatch, "merge batches");
-  float ov[2][kMergeBatch][DPL];
-  auto load_batch = [&](int b) {
-#pragma unroll
-    for (int sp = 0; sp < kMergeBatch; ++sp) {
-      if (b > 0 && b * kMergeBatch + sp >= P.nsplit) {  // uniform: no such record
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) ov[b][sp][e] = 0.0f;
-        continue;
-      }
-      const int idx =
-          min(b * kMergeBatch + sp, P.nsplit - 1) * rec_floats + g * HD + lane * DPL;
-      if constexpr (DPL == 2) {  // the lane's two dims in one 8-byte load
-        const float2 t = __builtin_bit_cast(
-            float2, __builtin_amdgcn_raw_buffer_load_b64(rr, idx * 4, 0, kSC1));
-        ov[b][sp][0] = t.x;
-        ov[b][sp][1] = t.y;
-      } else {
-        ov[b][sp][0] = ld(idx);
-      }
-    }
-  };
-  load_batch(0);
-  const bool two = P.nsplit > kMergeBatch;  // uniform
-  if (two) load_batch(1);
-  const int ns = min(P.n_sink, P.pos0 + qrow + 1);
-  const size_t h = static_cast<size_t>(qrow) * P.n_heads + kh * G + g;
-  float qd[DPL], kd[kSinkBatch][DPL], vd[kSinkBatch][DPL];
-  // sink row p; a fused step's own sink row is flushed after this merge,
-  // so that one comes from the step's inputs
-  auto sink_rows = [&](int p0) {
-#pragma unroll
-    for (int b = 0; b < kSinkBatch; ++b) {
-      const int p = min(p0 + b, ns - 1);
-      const bool fresh = A.slot >= 0 && p == A.pos;
-      const size_t at = (static_cast<size_t>(kh) * P.n_sink + p) * HD + lane * DPL;
-      if (PROD && fresh && A.prod) {  // raw projections: the produced row
-        const float* kb = A.kb != nullptr ? A.kb + kh * HD : nullptr;
-        const float* vb = A.vb != nullptr ? A.vb + kh * HD : nullptr;
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) {
-          kd[b][e] = produced<HD>(A.k + kh * HD, kb, A.kcs, lane * DPL + e);
-          vd[b][e] = produced<HD>(A.v + kh * HD, vb, nullptr, lane * DPL + e);
-        }
-      } else {
-        const float* kr = fresh ? A.k + kh * HD + lane * DPL : P.ksink + at;
-        const float* vr = fresh ? A.v + kh * HD + lane * DPL : P.vsink + at;
-        if constexpr (DPL == 2) {  // 8-byte aligned pairs: one load each
-          const float2 k2 = *reinterpret_cast<const float2*>(kr);
-          const float2 v2 = *reinterpret_cast<const float2*>(vr);
-          kd[b][0] = k2.x;
-          kd[b][1] = k2.y;
-          vd[b][0] = v2.x;
-          vd[b][1] = v2.y;
-        } else {
-          kd[b][0] = kr[0];
-          vd[b][0] = vr[0];
-        }
-      }
-    }
-  };
-  if (ns > 0) {
-#pragma unroll
-    for (int e = 0; e < DPL; ++e)
-      // the scaled q row the workgroup keeps in LDS (only dense int8 has
-      // sinks; the same bits as q * qscale, produced q in PROD)
-      qd[e] = qw[lane * DPL + e];
-    sink_rows(0);
-  }
-
-  float M = wave_max(on ? m : kMinit);
-  const float w = on ? fast_exp2(m - M) : 0.0f;
-  float L = wave_sum(on ? l * w : 0.0f);
-  float O[DPL] = {};
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    if (b == 1 && !two) break;
-#pragma unroll
-    for (int sp = 0; sp < kMergeBatch; ++sp) {
-      // lanes past nsplit hold weight 0 (and clamped records)
-      const float ws = __builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), b * kMergeBatch + sp));
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) O[e] += ws * ov[b][sp][e];
-    }
-  }
-  // sinks as further entries, a batch at a time with a running max
-  for (int p0 = 0; p0 < ns; p0 += kSinkBatch) {
-    if (p0 > 0) sink_rows(p0);
-    float sc[kSinkBatch];
-    float bm = M;
-#pragma unroll
-    for (int b = 0; b < kSinkBatch; ++b) {
-      float dot = 0.0f;
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) dot += qd[e] * kd[b][e];
-      sc[b] = -INFINITY;
-      if (p0 + b < ns) sc[b] = wave_sum(dot);  // uniform
-      bm = fmaxf(bm, sc[b]);
-    }
-    const float f = fast_exp2(M - bm);
-    M = bm;
-    L *= f;
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) O[e] *= f;
-#pragma unroll
-    for (int b = 0; b < kSinkBatch; ++b) {
-      const float ws = fast_exp2(sc[b] - M);
-      L += ws;
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) O[e] += ws * vd[b][e];
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < DPL; ++e) P.out[h * HD + lane * DPL + e] = O[e] / L;
-}
-
-
-// LDS stage of a fused step's new values, in the layouts the attention
-// reads them in, for the wave that processes the appended chunk.
-struct AppStage {
-  float ks[4];                       // ring int8: the new row's K block scales
-  float vs[4];                       // int8: the new row's V block scales
-  float krow[128];                   // fp32: the new K row
-  float vrow[128];                   // fp32: the new V row
-  uint32_t k8row[32];                // ring int8: the new K codes
-  uint32_t v8row[32];                // int8: the new V codes
-};
-
-// Dense int8: the requantized 32-token group of the fused step, shared by
-// the head groups of the workgroup.
-struct KGroupStage {
-  uint4 kchunk[kKGroup * 128 / 16];  // the group's codes, granule layout
-  float ks[128];                     // its channel scales
-  unsigned done;                     // requantizing waves done (zeroed at launch)
-};
-
-// One kv head's part of KVCache::append (model.cpp:357-404) inside the
-// attention kernel, with the arithmetic of the append kernels (quant.hpp):
-// fp32 rows are copied; int8 ring rows are block-quantized (a 32-element
-// block spans 16 lanes, two elements per lane); dense int8 stages the raw K
-// row and requantizes its 32-token group per channel, and block-quantizes
-// V, or stores both as fp32 sinks when pos < n_sink. New values go to LDS
-// stages in the layouts the attention reads, and to global memory only
-// after the writing wave's last load (a store in flight would hold back its
-// next wait on loads).
-//
-// Work split: the wave (of each head group) that attends the new row's
-// chunk, the owner, stages the row itself. The dense int8 group
-// requantization (32 codes per channel, far too long for one wave's
-// critical path) is shared by the first RW waves of the workgroup, CPW
-// channels each, before their own chunk: their loads go out first, so the
-// shares are done by the time the owner (usually a later wave) reaches the
-// new row's chunk. They publish through an LDS counter that only the owners
-// wait on; no other wave waits.
-//
-// Loads are LDS-direct (16 bytes per lane, no registers held): the new K
-// and V rows into `row` ([0, HD) and [HD, 2 HD) of 256 floats; k_dev and
-// v_dev are 16-byte aligned) and a wave's channels of the group's 32 staged
-// raw rows into its `raw` share ([32][CPW]). The compiler does not track
-// these loads: the consumers wait for them explicitly.
-template <int HD, int KIND, bool PROD>
-struct FusedAppend {
-  static constexpr bool kInt8 = (KIND == kI8Dense || KIND == kI8Ring);
-  static constexpr int NB = HD / kBlock;
-  static constexpr int RW = kWaves / 2;       // dense int8: requantizing waves
-  static constexpr int CPW = HD / RW;         // channels per requantizing wave
-  static constexpr int RPL = kKGroup * CPW / 64;  // raw rows per lane of a share
-
-  __device__ __forceinline__ static void wait_loads() {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  }
-  __device__ __forceinline__ static void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
-
-  __device__ __forceinline__ static void load_row(const AppendArgs& A, int kh, int lane,
-                                                  float* row) {
-    constexpr int Q = HD / 4;         // lanes per row
-    const int hl = lane % (2 * Q);    // lanes past 2Q (hd 64) repeat into row[2 HD, 4 HD)
-    const float* src = (hl < Q ? A.k : A.v) + kh * HD + (hl % Q) * 4;
-    __builtin_amdgcn_global_load_lds(src, row, 16, 0, 0);
-    if (PROD && A.prod) {  // raw projections: the (cos, sin) row and the biases too
-      if (A.kcs != nullptr)
-        __builtin_amdgcn_global_load_lds(A.kcs + lane % (HD / 2), row + 256, 16, 0, 0);
-      if (A.kb != nullptr || A.vb != nullptr) {  // a missing one is loaded but not added
-        const float* kb = A.kb != nullptr ? A.kb : A.vb;
-        const float* vb = A.vb != nullptr ? A.vb : A.kb;
-        __builtin_amdgcn_global_load_lds((hl < Q ? kb : vb) + kh * HD + (hl % Q) * 4, row + 512,
-                                         16, 0, 0);
-      }
-    }
-  }
-
-  // raw projections, owner wave, after wait_loads(): the row in LDS becomes
-  // k + kb roped and v + vb, exactly as produced() computes each element
-  __device__ __forceinline__ static void produce_row(const AppendArgs& A, int lane, float* row) {
-    constexpr int H2 = HD / 2;
-    const float* bias = row + 512;  // kb [0, HD), vb [HD, 2 HD)
-    if (lane < H2) {
-      float a = row[lane], b = row[lane + H2];
-      if (A.kb != nullptr) {
-        a += bias[lane];
-        b += bias[lane + H2];
-      }
-      if (A.kcs != nullptr) rope_pair(a, b, reinterpret_cast<const double2*>(row + 256)[lane]);
-      row[lane] = a;
-      row[lane + H2] = b;
-    }
-    if (A.vb != nullptr && 2 * lane < HD) {
-      row[HD + 2 * lane] += bias[HD + 2 * lane];
-      row[HD + 2 * lane + 1] += bias[HD + 2 * lane + 1];
-    }
-    wave_sync();
-  }
-
-  // the loaded inputs of a share's channel of the new K row: the value
-  // (raw projections: the pair's raw values and biases and its (cos, sin),
-  // combined only after the wait, so no wait stalls the share's loads)
-  struct ShareIn {
-    float x0, x1, b0, b1;
-    double2 cs;
-  };
-  __device__ __forceinline__ static float share_value(const AppendArgs& A, const ShareIn& in,
-                                                      int d) {
-    if constexpr (PROD) {
-      if (A.prod) {
-        float a = in.x0, b = in.x1;
-        if (A.kb != nullptr) {
-          a += in.b0;
-          b += in.b1;
-        }
-        if (A.kcs != nullptr) rope_pair(a, b, in.cs);
-        return d % HD < HD / 2 ? a : b;
-      }
-    }
-    return in.x0;
-  }
-
-  // dense int8, wave < RW: its raw share (LDS-direct) and its channel of
-  // the new K row (lane l holds channel l % CPW of the share)
-  __device__ __forceinline__ static ShareIn load_share(const AppendArgs& A, int kh, int wave,
-                                                       int lane, float* raw) {
-    constexpr int LPRW = CPW / 4, RPI = 64 / LPRW;  // lanes per share row, rows per load
-    const size_t P_ = static_cast<size_t>(A.nkv) * HD;
-    const float* src = A.k_raw + static_cast<size_t>(lane / LPRW) * P_ + kh * HD + wave * CPW +
-                       (lane % LPRW) * 4;
-#pragma unroll
-    for (int m = 0; m < kKGroup / RPI; ++m)
-      __builtin_amdgcn_global_load_lds(src + m * RPI * P_, raw + m * RPI * CPW, 16, 0, 0);
-    const int d = wave * CPW + lane % CPW;
-    ShareIn in{};
-    if (PROD && A.prod) {
-      const int j = d % (HD / 2);
-      const float* x = A.k + kh * HD;
-      in.x0 = x[j];
-      in.x1 = x[j + HD / 2];
-      if (A.kb != nullptr) {
-        in.b0 = A.kb[kh * HD + j];
-        in.b1 = A.kb[kh * HD + j + HD / 2];
-      }
-      if (A.kcs != nullptr) in.cs = A.kcs[j];
-    } else {
-      in.x0 = A.k[kh * HD + d];
-    }
-    return in;
-  }
-
-  // dense int8, wave < RW, after wait_loads(): requantize_kgroup
-  // (model.cpp:329-355) of the wave's CPW channels over raw rows
-  // [0, within] that are not sinks (row `within` is the new one). Lane l
-  // takes channel l % CPW over RPL rows; the channel max combines its lanes
-  // by xor shuffles. Rows outside the range count |x| * 0 (0, or a NaN that
-  // max_f skips as it skips NaN inputs) and their codes are neither
-  // attended (masked positions) nor flushed.
-  __device__ __forceinline__ static void requant_share(const AppendArgs& A, int wave, int lane,
-                                                       const ShareIn& in, float* raw,
-                                                       KGroupStage& kg) {
-    const int within = A.pos % kKGroup, first = A.pos - within;
-    const int c = lane % CPW, rb = lane / CPW;
-    const float knew = share_value(A, in, wave * CPW + c);
-    if (lane < CPW) raw[within * CPW + c] = knew;
-    wave_sync();
-    float x[RPL];
-#pragma unroll
-    for (int i = 0; i < RPL; ++i) x[i] = raw[(rb * RPL + i) * CPW + c];
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < RPL; ++i) {
-      const int w = rb * RPL + i;
-      m = max_f(m, fabsf(x[i]) * ((w <= within && first + w >= A.n_sink) ? 1.0f : 0.0f));
-    }
-#pragma unroll
-    for (int off = CPW; off < 64; off <<= 1) m = max_f(m, __shfl_xor(m, off));
-    const float sc = m / 127.0f;
-    const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
-    uint8_t* kc = reinterpret_cast<uint8_t*>(kg.kchunk);
-    const int d = wave * CPW + c;
-#pragma unroll
-    for (int i = 0; i < RPL; ++i)
-      kc[k_off_tiled(HD, true, rb * RPL + i, d)] = static_cast<uint8_t>(quant_code(x[i], inv));
-    if (lane < CPW) kg.ks[d] = sc;
-    // publish (the release orders the stage writes before the count)
-    if (lane == 0) __hip_atomic_fetch_add(&kg.done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-
-  // dense int8 owner: wait until all RW shares are published
-  __device__ __forceinline__ static void await_shares(const KGroupStage& kg) {
-    while (__hip_atomic_load(&kg.done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
-           static_cast<unsigned>(RW))
-      __builtin_amdgcn_s_sleep(1);
-  }
-
-  // quant_head of a 32-element block held two per lane by 16 lanes
-  __device__ __forceinline__ static float block_scale(float2 x) {
-    float m = max_f(fabsf(x.x), fabsf(x.y));
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) m = max_f(m, __shfl_xor(m, off, 16));
-    return m / 127.0f;
-  }
-  __device__ __forceinline__ static uint32_t codes2(float2 x, float s) {
-    const float inv = s > 0.0f ? 1.0f / s : 0.0f;
-    const uint32_t a = static_cast<uint8_t>(quant_code(x.x, inv));
-    const uint32_t b = static_cast<uint8_t>(quant_code(x.y, inv));
-    return a | (b << 8);
-  }
-
-  // owner wave, after wait_loads(): the row's own values into its stage
-  // (dense int8: V only; the K group is requant_share's)
-  __device__ __forceinline__ static void stage_row(const AppendArgs& A, int lane, AppStage& st,
-                                                   const float* row) {
-    const bool on = 2 * lane < HD;
-    const int d = 2 * lane;
-    const float2 kx = on ? *reinterpret_cast<const float2*>(row + d) : float2{};
-    const float2 vx = on ? *reinterpret_cast<const float2*>(row + HD + d) : float2{};
-    uint16_t* k8s = reinterpret_cast<uint16_t*>(st.k8row);
-    uint16_t* v8s = reinterpret_cast<uint16_t*>(st.v8row);
-    if constexpr (!kInt8) {
-      if (on) {
-        *reinterpret_cast<float2*>(&st.krow[d]) = kx;
-        *reinterpret_cast<float2*>(&st.vrow[d]) = vx;
-      }
-    } else if constexpr (KIND == kI8Ring) {
-      const float sk = block_scale(kx), sv = block_scale(vx);
-      if (on) {
-        k8s[lane] = static_cast<uint16_t>(codes2(kx, sk));
-        v8s[lane] = static_cast<uint16_t>(codes2(vx, sv));
-        if (d % kBlock == 0) {
-          st.ks[d / kBlock] = sk;
-          st.vs[d / kBlock] = sv;
-        }
-      }
-    } else if (A.pos < A.n_sink) {
-      if (on) {
-        v8s[lane] = 0;  // a sink position is masked in the stream; keep the stage finite
-        if (d % kBlock == 0) st.vs[d / kBlock] = 0.0f;
-      }
-    } else {
-      const float sv = block_scale(vx);
-      if (on) {
-        v8s[lane] = static_cast<uint16_t>(codes2(vx, sv));
-        if (d % kBlock == 0) st.vs[d / kBlock] = sv;
-      }
-    }
-    wave_sync();
-  }
-
-  // The stages to global memory in whole contiguous pieces, by one wave per
-  // kv head, after its last load.
-  __device__ __forceinline__ static void flush(const AppendArgs& A, int kh, int lane,
-                                               const AppStage& st, const KGroupStage& kg,
-                                               const float* row) {
-    const bool on = 2 * lane < HD;
-    const int d = 2 * lane;
-    const size_t hel = static_cast<size_t>(kh) * A.capg * HD;
-    constexpr int LPR = HD / 8, RPW = 64 / LPR;
-    const int pg = A.slot & 15, rr = pg % RPW, ii = pg / RPW;  // the row's granule slot
-    if constexpr (KIND == kI8Dense) {
-      const int pos = A.pos, grp = pos / kKGroup, within = pos % kKGroup, first = pos - within;
-#pragma unroll 4
-      for (int m = 0; m < kKGroup * HD / 8 / 64; ++m) {  // one 8-byte piece per lane each
-        const int o = (m * 64 + lane) * 8, gs = o / (kGranule * HD), og = o % (kGranule * HD);
-        const int l = (og % 1024) / 16, j = 2 * (og / 1024) + (og % 16) / 8;
-        const int r = l / LPR, c = l % LPR;
-        const int w = gs * kGranule + (j ^ kslot_xor(HD, c)) * RPW + r;
-        if (w <= within && first + w >= A.n_sink)  // later rows and sinks keep their memory
-          *reinterpret_cast<uint2*>(A.k8 + hel + static_cast<size_t>(first) * HD + o) =
-              *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(kg.kchunk) + o);
-      }
-      if (on) {
-        const float2 kx = *reinterpret_cast<const float2*>(row + d);
-        *reinterpret_cast<float2*>(A.ks + (static_cast<size_t>(kh) * A.ng + grp) * HD + d) =
-            *reinterpret_cast<const float2*>(&kg.ks[d]);
-        *reinterpret_cast<float2*>(A.k_raw + static_cast<size_t>(within) * A.nkv * HD + kh * HD +
-                                   d) = kx;
-        if (pos < A.n_sink) {
-          const size_t at = (static_cast<size_t>(kh) * A.n_sink + pos) * HD + d;
-          *reinterpret_cast<float2*>(A.ksink + at) = kx;
-          *reinterpret_cast<float2*>(A.vsink + at) = *reinterpret_cast<const float2*>(row + HD + d);
-        }
-      }
-      if (pos >= A.n_sink) {
-        if (lane < LPR)  // V row: dims 8c..8c+7 of lane (rr, c)
-          *reinterpret_cast<uint2*>(A.v8 + hel +
-                                    granule_off(HD, true, pos, ii, rr * LPR + lane, 0)) =
-              make_uint2(st.v8row[2 * lane], st.v8row[2 * lane + 1]);
-        if (lane < NB) A.vs[(static_cast<size_t>(kh) * A.capg + pos) * NB + lane] = st.vs[lane];
-      }
-    } else if constexpr (KIND == kI8Ring) {
-      if (lane < LPR) {
-        const int c = lane, j = ii ^ kslot_xor(HD, c);
-        *reinterpret_cast<uint2*>(A.k8 + hel + granule_off(HD, true, A.slot, j, rr * LPR + c, 0)) =
-            make_uint2(st.k8row[c], st.k8row[HD / 8 + c]);
-        *reinterpret_cast<uint2*>(A.v8 + hel + granule_off(HD, true, A.slot, ii, rr * LPR + c, 0)) =
-            make_uint2(st.v8row[2 * c], st.v8row[2 * c + 1]);
-      }
-      if (lane < NB) {
-        const size_t srow = static_cast<size_t>(kh) * A.capg + A.slot;
-        A.ks[srow * NB + lane] = st.ks[lane];
-        A.vs[srow * NB + lane] = st.vs[lane];
-      }
-    } else {
-      if (lane < LPR) {
-        const int c = lane, j = ii ^ kslot_xor(HD, c);
-        float* kdst = A.kf + hel + granule_off(HD, false, A.slot, j, rr * LPR + c, 0);
-        *reinterpret_cast<float4*>(kdst) = *reinterpret_cast<const float4*>(&row[4 * c]);
-        *reinterpret_cast<float4*>(kdst + 256) =
-            *reinterpret_cast<const float4*>(&row[HD / 2 + 4 * c]);
-        float* vdst = A.vf + hel + granule_off(HD, false, A.slot, ii, rr * LPR + c, 0);
-        *reinterpret_cast<float4*>(vdst) = *reinterpret_cast<const float4*>(&row[HD + 8 * c]);
-        *reinterpret_cast<float4*>(vdst + 256) =
-            *reinterpret_cast<const float4*>(&row[HD + 8 * c + 4]);
-      }
-    }
-  }
-};
-
-template <int HD, int G, int KIND, bool PROD>
-__global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, const AppendArgs A) {
-  using C = Cfg<HD, G, KIND>;
-  constexpr int LPR = C::LPR, RPW = C::RPW, NSG = C::NSG, NGC = C::NGC, NS = C::NS;
-  constexpr int CHUNK = C::CHUNK, GP = C::GP, NB = C::NB;
-  constexpr int GW = C::GW, WPG = C::WPG;
-  constexpr bool kInt8 = C::kInt8, kRing = C::kRing;
-
-  __shared__ float s_o[kWaves][GW][HD];
-  __shared__ float s_ml[kWaves][GW][2];
-  __shared__ float s_f[G][WPG];
-  __shared__ float s_M[G];
-  __shared__ float s_L[G];
-  __shared__ int s_last;
-  __shared__ __align__(16) float s_w[kWaves][CHUNK][GP];
-  __shared__ __align__(16) AppStage s_stage[C::NHG];
-  // dense int8 keeps each wave's scaled q in LDS, not registers, between
-  // chunks (it is re-scaled by every group's channel scales anyway)
-  __shared__ __align__(16) float s_qw[KIND == kI8Dense ? kWaves : 1][GW][HD];
-  // dense int8 fused step: each head group's copy of the group's raw K rows
-  // fused step inputs, per head group: the new K and V rows, and (dense
-  // int8) the group's raw K rows
-  // ([0, 256): K and V rows; raw projections: [256, 512) the (cos, sin)
-  // row, [512, 768) the K and V biases)
-  __shared__ __align__(16) float s_row[C::NHG][PROD ? 768 : 256];
-  __shared__ __align__(16) float s_raw[KIND == kI8Dense ? kWaves / 2 : 1][KIND == kI8Dense ? kKGroup * HD / (kWaves / 2) : 1];
-  __shared__ __align__(16) uint8_t s_kgbuf[KIND == kI8Dense ? sizeof(KGroupStage) : 16];
-  KGroupStage& s_kg = *reinterpret_cast<KGroupStage*>(s_kgbuf);
-
-  const int lane = threadIdx.x & 63;
-  // wave index as a provably uniform value: buffer-load SGPR offsets derive
-  // from it (a divergent one would turn every load into a waterfall loop)
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g0 = (wave / WPG) * GW;  // first query head of this wave's head group
-  const int wl = wave % WPG;         // wave index inside the head group
-  const int c = lane % LPR;
-  const int r = lane / LPR;
-  const int split = blockIdx.x;
-  const int kh = blockIdx.y;
-  const int qrow = blockIdx.z;
-  const int nkeys = kRing ? P.ring_nres : P.pos0 + qrow + 1;
-
-  const int nchunks = (nkeys + CHUNK - 1) / CHUNK;
-  const int c_end = min((split + 1) * P.chunks_per_split, nchunks);
-  const size_t head = static_cast<size_t>(kh) * P.capg;  // first row of this kv head
-  const size_t head_el = head * HD;
-  const int kx_slot = kslot_xor(HD, c);  // granule slot of this lane's scores
-  const int app_chunk = A.slot >= 0 ? A.slot / CHUNK : -1;
-  const bool app_here =
-      app_chunk >= split * P.chunks_per_split && app_chunk < c_end;  // workgroup-uniform
-
-  // ---- per-chunk register buffers
-  uint2 kq[kInt8 ? NS : 1], vq[kInt8 ? NS : 1];
-  float4 kf[kInt8 ? 1 : NS][2], vf[kInt8 ? 1 : NS][2];
-  float4 ksv[KIND == kI8Dense ? 2 : 1];    // dense int8 channel scales of the group
-  float ksc[KIND == kI8Ring ? NS : 1][2];  // ring int8 K block scales
-  float vsc[kInt8 ? NS : 1];               // int8 V block scales
-  float4 cs[kRing ? NS : 1][2];            // ring rope cos/sin of the lane's 4 pairs
-
-  auto rope_pos = [&](int slot) {
-    if (slot < P.ring_s) return slot;
-    int t = slot - P.ring_s - P.ring_base;
-    t += t < 0 ? P.ring_W : 0;
-    return P.ring_s + t;
-  };
-
-  // Buffer resources of this kv head's arrays: every load is a raw buffer
-  // load with a wave-uniform SGPR offset (chunk and slot) and one per-lane
-  // VGPR offset, so no 64-bit address registers are held per load.
-  constexpr int ES = kInt8 ? 1 : 4;  // bytes per K/V element
-  const int kv_bytes = P.capg * HD * ES;
-  const rsrc_t rk = make_rsrc(kInt8 ? static_cast<const void*>(P.k8 + head_el)
-                                    : static_cast<const void*>(P.kf + head_el), kv_bytes);
-  const rsrc_t rv = make_rsrc(kInt8 ? static_cast<const void*>(P.v8 + head_el)
-                                    : static_cast<const void*>(P.vf + head_el), kv_bytes);
-  // (arrays a layout lacks get an empty resource: every read returns 0)
-  const rsrc_t rks =
-      KIND == kI8Dense ? make_rsrc(P.ks + static_cast<size_t>(kh) * P.ng * HD, P.ng * HD * 4)
-      : KIND == kI8Ring ? make_rsrc(P.ks + head * NB, P.capg * NB * 4)
-                        : make_rsrc(P.q, 0);
-  const rsrc_t rvs = kInt8 ? make_rsrc(P.vs + head * NB, P.capg * NB * 4) : make_rsrc(P.q, 0);
-  const rsrc_t rcs = kRing ? make_rsrc(P.rope, P.rope_rows * (HD / 2) * 8) : make_rsrc(P.q, 0);
-
-  auto issue_k = [&](int ch) {
-    const int p0 = __builtin_amdgcn_readfirstlane(ch * CHUNK);  // uniform: SGPR offsets
-    // the group a fused step requantized comes from LDS (patch_k)
-    if (KIND == kI8Dense && ch == app_chunk) return;
-#pragma unroll
-    for (int gs = 0; gs < NGC; ++gs)
-#pragma unroll
-      for (int j = 0; j < NSG; ++j) {
-        const int sl = gs * NSG + j;
-        const int so = (p0 + gs * kGranule) * HD * ES + j * 512 * ES;
-        if constexpr (kInt8) {
-          if ((j & 1) == 0) {  // one 16-byte load per lane covers slots j, j + 1
-            const uint4 t = __builtin_bit_cast(uint4, stream_b128(rk, lane * 16, so));
-            kq[sl] = make_uint2(t.x, t.y);
-            kq[sl + 1] = make_uint2(t.z, t.w);
-          }
-        } else {
-          kf[sl][0] = stream_b128(rk, lane * 16, so);
-          kf[sl][1] = stream_b128(rk, lane * 16, so + 1024);
-        }
-        if constexpr (kRing) {
-          const int p = min(p0 + gs * kGranule + (j ^ kx_slot) * RPW + r, nkeys - 1);
-          const int co = rope_pos(p) * (HD / 2) * 8 + 32 * c;
-          cs[sl][0] = load_b128(rcs, co, 0);
-          cs[sl][1] = load_b128(rcs, co + 16, 0);
-          if constexpr (KIND == kI8Ring) {
-            // the position's block scales in one load: the lane's dims 4c..
-            // and hd/2 + 4c.. sit in blocks c / 8 and NB / 2 + c / 8
-            if constexpr (HD == 128) {
-              const float4 t = load_b128(rks, p * NB * 4, 0);
-              ksc[sl][0] = c >= 8 ? t.y : t.x;
-              ksc[sl][1] = c >= 8 ? t.w : t.z;
-            } else {
-              const float2 t = load_b64(rks, p * NB * 4, 0);
-              ksc[sl][0] = t.x;
-              ksc[sl][1] = t.y;
-            }
-          }
-        }
-      }
-    if constexpr (KIND == kI8Dense) {
-      const int so = (p0 / kKGroup) * HD * 4;
-      ksv[0] = load_b128(rks, 16 * c, so);
-      ksv[1] = load_b128(rks, 16 * c + HD * 2, so);
-    }
-  };
-
-  auto issue_v = [&](int ch) {
-    const int p0 = __builtin_amdgcn_readfirstlane(ch * CHUNK);  // uniform: SGPR offsets
-#pragma unroll
-    for (int gs = 0; gs < NGC; ++gs)
-#pragma unroll
-      for (int i = 0; i < NSG; ++i) {
-        const int sl = gs * NSG + i;
-        const int pb = p0 + gs * kGranule + i * RPW;  // position of row 0
-        const int so = (p0 + gs * kGranule) * HD * ES + i * 512 * ES;
-        if constexpr (kInt8) {
-          if ((i & 1) == 0) {
-            const uint4 t = __builtin_bit_cast(uint4, stream_b128(rv, lane * 16, so));
-            vq[sl] = make_uint2(t.x, t.y);
-            vq[sl + 1] = make_uint2(t.z, t.w);
-          }
-          vsc[sl] = load_b32(rvs, (r * NB + (8 * c) / kBlock) * 4, pb * NB * 4);
-        } else {
-          vf[sl][0] = stream_b128(rv, lane * 16, so);
-          vf[sl][1] = stream_b128(rv, lane * 16, so + 1024);
-        }
-      }
-  };
-
-  // ---- q of this lane's K dims (4c..4c+3, hd/2+4c..), in the log2 domain;
-  // the ring ropes it at n_res - 1 (model.cpp:669-671). Its loads go out
-  // before the first chunk's: vector loads return in order, so q issued last
-  // would hold QK back until the whole chunk (V included) had arrived.
-  float4 qa[GW], qc[GW], cq[2];
-  // Raw projections (PROD, decode): the q bias of the lane's dims and the
-  // (cos, sin) of its 4 pairs load with q and are applied with the scaling
-  // below (bias, then the fp64 rope of every head the lane holds)
-  float4 qba[GW], qbc[GW];
-  double2 qt[4];
-  const bool q_bias = PROD && P.qb != nullptr, q_rope = PROD && !kRing && P.qcs != nullptr;
-  if (q_bias) {
-#pragma unroll
-    for (int g = 0; g < GW; ++g) {
-      const float* bg = P.qb + (kh * G + min(g0 + g, G - 1)) * HD;
-      qba[g] = *reinterpret_cast<const float4*>(bg + 4 * c);
-      qbc[g] = *reinterpret_cast<const float4*>(bg + HD / 2 + 4 * c);
-    }
-  }
-  if (q_rope) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) qt[t] = P.qcs[4 * c + t];
-  }
-  {
-    const float* qb = P.q + (static_cast<size_t>(qrow) * P.n_heads + kh * G) * HD;
-    if constexpr (kRing) {
-      const float4* t = reinterpret_cast<const float4*>(
-          P.rope + static_cast<size_t>(P.ring_nres - 1) * (HD / 2) + 4 * c);
-      cq[0] = t[0];
-      cq[1] = t[1];
-    }
-#pragma unroll
-    for (int g = 0; g < GW; ++g) {
-      const float* qg = qb + min(g0 + g, G - 1) * HD;
-      qa[g] = *reinterpret_cast<const float4*>(qg + 4 * c);
-      qc[g] = *reinterpret_cast<const float4*>(qg + HD / 2 + 4 * c);
-    }
-  }
-  // fused decode step (FusedAppend): the owner wave of each head group
-  // stages the new row and takes its values from the stage for that chunk,
-  // so no global read-after-write happens inside the kernel. The row's
-  // inputs load ahead of the owner's first chunk when that chunk is the new
-  // row's, else right behind it (vector loads return in order, so they then
-  // hold back nothing before that chunk), and are staged on reaching the
-  // chunk. Dense int8: waves [0, RW) requantize the row's group before their
-  // own chunk and count themselves done in LDS (zeroed here first).
-  AppStage& s_app = s_stage[wave / WPG];
-  const int app_rel = app_chunk - split * P.chunks_per_split;
-  const bool app_owner = app_here && wl == app_rel % WPG;  // wave-uniform
-  const bool app_first = app_rel / WPG == 0;
-  using App = FusedAppend<HD, KIND, PROD>;
-  float* app_row = s_row[wave / WPG];
-  constexpr bool kShare = KIND == kI8Dense;
-  const bool app_share = kShare && app_here && wave < App::RW;  // wave-uniform
-  float* app_raw = s_raw[kShare && wave < App::RW ? wave : 0];
-  if constexpr (kShare) {
-    if (app_here) {  // workgroup-uniform
-      if (threadIdx.x == 0) s_kg.done = 0;
-      __syncthreads();
-    }
-  }
-  typename App::ShareIn app_knew{};
-  if (app_share) app_knew = App::load_share(A, kh, wave, lane, app_raw);
-  if (app_owner && app_first) App::load_row(A, kh, lane, app_row);
-  __builtin_amdgcn_sched_barrier(0);
-  int ch = split * P.chunks_per_split + wl;
-  if (ch < c_end) {
-    issue_k(ch);
-    issue_v(ch);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  if (app_owner && !app_first) App::load_row(A, kh, lane, app_row);
-  __builtin_amdgcn_sched_barrier(0);
-  if (app_share) {
-    App::wait_loads();
-    App::requant_share(A, wave, lane, app_knew, app_raw, s_kg);
-  }
-  float qv[GW][8];
-#pragma unroll
-  for (int g = 0; g < GW; ++g) {
-    // a head group's padding head (odd G) gets q = 0 and is never stored
-    const bool hv = g0 + g < G;
-    float x[8] = {qa[g].x, qa[g].y, qa[g].z, qa[g].w, qc[g].x, qc[g].y, qc[g].z, qc[g].w};
-    if (q_bias) {
-      const float b[8] = {qba[g].x, qba[g].y, qba[g].z, qba[g].w,
-                          qbc[g].x, qbc[g].y, qbc[g].z, qbc[g].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] += b[e];
-    }
-    if (q_rope) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) rope_pair(x[t], x[4 + t], qt[t]);
-    }
-    if constexpr (kRing) {
-      const float cv[4] = {cq[0].x, cq[0].z, cq[1].x, cq[1].z};
-      const float sv[4] = {cq[0].y, cq[0].w, cq[1].y, cq[1].w};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float u = x[t], w = x[4 + t];
-        // explicit fused forms: every instance rounds the same way
-        x[t] = fmaf(u, cv[t], -(w * sv[t]));
-        x[4 + t] = fmaf(w, cv[t], u * sv[t]);
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qv[g][e] = hv ? x[e] * P.qscale : 0.0f;
-  }
-  if constexpr (KIND == kI8Dense) {
-    if (r == 0) {
-#pragma unroll
-      for (int g = 0; g < GW; ++g) {
-        *reinterpret_cast<float4*>(&s_qw[wave][g][4 * c]) =
-            make_float4(qv[g][0], qv[g][1], qv[g][2], qv[g][3]);
-        *reinterpret_cast<float4*>(&s_qw[wave][g][HD / 2 + 4 * c]) =
-            make_float4(qv[g][4], qv[g][5], qv[g][6], qv[g][7]);
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
-
-  float M[GW], l[GW], o[GW][8];
-#pragma unroll
-  for (int g = 0; g < GW; ++g) {
-    M[g] = kMinit;
-    l[g] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
-  }
-
-  while (ch < c_end) {
-    const int nch = ch + WPG;
-    const int p0 = ch * CHUNK;
-
-    // ---- the appended row (fused step): take its new values from the stage
-    const bool app_now = ch == app_chunk;  // uniform
-    const int app_pc = A.slot - p0;        // its position inside the chunk
-    const int app_r = (app_pc & 15) % RPW, app_i = (app_pc & 15) / RPW, app_gs = app_pc >> 4;
-    if (app_now) {
-      App::wait_loads();
-      if (PROD && A.prod) App::produce_row(A, lane, app_row);
-      App::stage_row(A, lane, s_app, app_row);
-      if constexpr (kShare) App::await_shares(s_kg);
-      if constexpr (KIND == kI8Dense) {
-#pragma unroll
-        for (int gs = 0; gs < NGC; ++gs)
-#pragma unroll
-          for (int j = 0; j < NSG; j += 2) {
-            const uint4 t = s_kg.kchunk[(gs * kGranule * HD + j * 512) / 16 + lane];
-            kq[gs * NSG + j] = make_uint2(t.x, t.y);
-            kq[gs * NSG + j + 1] = make_uint2(t.z, t.w);
-          }
-        ksv[0] = *reinterpret_cast<const float4*>(&s_kg.ks[4 * c]);
-        ksv[1] = *reinterpret_cast<const float4*>(&s_kg.ks[HD / 2 + 4 * c]);
-      } else {
-        const bool mine = r == app_r;
-#pragma unroll
-        for (int gs = 0; gs < NGC; ++gs)
-#pragma unroll
-          for (int j = 0; j < NSG; ++j) {
-            const int sl = gs * NSG + j;
-            if (mine && gs == app_gs && (j ^ kx_slot) == app_i) {
-              if constexpr (kInt8) {
-                kq[sl] = make_uint2(s_app.k8row[c], s_app.k8row[HD / 8 + c]);
-                ksc[sl][0] = s_app.ks[(4 * c) / kBlock];
-                ksc[sl][1] = s_app.ks[(HD / 2 + 4 * c) / kBlock];
-              } else {
-                kf[sl][0] = *reinterpret_cast<const float4*>(&s_app.krow[4 * c]);
-                kf[sl][1] = *reinterpret_cast<const float4*>(&s_app.krow[HD / 2 + 4 * c]);
-              }
-            }
-          }
-      }
-    }
-
-    // ---- q for this chunk: dense int8 folds the group's channel scales in
-    float qt[GW][8];
-#pragma unroll
-    for (int g = 0; g < GW; ++g) {
-      if constexpr (KIND == kI8Dense) {
-        const float ks8[8] = {ksv[0].x, ksv[0].y, ksv[0].z, ksv[0].w,
-                              ksv[1].x, ksv[1].y, ksv[1].z, ksv[1].w};
-        const float4 qa4 = *reinterpret_cast<const float4*>(&s_qw[wave][g][4 * c]);
-        const float4 qb4 = *reinterpret_cast<const float4*>(&s_qw[wave][g][HD / 2 + 4 * c]);
-        const float q8[8] = {qa4.x, qa4.y, qa4.z, qa4.w, qb4.x, qb4.y, qb4.z, qb4.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qt[g][e] = q8[e] * ks8[e];
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qt[g][e] = qv[g][e];
-      }
-    }
-
-    // ---- QK: per granule, NSG slot partials -> one score per lane
-    float sc[NGC][GW];
-#pragma unroll
-    for (int gs = 0; gs < NGC; ++gs) {
-      float acc[GW][NSG];
-#pragma unroll
-      for (int j = 0; j < NSG; ++j) {
-        const int sl = gs * NSG + j;
-        float kx[8];
-        if constexpr (kInt8) {
-          cvt8(kq[sl], kx);
-          if constexpr (KIND == kI8Ring) {
-            // dequantize (code * block scale, model.cpp:689-690)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) kx[e] = ksc[sl][e >> 2] * kx[e];
-          }
-        } else {
-          kx[0] = kf[sl][0].x; kx[1] = kf[sl][0].y; kx[2] = kf[sl][0].z; kx[3] = kf[sl][0].w;
-          kx[4] = kf[sl][1].x; kx[5] = kf[sl][1].y; kx[6] = kf[sl][1].z; kx[7] = kf[sl][1].w;
-        }
-        if constexpr (kRing) {
-          const float cv[4] = {cs[sl][0].x, cs[sl][0].z, cs[sl][1].x, cs[sl][1].z};
-          const float sv[4] = {cs[sl][0].y, cs[sl][0].w, cs[sl][1].y, cs[sl][1].w};
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float a = kx[t], b = kx[4 + t];
-            kx[t] = fmaf(a, cv[t], -(b * sv[t]));
-            kx[4 + t] = fmaf(b, cv[t], a * sv[t]);
-          }
-        }
-#pragma unroll
-        for (int g = 0; g < GW; ++g) {
-          float a = qt[g][0] * kx[0];
-#pragma unroll
-          for (int e = 1; e < 8; ++e) a += qt[g][e] * kx[e];
-          acc[g][j] = a;
-        }
-      }
-      const int p = p0 + gs * kGranule + kx_slot * RPW + r;
-      const bool valid = p < nkeys && (KIND != kI8Dense || p >= P.n_sink);
-#pragma unroll
-      for (int g = 0; g < GW; ++g) {
-        const float s = treduce<HD>(acc[g]);
-        sc[gs][g] = valid ? s : -INFINITY;
-      }
-    }
-    // the scheduler must not hoist the next chunk's loads above the use of
-    // this chunk's registers (that doubles the live buffers)
-    __builtin_amdgcn_sched_barrier(0);
-    if (nch < c_end) issue_k(nch);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- online softmax with a wave-uniform running max
-#pragma unroll
-    for (int g = 0; g < GW; ++g) {
-      float mx = sc[0][g];
-#pragma unroll
-      for (int gs = 1; gs < NGC; ++gs) mx = fmaxf(mx, sc[gs][g]);
-      const float mn = fmaxf(M[g], wave_max(mx));
-      const float alpha = fast_exp2(M[g] - mn);
-      M[g] = mn;
-      float ls = l[g] * alpha;
-#pragma unroll
-      for (int gs = 0; gs < NGC; ++gs) {
-        const float w = fast_exp2(sc[gs][g] - mn);
-        sc[gs][g] = w;
-        ls += w;
-      }
-      l[g] = ls;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
-    }
-
-    // ---- weights to the PV mapping through this wave's LDS rows
-    if ((c & 3) == 0) {
-#pragma unroll
-      for (int gs = 0; gs < NGC; ++gs) {
-        float* wr = &s_w[wave][gs * kGranule + kx_slot * RPW + r][0];
-#pragma unroll
-        for (int gq = 0; gq < GP; gq += 4) {
-          float4 w4;
-          w4.x = gq + 0 < GW ? sc[gs][gq + 0 < GW ? gq + 0 : 0] : 0.0f;
-          w4.y = gq + 1 < GW ? sc[gs][gq + 1 < GW ? gq + 1 : 0] : 0.0f;
-          w4.z = gq + 2 < GW ? sc[gs][gq + 2 < GW ? gq + 2 : 0] : 0.0f;
-          w4.w = gq + 3 < GW ? sc[gs][gq + 3 < GW ? gq + 3 : 0] : 0.0f;
-          *reinterpret_cast<float4*>(wr + gq) = w4;
-        }
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    if (app_now && r == app_r) {
-#pragma unroll
-      for (int gs = 0; gs < NGC; ++gs)
-#pragma unroll
-        for (int i = 0; i < NSG; ++i) {
-          const int sl = gs * NSG + i;
-          if (gs == app_gs && i == app_i) {
-            if constexpr (kInt8) {
-              vq[sl] = make_uint2(s_app.v8row[2 * c], s_app.v8row[2 * c + 1]);
-              vsc[sl] = s_app.vs[(8 * c) / kBlock];
-            } else {
-              vf[sl][0] = *reinterpret_cast<const float4*>(&s_app.vrow[8 * c]);
-              vf[sl][1] = *reinterpret_cast<const float4*>(&s_app.vrow[8 * c + 4]);
-            }
-          }
-        }
-    }
-
-    // ---- PV: lane (row r, dims 8c..8c+7), slot i -> position i*RPW + r.
-    // Rows past the last key have weight 0; in the final partial chunk their
-    // (stale) V and scales are zeroed as well, so nothing non-finite enters.
-    const bool full = p0 + CHUNK <= nkeys;  // uniform
-#pragma unroll
-    for (int gs = 0; gs < NGC; ++gs)
-#pragma unroll
-      for (int i = 0; i < NSG; ++i) {
-        const int sl = gs * NSG + i;
-        const float* wr = &s_w[wave][gs * kGranule + i * RPW + r][0];
-        float wv[GP];
-#pragma unroll
-        for (int gq = 0; gq < GP; gq += 4) {
-          const float4 w4 = *reinterpret_cast<const float4*>(wr + gq);
-          wv[gq] = w4.x;
-          wv[gq + 1] = w4.y;
-          wv[gq + 2] = w4.z;
-          wv[gq + 3] = w4.w;
-        }
-        float vx[8];
-        float vsl = 0.0f;
-        if constexpr (kInt8) {
-          cvt8(vq[sl], vx);
-          vsl = vsc[sl];
-        } else {
-          vx[0] = vf[sl][0].x; vx[1] = vf[sl][0].y; vx[2] = vf[sl][0].z; vx[3] = vf[sl][0].w;
-          vx[4] = vf[sl][1].x; vx[5] = vf[sl][1].y; vx[6] = vf[sl][1].z; vx[7] = vf[sl][1].w;
-        }
-        if (!full) {
-          const bool ok = p0 + gs * kGranule + i * RPW + r < nkeys;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vx[e] = ok ? vx[e] : 0.0f;
-          vsl = ok ? vsl : 0.0f;
-        }
-        if constexpr (kInt8) {
-#pragma unroll
-          for (int g = 0; g < GW; ++g) wv[g] *= vsl;
-        }
-#pragma unroll
-        for (int g = 0; g < GW; ++g)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[g][e] += wv[g] * vx[e];
-      }
-    __builtin_amdgcn_sched_barrier(0);
-    if (nch < c_end) issue_v(nch);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_wave_barrier();
-    ch = nch;
-  }
-
-  // ---- wave epilogue: l over lanes, o over the RPW lane rows (transposing
-  // permlane swaps: lane ends with values K = k + 2GW * (lane / 16), k < 2GW)
-#pragma unroll
-  for (int g = 0; g < GW; ++g) l[g] = wave_sum(l[g]) * (1.0f / C::DUP);
-  float v1[4 * GW], v2[2 * GW];
-#pragma unroll
-  for (int k = 0; k < 4 * GW; ++k)
-    v1[k] = swap32_sum(o[k / 8][k % 8], o[(k + 4 * GW) / 8][(k + 4 * GW) % 8]);
-#pragma unroll
-  for (int k = 0; k < 2 * GW; ++k) v2[k] = swap16_sum(v1[k], v1[k + 2 * GW]);
-  if constexpr (HD == 64) {
-#pragma unroll
-    for (int k = 0; k < 2 * GW; ++k) v2[k] += dpp<kX8>(v2[k]);
-  }
-  if (HD == 128 || (lane & 8) == 0) {
-    const int q4 = lane >> 4;
-#pragma unroll
-    for (int k = 0; k < 2 * GW; ++k) {
-      const int K = k + 2 * GW * q4;
-      s_o[wave][K / 8][8 * c + K % 8] = v2[k];
-    }
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < GW; ++g) {
-      s_ml[wave][g][0] = M[g];
-      s_ml[wave][g][1] = l[g];
-    }
-  }
-  finish<HD, G, GW, WPG>(P, s_o, s_ml, s_f, s_M, s_L, split, kh, qrow);
-  if (!P.direct) {
-    // this thread's record stores have reached the coherence point
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      unsigned* cnt = P.cnt + (static_cast<size_t>(qrow) * P.nkv + kh) * kCounterStride;
-      const unsigned before =
-          __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = before == static_cast<unsigned>(P.nsplit - 1);
-      if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = last;
-    }
-    __syncthreads();
-    // (wave g merges head g; its scaled q row in s_qw, dense int8 only,
-    // belongs to the first wave of head g's group)
-    if (s_last)
-      merge_last<HD, G, PROD>(P, A, kh, qrow, wave, lane,
-                              &s_qw[KIND == kI8Dense ? (min(wave, G - 1) / GW) * WPG : 0]
-                                   [KIND == kI8Dense ? min(wave, G - 1) % GW : 0][0]);
-  }
-  if (app_owner && g0 == 0) App::flush(A, kh, lane, s_app, s_kg, app_row);
-}
-
-// ---------------------------------------------------------------------------
-// dispatch
-
-// PROD: the decode step from raw projections (bias and rope inside the
-// launch); a separate instance, so the plain path carries none of it
-template <int HD, int G, int KIND>
-void* kernel_for(bool prod) {
-  return prod ? reinterpret_cast<void*>(&attn_kernel<HD, G, KIND, true>)
-              : reinterpret_cast<void*>(&attn_kernel<HD, G, KIND, false>);
-}
-
-template <int HD, int KIND>
-void* pick_g(int G, bool prod) {
-  switch (G) {
-    case 1: return kernel_for<HD, 1, KIND>(prod);
-    case 2: return kernel_for<HD, 2, KIND>(prod);
-    case 3: return kernel_for<HD, 3, KIND>(prod);
-    case 4: return kernel_for<HD, 4, KIND>(prod);
-    case 5: return kernel_for<HD, 5, KIND>(prod);
-    case 6: return kernel_for<HD, 6, KIND>(prod);
-    case 7: return kernel_for<HD, 7, KIND>(prod);
-    case 8: return kernel_for<HD, 8, KIND>(prod);
+void* pick_kernel(int hd, int kind, int G, bool prod = false, int cpw = 1) {
+  switch (kind * 2 + (prod ? 1 : 0)) {
+    case 0: return attn_instance_0_0(hd, G, cpw);
+    case 1: return attn_instance_0_1(hd, G, cpw);
+    case 2: return attn_instance_1_0(hd, G, cpw);
+    case 3: return attn_instance_1_1(hd, G, cpw);
+    case 4: return attn_instance_2_0(hd, G, cpw);
+    case 5: return attn_instance_2_1(hd, G, cpw);
+    case 6: return attn_instance_3_0(hd, G, cpw);
+    case 7: return attn_instance_3_1(hd, G, cpw);
     default: return nullptr;
   }
 }
 
-template <int HD>
-void* pick_kind(int kind, int G, bool prod) {
-  switch (kind) {
-    case kF32Dense: return pick_g<HD, kF32Dense>(G, prod);
-    case kI8Dense: return pick_g<HD, kI8Dense>(G, prod);
-    case kF32Ring: return pick_g<HD, kF32Ring>(G, prod);
-    case kI8Ring: return pick_g<HD, kI8Ring>(G, prod);
-    default: return nullptr;
-  }
-}
-
-void* pick_kernel(int hd, int kind, int G, bool prod = false) {
-  if (hd == 64) return pick_kind<64>(kind, G, prod);
-  if (hd == 128) return pick_kind<128>(kind, G, prod);
-  return nullptr;
-}
 
 int kind_of(const KvGeom& g) { return (g.ring ? 2 : 0) + (g.int8 ? 1 : 0); }
 
@@ -1421,19 +26,13 @@ int kind_of(const KvGeom& g) { return (g.ring ? 2 : 0) + (g.int8 ? 1 : 0); }
 int chunk_of(const KvGeom& g) { return g.int8 && !g.ring ? 2 * kGranule : kGranule; }
 
 // Workgroups one launch aims for (split-K fan-out: one 8-wave workgroup per
-// CU); DBI_ATTN_TARGET_BLOCKS overrides it for tuning sweeps.
-int target_blocks() {
-  static const int v = [] {
-    const char* e = std::getenv("DBI_ATTN_TARGET_BLOCKS");
-    const int x = e ? std::atoi(e) : 0;
-    return x > 0 ? x : 256;
-  }();
-  return v;
-}
+// CU).
+constexpr int kTargetBlocks = 256;
 
 struct Plan {
   int nsplit, chunks_per_split;
-  bool merge;  // a merge launch follows (several splits, or fp32 sinks)
+  int cpw;     // kernel instance: chunks per wave (1, 2, 4; 0 = runtime loop)
+  bool merge;  // several splits: the last to finish merges them
 };
 
 Plan plan(const KvGeom& g, const AttnCall& c) {
@@ -1441,11 +40,10 @@ Plan plan(const KvGeom& g, const AttnCall& c) {
   const int chunk = chunk_of(g);
   const int nkeys_max = g.ring ? c.ring.n_res : c.pos0 + c.rows;
   const int nchunks = (nkeys_max + chunk - 1) / chunk;
-  const bool sinks = g.int8 && !g.ring && g.n_sink > 0;
   const int units = g.nkv * c.rows;
   // whole waves of workgroups only: a launch of target + a few would run a
   // second, nearly empty round on the CUs
-  int want = target_blocks() / units;
+  int want = kTargetBlocks / units;
   const int wpg = (G > 4 && (g.hd == 128 || (g.int8 && !g.ring))) ? kWaves / 2 : kWaves;
   const int max_by_chunks = (nchunks + wpg - 1) / wpg;  // >= one chunk per wave
   if (want > max_by_chunks) want = max_by_chunks;
@@ -1454,7 +52,9 @@ Plan plan(const KvGeom& g, const AttnCall& c) {
   Plan p;
   p.chunks_per_split = (nchunks + want - 1) / want;
   p.nsplit = (nchunks + p.chunks_per_split - 1) / p.chunks_per_split;
-  p.merge = p.nsplit > 1 || sinks;
+  p.merge = p.nsplit > 1;
+  const int per_wave = (p.chunks_per_split + wpg - 1) / wpg;
+  p.cpw = per_wave <= 1 ? 1 : per_wave <= 2 ? 2 : per_wave <= 4 ? 4 : 0;
   return p;
 }
 
@@ -1474,7 +74,7 @@ size_t attention_counters_need(const KvGeom& g, const AttnCall& c) {
 size_t attention_workspace_need(const KvGeom& g, const AttnCall& c) {
   const Plan p = plan(g, c);
   const int G = c.n_heads / g.nkv;
-  return p.merge ? static_cast<size_t>(c.rows) * g.nkv * p.nsplit * G * (g.hd + 2) : 0;
+  return p.merge ? static_cast<size_t>(c.rows) * g.nkv * record_region(p.nsplit, G, g.hd) : 0;
 }
 
 hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, const AttnCall& c,
@@ -1482,7 +82,8 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
   const int G = c.n_heads / g.nkv;
   const bool prod = c.rows == 1 && (c.q_bias != nullptr || c.k_bias != nullptr ||
                                     c.v_bias != nullptr || c.rope_row != nullptr);
-  void* fn = pick_kernel(g.hd, kind_of(g), G, prod);
+  const Plan pl = plan(g, c);
+  void* fn = pick_kernel(g.hd, kind_of(g), G, prod, pl.cpw);
   if (fn == nullptr || !g.tiled) return hipErrorNotSupported;
   AttnParams p{};
   const size_t layer_heads = static_cast<size_t>(c.layer) * g.nkv;
@@ -1521,7 +122,6 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
   p.ring_s = c.ring.s;
   p.ring_W = c.ring.W > 0 ? c.ring.W : 1;
   p.ring_base = c.ring.base;
-  const Plan pl = plan(g, c);
   p.nsplit = pl.nsplit;
   p.direct = pl.merge ? 0 : 1;
   p.chunks_per_split = pl.chunks_per_split;

@@ -1,0 +1,12 @@
+// Instances of attn_kernel for the f32 ring layout.
+#include "attn_kernel.hpp"
+
+namespace dbi {
+
+void* attn_instance_2_0(int hd, int G, int cpw) {
+  return hd == 64 ? pick_g<64, 2, false>(G, cpw)
+       : hd == 128 ? pick_g<128, 2, false>(G, cpw)
+                   : nullptr;
+}
+
+}  // namespace dbi

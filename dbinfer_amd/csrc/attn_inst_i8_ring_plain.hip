@@ -1,0 +1,12 @@
+// Instances of attn_kernel for the i8 ring layout.
+#include "attn_kernel.hpp"
+
+namespace dbi {
+
+void* attn_instance_3_0(int hd, int G, int cpw) {
+  return hd == 64 ? pick_g<64, 3, false>(G, cpw)
+       : hd == 128 ? pick_g<128, 3, false>(G, cpw)
+                   : nullptr;
+}
+
+}  // namespace dbi

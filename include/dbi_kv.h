@@ -155,9 +155,10 @@ dbi_status dbi_kv_decode_async(dbi_kv* kv, uint32_t layer, uint32_t pos, const f
  * harnesses that forbid hipMalloc. Same arguments, kernels and results; it
  * calls no allocating routine, ever. Its split records and arrival counters
  * live in a static per-GPU scratch array (2 MiB of records, 64 KiB of
- * counters), set up when the first handle on that GPU is created; a call
- * whose split plan needs more fails with DBI_ERR_UNSUPPORTED and leaves the
- * cache as it was. Every call on one GPU shares that array: calls that
+ * counters), set up when the first handle on that GPU is created. Every
+ * decode plan fits (at most 256 split records of at most 8 heads x 130
+ * floats); a call whose plan needed more would fail with DBI_ERR_UNSUPPORTED
+ * before any launch. Every call on one GPU shares that array: calls that
  * overlap on one GPU (other handles, other streams) race. */
 dbi_status dbi_kv_decode_noalloc_async(dbi_kv* kv, uint32_t layer, uint32_t pos,
                                        const float* k_dev, const float* v_dev, uint32_t n_heads,

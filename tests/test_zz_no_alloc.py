@@ -1,14 +1,14 @@
 """The allocation-free decode step (dbi_kv_decode_noalloc_async) against the
 fused step it mirrors (dbi_kv_decode_async), through the C-ABI on one GPU:
 identical output bits and identical stores on two calls in a row, the
-second smaller, over several split plans and layouts; the oracle checks the
-result to the attention tolerance; a call beyond the scratch is refused and
-leaves the cache as it was."""
+second smaller, over several split plans and layouts, and at the largest
+split plan a decode call can have; the oracle checks the result to the
+attention tolerance."""
 import numpy as np
 import pytest
 
 import pyoracle
-from dbinfer_amd.kv import F32, INT8, DbiError, HipKV
+from dbinfer_amd.kv import F32, INT8, HipKV
 from helpers import assert_close
 
 pytestmark = pytest.mark.gpu
@@ -78,19 +78,36 @@ def test_noalloc_decode_matches_decode_async(dtype, nh, nkv, hd, n_sink, window,
             kv.close()
 
 
-def test_noalloc_refuses_beyond_scratch():
-    """Dense int8 with sinks always merges; 512 kv heads x gqa 8 x 130 floats
-    of records exceed the 2 MiB scratch. The refusal comes before any launch."""
+def test_noalloc_largest_plan():
+    """The largest split plan a decode call can have: 4 kv heads x 64 splits
+    = 256 workgroups of gqa 8 at hd 128, 1.06 MB of split records, within the
+    scratch; bit-identical to dbi_kv_decode_async."""
     torch = pytest.importorskip("torch")
-    nkv, hd, nh = 512, 128, 4096
-    kv = HipKV(1, 64, nkv, hd, 4, 0, INT8, 1e4)
-    kd = torch.zeros(nkv * hd, device="cuda")
-    qd = torch.zeros(nh * hd, device="cuda")
-    out = torch.zeros(nh * hd, device="cuda")
+    nh, nkv, hd, ctx = 32, 4, 128, 8192
+    P, Q = nkv * hd, nh * hd
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    rng = np.random.default_rng(1600)
+    K = rng.standard_normal((ctx, P), dtype=np.float32)
+    V = rng.standard_normal((ctx, P), dtype=np.float32)
+    q = rng.standard_normal(Q, dtype=np.float32)
+    ref = HipKV(1, ctx, nkv, hd)
+    new = HipKV(1, ctx, nkv, hd)
+    for kv in (ref, new):
+        kv.append_n(0, 0, K[:-1], V[:-1])
+    assert new.splits(ctx - 1, 1, nh) == 64
+    Kd, Vd, qd = (torch.from_numpy(a).cuda() for a in (K, V, q))
+    outs = [torch.full((Q,), float("nan"), device="cuda") for _ in range(2)]
+    stream = torch.cuda.current_stream()
+    for kv in (ref, new):
+        kv.set_stream(stream.cuda_stream)
     torch.cuda.synchronize()
-    with pytest.raises(DbiError) as e:
-        kv.decode_noalloc_async(0, 0, kd.data_ptr(), kd.data_ptr(), nh, 0.088, qd.data_ptr(),
-                                out.data_ptr())
-    assert "scratch holds" in e.value.message
-    assert kv.n_seen == 0
-    kv.close()
+    pos = ctx - 1
+    ref.decode_async(0, pos, Kd[pos].data_ptr(), Vd[pos].data_ptr(), nh, scale, qd.data_ptr(),
+                     outs[0].data_ptr())
+    new.decode_noalloc_async(0, pos, Kd[pos].data_ptr(), Vd[pos].data_ptr(), nh, scale,
+                             qd.data_ptr(), outs[1].data_ptr())
+    torch.cuda.synchronize()
+    a, b = outs[1].cpu().numpy(), outs[0].cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for kv in (ref, new):
+        kv.close()
