@@ -1,12 +1,11 @@
-// Instances of attn_kernel for the i8 dense layout.
-#include "attn_kernel.hpp"
+// Kernel instances of the dense int8 layout, plain inputs (matrix-core
+// kernel of attn_mfma.hpp).
+#include "attn_mfma.hpp"
 
 namespace dbi {
 
 void* attn_instance_1_0(int hd, int G, int cpw) {
-  return hd == 64 ? pick_g<64, 1, false>(G, cpw)
-       : hd == 128 ? pick_g<128, 1, false>(G, cpw)
-                   : nullptr;
+  return hd == 64 ? pick_i8<64, false>(G, cpw) : hd == 128 ? pick_i8<128, false>(G, cpw) : nullptr;
 }
 
 }  // namespace dbi

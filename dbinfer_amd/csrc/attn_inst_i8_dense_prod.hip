@@ -1,12 +1,11 @@
-// Instances of attn_kernel for the i8 dense layout, raw-projection producer.
-#include "attn_kernel.hpp"
+// Kernel instances of the dense int8 layout, raw-projection inputs
+// (matrix-core kernel of attn_mfma.hpp).
+#include "attn_mfma.hpp"
 
 namespace dbi {
 
 void* attn_instance_1_1(int hd, int G, int cpw) {
-  return hd == 64 ? pick_g<64, 1, true>(G, cpw)
-       : hd == 128 ? pick_g<128, 1, true>(G, cpw)
-                   : nullptr;
+  return hd == 64 ? pick_i8<64, true>(G, cpw) : hd == 128 ? pick_i8<128, true>(G, cpw) : nullptr;
 }
 
 }  // namespace dbi

@@ -156,7 +156,6 @@ __device__ __forceinline__ float swap16_sum(float a, float b) {
   asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
   return a + b;
 }
-
 // Raw v_exp_f32 (2^x). Softmax weights below 2^-126 are far under the
 // output tolerance, so the denormal-range handling of exp2f is not needed.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -225,22 +224,21 @@ struct Cfg {
   static constexpr int LPR = HD / 8;            // lanes per position row
   static constexpr int RPW = 64 / LPR;          // rows per load instruction
   static constexpr int NSG = kGranule / RPW;    // slots per granule
-  // granules per chunk: 2 (32 positions, one int8 K group) for dense int8;
-  // fp32 rows and the ring's rope table need the registers of a second one
-  static constexpr int NGC = KIND == kI8Dense ? 2 : 1;
+  static constexpr int NGC = 1;                 // granules per chunk
   static constexpr int CHUNK = kGranule * NGC;
   static constexpr int NS = NSG * NGC;          // slots per chunk
   // wide groups split their heads over two halves of the workgroup (each
   // half streams the same chunks, the second read hitting L1/L2): a wave
   // then holds q and o of GW <= 4 heads, which keeps them in registers
-  static constexpr int NHG = (G > 4 && (HD == 128 || KIND == kI8Dense)) ? 2 : 1;
+  static constexpr int NHG = (G > 4 && HD == 128) ? 2 : 1;
   static constexpr int GW = (G + NHG - 1) / NHG;  // query heads per wave
   static constexpr int WPG = kWaves / NHG;        // waves per head group
   static constexpr int GP = GW <= 4 ? 4 : 8;      // padded heads of an LDS weight row
   static constexpr int DUP = LPR / NSG;         // lanes holding one position's score
   static constexpr int NB = HD / kBlock;
   static_assert(HD == 64 || HD == 128, "head dim");
-  static_assert(KIND != kI8Dense || CHUNK == kKGroup, "int8 chunk must be one K group");
+  // dense int8 runs on the matrix-core kernel (attn_mfma.hpp)
+  static_assert(KIND != kI8Dense, "dense int8: attn_i8_kernel");
 };
 
 // Reduces the NSG per-slot partial dots of a lane row to full scores, one
@@ -297,35 +295,38 @@ __host__ __device__ constexpr size_t record_region(int nsplit, int G, int HD) {
 
 // Cross-wave combine of (m, l, o) in LDS, then either the final output
 // (single split) or this split's partial record. Head g was handled by the
-// WPG waves of head group g / GW, at their local head index g % GW.
+// WPG waves of head group g / GW, at their local head index g % GW. Every
+// thread derives its head's combined max and wave factors itself from the
+// waves' (m, l) (broadcast LDS reads), so one barrier orders the whole step.
 template <int HD, int G, int GW, int WPG>
 __device__ __forceinline__ void finish(const AttnParams& P, float (&s_o)[kWaves][GW][HD],
-                                       float (&s_ml)[kWaves][GW][2], float (&s_f)[G][WPG],
-                                       float (&s_M)[G], float (&s_L)[G], int split, int kh,
+                                       float (&s_ml)[kWaves][GW][2], int split, int kh,
                                        int qrow) {
   __syncthreads();
-  if (static_cast<int>(threadIdx.x) < G) {
-    const int g = threadIdx.x, w0 = (g / GW) * WPG, gl = g % GW;
-    float M = kMinit;
-#pragma unroll
-    for (int i = 0; i < WPG; ++i) M = fmaxf(M, s_ml[w0 + i][gl][0]);
-    float L = 0.0f;
+  // head g: combined max M, weight f[i] of wave i, combined sum L
+  auto combine = [&](int g, float& M, float (&f)[WPG], float& L) {
+    const int w0 = (g / GW) * WPG, gl = g % GW;
+    float m[WPG], l[WPG];
 #pragma unroll
     for (int i = 0; i < WPG; ++i) {
-      const float f = fast_exp2(s_ml[w0 + i][gl][0] - M);
-      s_f[g][i] = f;
-      L += s_ml[w0 + i][gl][1] * f;
+      m[i] = s_ml[w0 + i][gl][0];
+      l[i] = s_ml[w0 + i][gl][1];
     }
-    s_M[g] = M;
-    s_L[g] = L;
-  }
-  __syncthreads();
-
-  auto o_of = [&](int g, int d) {
+    M = kMinit;
+#pragma unroll
+    for (int i = 0; i < WPG; ++i) M = fmaxf(M, m[i]);
+    L = 0.0f;
+#pragma unroll
+    for (int i = 0; i < WPG; ++i) {
+      f[i] = fast_exp2(m[i] - M);
+      L += l[i] * f[i];
+    }
+  };
+  auto o_of = [&](int g, int d, const float (&f)[WPG]) {
     const int w0 = (g / GW) * WPG, gl = g % GW;
     float O = 0.0f;
 #pragma unroll
-    for (int i = 0; i < WPG; ++i) O += s_o[w0 + i][gl][d] * s_f[g][i];
+    for (int i = 0; i < WPG; ++i) O += s_o[w0 + i][gl][d] * f[i];
     return O;
   };
   const size_t head_base = static_cast<size_t>(qrow) * P.nkv + kh;
@@ -333,7 +334,9 @@ __device__ __forceinline__ void finish(const AttnParams& P, float (&s_o)[kWaves]
     float* out_base = P.out + (static_cast<size_t>(qrow) * P.n_heads + kh * G) * HD;
     for (int idx = threadIdx.x; idx < G * HD; idx += kThreads) {
       const int g = idx / HD, d = idx % HD;
-      out_base[idx] = o_of(g, d) / s_L[g];
+      float M, f[WPG], L;
+      combine(g, M, f, L);
+      out_base[idx] = o_of(g, d, f) / L;
     }
     return;
   }
@@ -344,13 +347,15 @@ __device__ __forceinline__ void finish(const AttnParams& P, float (&s_o)[kWaves]
                 static_cast<size_t>(split) * record_floats(G, HD);
   float* mlrec = orec + G * HD;
   for (int idx = threadIdx.x; idx < G * HD + 2 * G; idx += kThreads) {
+    const int g = idx < G * HD ? idx / HD : (idx - G * HD) >> 1;
+    float M, f[WPG], L;
+    combine(g, M, f, L);
     if (idx < G * HD) {
-      __hip_atomic_store(orec + idx, o_of(idx / HD, idx % HD), __ATOMIC_RELAXED,
+      __hip_atomic_store(orec + idx, o_of(g, idx % HD, f), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     } else {
       const int r = idx - G * HD;  // (m, l) of head r / 2
-      __hip_atomic_store(mlrec + r, (r & 1) ? s_L[r >> 1] : s_M[r >> 1], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(mlrec + r, (r & 1) ? L : M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -442,7 +447,7 @@ struct AppStage {
 // Dense int8: the requantized 32-token group of the fused step, shared by
 // the head groups of the workgroup.
 struct KGroupStage {
-  uint4 kchunk[kKGroup * 128 / 16];  // the group's codes, granule layout
+  uint4 kchunk[kKGroup * 128 / 16];  // the group's codes, dense int8 layout
   float ks[128];                     // its channel scales
   unsigned done;                     // requantizing waves done (zeroed at launch)
 };
@@ -632,7 +637,7 @@ struct FusedAppend {
     const int d = wave * CPW + c;
 #pragma unroll
     for (int i = 0; i < RPL; ++i)
-      kc[k_off_tiled(HD, true, rb * RPL + i, d)] = static_cast<uint8_t>(quant_code(x[i], inv));
+      kc[k_off_i8d(HD, rb * RPL + i, d)] = static_cast<uint8_t>(quant_code(x[i], inv));
     if (lane < CPW) kg.ks[d] = sc;
     // publish (the release orders the stage writes before the count)
     if (lane == 0) __hip_atomic_fetch_add(&kg.done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -701,8 +706,9 @@ struct FusedAppend {
 
   // The stages to global memory in whole contiguous pieces, by one wave per
   // kv head, after its last load.
+  // (kg: the dense int8 group stage; null for the other layouts)
   __device__ __forceinline__ static void flush(const AppendArgs& A, int kh, int lane,
-                                               const AppStage& st, const KGroupStage& kg,
+                                               const AppStage& st, const KGroupStage* kg,
                                                const float* row) {
     const bool on = 2 * lane < HD;
     const int d = 2 * lane;
@@ -713,18 +719,18 @@ struct FusedAppend {
       const int pos = A.pos, grp = pos / kKGroup, within = pos % kKGroup, first = pos - within;
 #pragma unroll 4
       for (int m = 0; m < kKGroup * HD / 8 / 64; ++m) {  // one 8-byte piece per lane each
-        const int o = (m * 64 + lane) * 8, gs = o / (kGranule * HD), og = o % (kGranule * HD);
-        const int l = (og % 1024) / 16, j = 2 * (og / 1024) + (og % 16) / 8;
-        const int r = l / LPR, c = l % LPR;
-        const int w = gs * kGranule + (j ^ kslot_xor(HD, c)) * RPW + r;
+        // (a piece is 8 channels of one position: 1 KiB block o / 1024 of
+        // granule block / (hd / 64), position n of lane (o % 1024) / 16)
+        const int o = (m * 64 + lane) * 8;
+        const int w = kGranule * ((o / 1024) / (HD / 64)) + ((o % 1024) / 16) % 16;
         if (w <= within && first + w >= A.n_sink)  // later rows and sinks keep their memory
           *reinterpret_cast<uint2*>(A.k8 + hel + static_cast<size_t>(first) * HD + o) =
-              *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(kg.kchunk) + o);
+              *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(kg->kchunk) + o);
       }
       if (on) {
         const float2 kx = *reinterpret_cast<const float2*>(row + d);
         *reinterpret_cast<float2*>(A.ks + (static_cast<size_t>(kh) * A.ng + grp) * HD + d) =
-            *reinterpret_cast<const float2*>(&kg.ks[d]);
+            *reinterpret_cast<const float2*>(&kg->ks[d]);
         *reinterpret_cast<float2*>(A.k_raw + static_cast<size_t>(within) * A.nkv * HD + kh * HD +
                                    d) = kx;
         if (pos < A.n_sink) {
@@ -734,10 +740,11 @@ struct FusedAppend {
         }
       }
       if (pos >= A.n_sink) {
-        if (lane < LPR)  // V row: dims 8c..8c+7 of lane (rr, c)
-          *reinterpret_cast<uint2*>(A.v8 + hel +
-                                    granule_off(HD, true, pos, ii, rr * LPR + lane, 0)) =
-              make_uint2(st.v8row[2 * lane], st.v8row[2 * lane + 1]);
+        if (on) {  // V row: one byte per channel (channels d, d + 1 of this lane)
+          const uint8_t* v8s = reinterpret_cast<const uint8_t*>(st.v8row);
+          A.v8[hel + v_off_i8d(HD, pos, d)] = v8s[d];
+          A.v8[hel + v_off_i8d(HD, pos, d + 1)] = v8s[d + 1];
+        }
         if (lane < NB) A.vs[(static_cast<size_t>(kh) * A.capg + pos) * NB + lane] = st.vs[lane];
       }
     } else if constexpr (KIND == kI8Ring) {
@@ -779,12 +786,11 @@ struct ChunkBuf {
   static constexpr bool kInt8 = C::kInt8, kRing = C::kRing;
   uint2 kq[kInt8 ? NS : 1], vq[kInt8 ? NS : 1];
   float4 kf[kInt8 ? 1 : NS][2], vf[kInt8 ? 1 : NS][2];
-  float4 ksv[KIND == kI8Dense ? 2 : 1];    // dense int8 channel scales of the group
   float ksc[KIND == kI8Ring ? NS : 1][2];  // ring int8 K block scales
   float vsc[kInt8 ? NS : 1];               // int8 V block scales
   float4 cs[kRing ? NS : 1][2];            // ring rope cos/sin of the lane's 4 pairs
   // VGPRs the buffer holds
-  static constexpr int kVgprs = (kInt8 ? 4 * NS + NS : 16 * NS) + (KIND == kI8Dense ? 8 : 0) +
+  static constexpr int kVgprs = (kInt8 ? 4 * NS + NS : 16 * NS) +
                                 (KIND == kI8Ring ? 2 * NS : 0) + (kRing ? 8 * NS : 0);
 };
 
@@ -800,24 +806,15 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
 
   __shared__ float s_o[kWaves][GW][HD];
   __shared__ float s_ml[kWaves][GW][2];
-  __shared__ float s_f[G][WPG];
-  __shared__ float s_M[G];
-  __shared__ float s_L[G];
   __shared__ int s_last;
   __shared__ __align__(16) float s_w[kWaves][CHUNK][GP];
   __shared__ __align__(16) AppStage s_stage[C::NHG];
-  // dense int8 keeps each wave's scaled q in LDS, not registers, between
-  // chunks (it is re-scaled by every group's channel scales anyway)
-  __shared__ __align__(16) float s_qw[KIND == kI8Dense ? kWaves : 1][GW][HD];
   // dense int8 fused step: each head group's copy of the group's raw K rows
   // fused step inputs, per head group: the new K and V rows, and (dense
   // int8) the group's raw K rows
   // ([0, 256): K and V rows; raw projections: [256, 512) the (cos, sin)
   // row, [512, 768) the K and V biases)
   __shared__ __align__(16) float s_row[C::NHG][PROD ? 768 : 256];
-  __shared__ __align__(16) float s_raw[KIND == kI8Dense ? kWaves / 2 : 1][KIND == kI8Dense ? kKGroup * HD / (kWaves / 2) : 1];
-  __shared__ __align__(16) uint8_t s_kgbuf[KIND == kI8Dense ? sizeof(KGroupStage) : 16];
-  KGroupStage& s_kg = *reinterpret_cast<KGroupStage*>(s_kgbuf);
 
   const int lane = threadIdx.x & 63;
   // wave index as a provably uniform value: buffer-load SGPR offsets derive
@@ -864,8 +861,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
                                     : static_cast<const void*>(P.vf + head_el), kv_bytes);
   // (arrays a layout lacks get an empty resource: every read returns 0)
   const rsrc_t rks =
-      KIND == kI8Dense ? make_rsrc(P.ks + static_cast<size_t>(kh) * P.ng * HD, P.ng * HD * 4)
-      : KIND == kI8Ring ? make_rsrc(P.ks + head * NB, P.capg * NB * 4)
+      KIND == kI8Ring ? make_rsrc(P.ks + head * NB, P.capg * NB * 4)
                         : make_rsrc(P.q, 0);
   const rsrc_t rvs = kInt8 ? make_rsrc(P.vs + head * NB, P.capg * NB * 4) : make_rsrc(P.q, 0);
   const int cs_bytes = P.rope_rows * (HD / 2) * 8;
@@ -917,11 +913,6 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
           }
         }
       }
-    if constexpr (KIND == kI8Dense) {
-      const int so = (p0 / kKGroup) * HD * 4;
-      b.ksv[0] = load_b128(rks, 16 * c, so);
-      b.ksv[1] = load_b128(rks, 16 * c + HD * 2, so);
-    }
 #pragma unroll
     for (int gs = 0; gs < NGC; ++gs)
 #pragma unroll
@@ -987,27 +978,15 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
   // inputs load ahead of the owner's first chunk when that chunk is the new
   // row's, else right behind it (vector loads return in order, so they then
   // hold back nothing before that chunk), and are staged on reaching the
-  // chunk. Dense int8: waves [0, RW) requantize the row's group before their
-  // own chunk and count themselves done in LDS (zeroed here first).
+  // chunk.
   AppStage& s_app = s_stage[wave / WPG];
   const int app_rel = app_chunk - split * P.chunks_per_split;
   const bool app_owner = app_here && wl == app_rel % WPG;  // wave-uniform
   using App = FusedAppend<HD, KIND, PROD>;
   float* app_row = s_row[wave / WPG];
-  constexpr bool kShare = KIND == kI8Dense;
-  const bool app_share = kShare && app_here && wave < App::RW;  // wave-uniform
-  float* app_raw = s_raw[kShare && wave < App::RW ? wave : 0];
-  if constexpr (kShare) {
-    if (app_here) {  // workgroup-uniform
-      if (threadIdx.x == 0) s_kg.done = 0;
-      __syncthreads();
-    }
-  }
   // (loaded ahead of the chunks, the oldest loads in flight: a register
   // reused later never waits on them longer than on the chunk loads)
-  typename App::ShareIn app_knew{};
   typename App::RowIn app_in{};
-  if (app_share) App::load_share(A, kh, wave, lane, app_knew);
   if (app_owner) App::load_row(A, kh, lane, app_in);
   __builtin_amdgcn_sched_barrier(0);
   const int ch0 = split * P.chunks_per_split + wl;  // chunk t of this wave: ch0 + t * WPG
@@ -1016,8 +995,6 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (NBUF == 2 && CPW != 1) issue(RB, ch0 + WPG);
   __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_sched_barrier(0);
-  if (app_share) App::requant_share(A, wave, lane, app_knew, app_raw, s_kg);
   float qv[GW][8];
 #pragma unroll
   for (int g = 0; g < GW; ++g) {
@@ -1048,20 +1025,6 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
 #pragma unroll
     for (int e = 0; e < 8; ++e) qv[g][e] = hv ? x[e] * P.qscale : 0.0f;
   }
-  if constexpr (KIND == kI8Dense) {
-    if (r == 0) {
-#pragma unroll
-      for (int g = 0; g < GW; ++g) {
-        *reinterpret_cast<float4*>(&s_qw[wave][g][4 * c]) =
-            make_float4(qv[g][0], qv[g][1], qv[g][2], qv[g][3]);
-        *reinterpret_cast<float4*>(&s_qw[wave][g][HD / 2 + 4 * c]) =
-            make_float4(qv[g][4], qv[g][5], qv[g][6], qv[g][7]);
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
 
   float M[GW], l[GW], o[GW][8];
 #pragma unroll
@@ -1083,19 +1046,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
       App::put_row(A, app_in, lane, app_row);
       if (PROD && A.prod) App::produce_row(A, lane, app_row);
       App::stage_row(A, lane, s_app, app_row);
-      if constexpr (kShare) App::await_shares(s_kg);
-      if constexpr (KIND == kI8Dense) {
-#pragma unroll
-        for (int gs = 0; gs < NGC; ++gs)
-#pragma unroll
-          for (int j = 0; j < NSG; j += 2) {
-            const uint4 t = s_kg.kchunk[(gs * kGranule * HD + j * 512) / 16 + lane];
-            b.kq[gs * NSG + j] = make_uint2(t.x, t.y);
-            b.kq[gs * NSG + j + 1] = make_uint2(t.z, t.w);
-          }
-        b.ksv[0] = *reinterpret_cast<const float4*>(&s_kg.ks[4 * c]);
-        b.ksv[1] = *reinterpret_cast<const float4*>(&s_kg.ks[HD / 2 + 4 * c]);
-      } else {
+      {
         const bool mine = r == app_r;
 #pragma unroll
         for (int gs = 0; gs < NGC; ++gs)
@@ -1116,23 +1067,12 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
       }
     }
 
-    // ---- q for this chunk: dense int8 folds the group's channel scales in
+    // ---- q for this chunk
     float qt[GW][8];
 #pragma unroll
-    for (int g = 0; g < GW; ++g) {
-      if constexpr (KIND == kI8Dense) {
-        const float ks8[8] = {b.ksv[0].x, b.ksv[0].y, b.ksv[0].z, b.ksv[0].w,
-                              b.ksv[1].x, b.ksv[1].y, b.ksv[1].z, b.ksv[1].w};
-        const float4 qa4 = *reinterpret_cast<const float4*>(&s_qw[wave][g][4 * c]);
-        const float4 qb4 = *reinterpret_cast<const float4*>(&s_qw[wave][g][HD / 2 + 4 * c]);
-        const float q8[8] = {qa4.x, qa4.y, qa4.z, qa4.w, qb4.x, qb4.y, qb4.z, qb4.w};
+    for (int g = 0; g < GW; ++g)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qt[g][e] = q8[e] * ks8[e];
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qt[g][e] = qv[g][e];
-      }
-    }
+      for (int e = 0; e < 8; ++e) qt[g][e] = qv[g][e];
 
     // ---- QK: per granule, NSG slot partials -> one score per lane
     float sc[NGC][GW];
@@ -1173,7 +1113,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
         }
       }
       const int p = p0 + gs * kGranule + kx_slot * RPW + r;
-      const bool valid = p < nkeys && (KIND != kI8Dense || p >= P.n_sink);
+      const bool valid = p < nkeys;
 #pragma unroll
       for (int g = 0; g < GW; ++g) {
         const float s = treduce<HD>(acc[g]);
@@ -1317,135 +1257,6 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
   }
 
 
-  // ---- the fp32 sinks of the dense int8 layout (positions < n_sink, keys
-  // and values from the fp32 sink arrays, model.cpp:612-626), attended by
-  // the wave that holds chunk 0 (where the int8 stream masks them) as
-  // further 16-position blocks. A fused step's own sink row is flushed last:
-  // that row comes from the step's inputs (produced, for raw projections).
-  if constexpr (KIND == kI8Dense) {
-    const int ns = min(P.n_sink, nkeys);
-    if (split == 0 && wl == 0 && ns > 0) {  // wave-uniform
-      const float* ksb = P.ksink + static_cast<size_t>(kh) * P.n_sink * HD;
-      const float* vsb = P.vsink + static_cast<size_t>(kh) * P.n_sink * HD;
-      const bool fresh_sink = A.slot >= 0 && A.pos < P.n_sink;
-      const float* kin = fresh_sink ? A.k + kh * HD : nullptr;
-      const float* vin = fresh_sink ? A.v + kh * HD : nullptr;
-      for (int sb = 0; sb < ns; sb += kGranule) {
-        float4 kf2[NSG][2], vf2[NSG][2];
-#pragma unroll
-        for (int j = 0; j < NSG; ++j) {
-          const int p = sb + (j ^ kx_slot) * RPW + r;
-          const bool fresh = fresh_sink && p == A.pos;
-          const float* src = fresh ? kin : ksb + min(p, ns - 1) * HD;
-          kf2[j][0] = *reinterpret_cast<const float4*>(src + 4 * c);
-          kf2[j][1] = *reinterpret_cast<const float4*>(src + HD / 2 + 4 * c);
-          if constexpr (PROD) {
-            if (fresh && A.prod) {
-              const float* kb = A.kb != nullptr ? A.kb + kh * HD : nullptr;
-              float* k8 = &kf2[j][0].x;
-              float* k8b = &kf2[j][1].x;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                k8[e] = produced<HD>(kin, kb, A.kcs, 4 * c + e);
-                k8b[e] = produced<HD>(kin, kb, A.kcs, HD / 2 + 4 * c + e);
-              }
-            }
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < NSG; ++i) {
-          const int p = sb + i * RPW + r;
-          const bool fresh = fresh_sink && p == A.pos;
-          const float* src = fresh ? vin : vsb + min(p, ns - 1) * HD;
-          vf2[i][0] = *reinterpret_cast<const float4*>(src + 8 * c);
-          vf2[i][1] = *reinterpret_cast<const float4*>(src + 8 * c + 4);
-          if constexpr (PROD) {
-            if (fresh && A.prod) {
-              const float* vb = A.vb != nullptr ? A.vb + kh * HD : nullptr;
-              float* v8 = &vf2[i][0].x;
-              float* v8b = &vf2[i][1].x;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                v8[e] = produced<HD>(vin, vb, nullptr, 8 * c + e);
-                v8b[e] = produced<HD>(vin, vb, nullptr, 8 * c + 4 + e);
-              }
-            }
-          }
-        }
-        float sc[GW];
-        {
-          float acc[GW][NSG];
-#pragma unroll
-          for (int j = 0; j < NSG; ++j) {
-            const float kx[8] = {kf2[j][0].x, kf2[j][0].y, kf2[j][0].z, kf2[j][0].w,
-                                 kf2[j][1].x, kf2[j][1].y, kf2[j][1].z, kf2[j][1].w};
-#pragma unroll
-            for (int g = 0; g < GW; ++g) {
-              const float4 qa4 = *reinterpret_cast<const float4*>(&s_qw[wave][g][4 * c]);
-              const float4 qb4 = *reinterpret_cast<const float4*>(&s_qw[wave][g][HD / 2 + 4 * c]);
-              const float q8[8] = {qa4.x, qa4.y, qa4.z, qa4.w, qb4.x, qb4.y, qb4.z, qb4.w};
-              float a = q8[0] * kx[0];
-#pragma unroll
-              for (int e = 1; e < 8; ++e) a += q8[e] * kx[e];
-              acc[g][j] = a;
-            }
-          }
-          const bool valid = sb + kx_slot * RPW + r < ns;
-#pragma unroll
-          for (int g = 0; g < GW; ++g) {
-            const float t = treduce<HD>(acc[g]);
-            sc[g] = valid ? t : -INFINITY;
-          }
-        }
-#pragma unroll
-        for (int g = 0; g < GW; ++g) {
-          const float mn = fmaxf(M[g], wave_max(sc[g]));
-          const float alpha = fast_exp2(M[g] - mn);
-          M[g] = mn;
-          sc[g] = fast_exp2(sc[g] - mn);
-          l[g] = l[g] * alpha + sc[g];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
-        }
-        if ((c & 3) == 0) {
-          float* wr = &s_w[wave][kx_slot * RPW + r][0];
-#pragma unroll
-          for (int gq = 0; gq < GP; gq += 4) {
-            float4 w4;
-            w4.x = gq + 0 < GW ? sc[gq + 0 < GW ? gq + 0 : 0] : 0.0f;
-            w4.y = gq + 1 < GW ? sc[gq + 1 < GW ? gq + 1 : 0] : 0.0f;
-            w4.z = gq + 2 < GW ? sc[gq + 2 < GW ? gq + 2 : 0] : 0.0f;
-            w4.w = gq + 3 < GW ? sc[gq + 3 < GW ? gq + 3 : 0] : 0.0f;
-            *reinterpret_cast<float4*>(wr + gq) = w4;
-          }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int i = 0; i < NSG; ++i) {
-          const float* wr = &s_w[wave][i * RPW + r][0];
-          float wv[GP];
-#pragma unroll
-          for (int gq = 0; gq < GP; gq += 4) {
-            const float4 w4 = *reinterpret_cast<const float4*>(wr + gq);
-            wv[gq] = w4.x;
-            wv[gq + 1] = w4.y;
-            wv[gq + 2] = w4.z;
-            wv[gq + 3] = w4.w;
-          }
-          const float vx[8] = {vf2[i][0].x, vf2[i][0].y, vf2[i][0].z, vf2[i][0].w,
-                               vf2[i][1].x, vf2[i][1].y, vf2[i][1].z, vf2[i][1].w};
-#pragma unroll
-          for (int g = 0; g < GW; ++g)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[g][e] += wv[g] * vx[e];
-        }
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
-  }
-
   // ---- wave epilogue: l over lanes, o over the RPW lane rows (transposing
   // permlane swaps: lane ends with values K = k + 2GW * (lane / 16), k < 2GW)
 #pragma unroll
@@ -1475,7 +1286,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
       s_ml[wave][g][1] = l[g];
     }
   }
-  finish<HD, G, GW, WPG>(P, s_o, s_ml, s_f, s_M, s_L, split, kh, qrow);
+  finish<HD, G, GW, WPG>(P, s_o, s_ml, split, kh, qrow);
   if (!P.direct) {
     // this thread's record stores have reached the coherence point
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1489,11 +1300,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
       s_last = last;
     }
     __syncthreads();
-    // (wave g merges head g; its scaled q row in s_qw, dense int8 only,
-    // belongs to the first wave of head g's group)
+    // (wave g merges head g)
     if (s_last) merge_last<HD, G>(P, kh, qrow, wave, lane);
   }
-  if (app_owner && g0 == 0) App::flush(A, kh, lane, s_app, s_kg, app_row);
+  if (app_owner && g0 == 0) App::flush(A, kh, lane, s_app, nullptr, app_row);
 }
 
 }  // namespace

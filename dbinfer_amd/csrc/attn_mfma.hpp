@@ -1,0 +1,582 @@
+// Dense int8 GQA attention on the matrix cores (attend_dense_int8,
+// model.cpp:600-661; the causal chunk rows of decode_layer_chunk,
+// model.cpp:956-981), instantiated by attn_inst_i8_dense_*.hip.
+//
+// Design (CDNA4, wave64, v_mfma_f32_16x16x32_bf16):
+//  - Grid and split plan as attn_kernel: (split, kv head, query row), 8 waves
+//    per workgroup, 32-position chunks (one K group each), chunk t -> wave
+//    t % 8; every query head of the kv head is served from the same bytes.
+//  - Exact bf16 products: int8 codes are exact in bf16, and an fp32 value is
+//    exactly hi + mid + lo of three bf16 parts (split3), so each score is the
+//    fp32 accumulation of exact products q~_i * k8_i, q~ = (q * scale * log2 e)
+//    * ks (the reference's (q_i * ks_i) * k8_i, per K group), and each output
+//    the fp32 accumulation of exact (p * vs) * v8 products.
+//  - QK^T: A = the chunk's K codes (rows: positions, read straight from the
+//    layout of kv_internal.hpp), B = q~ in three parts (columns: (query,
+//    V block) pairs, each query repeated once per 32-channel V block), built
+//    per chunk by the whole wave (8 values per lane) and read back from LDS.
+//  - Softmax on the scores as they leave the matrix core: lane n + 16g holds
+//    column n at positions 16h + 4g + i, so a column's max and sum are lane-
+//    local plus two permlane swaps, and the weight of (query, block) at those
+//    positions is exactly the PV A operand of that lane (row = column): the
+//    V layout stores each lane's 8 positions in that order. No LDS transpose.
+//  - PV: A = weight * V block scale in three bf16 parts, B = the V codes of a
+//    16-channel tile; row (query, block) is kept for the tiles of its block.
+//  - Records, merge, fused append and the fp32 sinks as attn_kernel.
+#pragma once
+
+#include "attn_kernel.hpp"
+
+namespace dbi {
+namespace {
+
+using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
+using f32x4 = float __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ __forceinline__ float ffrom(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// the upper halves (bf16) of two fp32 bit patterns, a in the low half
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// 8 signed int8 codes (bytes of lo, then hi) -> 8 bf16, exactly (|code| <=
+// 127 leaves the low 16 bits of its fp32 value zero)
+__device__ __forceinline__ bf16x8 codes_bf16(uint32_t lo, uint32_t hi) {
+  float f[8];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) f[b] = static_cast<float>(static_cast<int8_t>(lo >> (8 * b)));
+#pragma unroll
+  for (int b = 0; b < 4; ++b) f[4 + b] = static_cast<float>(static_cast<int8_t>(hi >> (8 * b)));
+  uint4 w;
+  w.x = pack_hi(fbits(f[0]), fbits(f[1]));
+  w.y = pack_hi(fbits(f[2]), fbits(f[3]));
+  w.z = pack_hi(fbits(f[4]), fbits(f[5]));
+  w.w = pack_hi(fbits(f[6]), fbits(f[7]));
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+// x = hi + mid + lo exactly, each part a bf16 (truncations: the residual of
+// an 8-bit truncation of a 24-bit significand keeps at most 16 bits, that of
+// the second at most 8); parts packed 8 per uint4
+__device__ __forceinline__ void split3(const float (&x)[8], uint4 (&part)[3]) {
+  uint32_t h[8], m[8], l[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    h[e] = fbits(x[e]) & 0xFFFF0000u;
+    const float r1 = x[e] - ffrom(h[e]);
+    m[e] = fbits(r1) & 0xFFFF0000u;
+    l[e] = fbits(r1 - ffrom(m[e]));
+  }
+  part[0] = make_uint4(pack_hi(h[0], h[1]), pack_hi(h[2], h[3]), pack_hi(h[4], h[5]),
+                       pack_hi(h[6], h[7]));
+  part[1] = make_uint4(pack_hi(m[0], m[1]), pack_hi(m[2], m[3]), pack_hi(m[4], m[5]),
+                       pack_hi(m[6], m[7]));
+  part[2] = make_uint4(pack_hi(l[0], l[1]), pack_hi(l[2], l[3]), pack_hi(l[4], l[5]),
+                       pack_hi(l[6], l[7]));
+}
+
+__device__ __forceinline__ f32x4 mfma(const uint4& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma(const bf16x8& a, const uint4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// max / sum of a lane's value over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four
+// 16-lane rows of one matrix column)
+__device__ __forceinline__ float col_max(float a) {
+  float b = a;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  a = fmaxf(a, b);
+  b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float col_sum(float a) {
+  a = swap16_sum(a, a);
+  return swap32_sum(a, a);
+}
+
+template <int HD, int G>
+struct MCfg {
+  static constexpr int NBK = HD / kBlock;      // V blocks per head
+  static constexpr int QVT = 16 / NBK;         // query vectors per 16-column tile
+  static constexpr int NT = (G + QVT - 1) / QVT;  // column tiles
+  static constexpr int LPQ = HD / 8;           // lanes per query in the q~ layout
+  static constexpr int NJ = HD / 32;           // QK k-steps (32 channels)
+  static constexpr int KL = HD / 64;           // K loads per granule (two k-steps each)
+  static constexpr int NTV = HD / 16;          // PV channel tiles
+  static constexpr int VL = HD / 32;           // V loads per chunk (two tiles each)
+  static constexpr int QROW = HD / 8 + 4;      // uint4 per q~ row in LDS (64-byte pad: no
+                                               // bank conflicts between the 4 x 4 lane groups)
+  static_assert(HD == 64 || HD == 128, "head dim");
+  static_assert(QVT * LPQ == 64, "one q~ tile per wave pass");
+};
+
+// One chunk's loads.
+template <int HD, int G>
+struct MBuf {
+  using C = MCfg<HD, G>;
+  uint4 k[2][C::KL];  // K: granule h, load jp
+  float4 ks[2];       // the K group's channel scales of this lane's 8 q~ channels
+  uint4 v[C::VL];     // V: load tp
+  float vs[8];        // V block scale of slot s (position 16(s/4) + 4g + s%4, block col % NBK)
+};
+
+template <int HD, int G, bool PROD, int CPW>
+__global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, const AppendArgs A) {
+  using C = MCfg<HD, G>;
+  constexpr int NBK = C::NBK, QVT = C::QVT, NT = C::NT, LPQ = C::LPQ, NJ = C::NJ;
+  constexpr int KL = C::KL, NTV = C::NTV, VL = C::VL, QROW = C::QROW;
+  constexpr int CHUNK = kKGroup;
+  constexpr int NB = NBK;
+
+  __shared__ float s_o[kWaves][G][HD];
+  __shared__ float s_ml[kWaves][G][2];
+  __shared__ int s_last;
+  __shared__ __align__(16) uint4 s_qt[kWaves][NT][3][QVT][QROW];
+  // fused step stages (the single head group's)
+  __shared__ __align__(16) AppStage s_stage;
+  __shared__ __align__(16) float s_row[PROD ? 768 : 256];
+  __shared__ __align__(16) float s_raw[kWaves / 2][kKGroup * HD / (kWaves / 2)];
+  __shared__ __align__(16) uint8_t s_kgbuf[sizeof(KGroupStage)];
+  KGroupStage& s_kg = *reinterpret_cast<KGroupStage*>(s_kgbuf);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;    // matrix column / row group of this lane
+  const int qvl = lane / LPQ, c8 = lane % LPQ;   // q~ layout: query qvl, channels 8*c8..
+  const int split = blockIdx.x;
+  const int kh = blockIdx.y;
+  const int qrow = blockIdx.z;
+  const int nkeys = P.pos0 + qrow + 1;
+  const int nchunks = (nkeys + CHUNK - 1) / CHUNK;
+  const int c_end = min((split + 1) * P.chunks_per_split, nchunks);
+  const size_t head = static_cast<size_t>(kh) * P.capg;
+  const size_t head_el = head * HD;
+  const int app_chunk = A.slot >= 0 ? A.slot / CHUNK : -1;
+  const bool app_here = app_chunk >= split * P.chunks_per_split && app_chunk < c_end;
+
+  const int kv_bytes = P.capg * HD;
+  const rsrc_t rk = make_rsrc(P.k8 + head_el, kv_bytes);
+  const rsrc_t rv = make_rsrc(P.v8 + head_el, kv_bytes);
+  const rsrc_t rks = make_rsrc(P.ks + static_cast<size_t>(kh) * P.ng * HD, P.ng * HD * 4);
+  const rsrc_t rvs = make_rsrc(P.vs + head * NB, P.capg * NB * 4);
+
+  using Buf = MBuf<HD, G>;
+  // one chunk buffer: fewer registers, and measured no slower than two (the
+  // next chunk's loads wait for the current chunk's math either way)
+  constexpr int NBUF = 1;
+
+  // Every chunk issues the same loads, so the load waits are exact; a chunk
+  // past c_end reads from p0 = capg, past the end of every array (reads
+  // return 0). The group a fused step requantizes is read as well and
+  // replaced from LDS.
+  auto issue = [&](Buf& b, int ch) {
+    const bool live = ch < c_end;
+    const int p0 = __builtin_amdgcn_readfirstlane(live ? ch * CHUNK : P.capg);
+    const int base = p0 * HD;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int jp = 0; jp < KL; ++jp)
+        b.k[h][jp] = __builtin_bit_cast(uint4, stream_b128(rk, lane * 16, base + (h * KL + jp) * 1024));
+    const int so = (p0 / kKGroup) * HD * 4;
+    b.ks[0] = load_b128(rks, 32 * c8, so);
+    b.ks[1] = load_b128(rks, 32 * c8 + 16, so);
+#pragma unroll
+    for (int tp = 0; tp < VL; ++tp)
+      b.v[tp] = __builtin_bit_cast(uint4, stream_b128(rv, lane * 16, base + tp * 1024));
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      b.vs[s] = load_b32(rvs, ((16 * (s / 4) + 4 * grp + s % 4) * NB + col % NBK) * 4, p0 * NB * 4);
+  };
+
+  // ---- q * scale * log2(e) of this lane's 8 channels of query T*QVT + qvl
+  // (raw projections: bias, then the fp64 rope, as the producer computes
+  // each element; padding queries >= G are 0)
+  float qs[NT][8];
+  const float* qbase = P.q + (static_cast<size_t>(qrow) * P.n_heads + kh * G) * HD;
+  const bool q_prod = PROD && (P.qb != nullptr || P.qcs != nullptr);
+  auto load_q = [&]() {
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const int qv = T * QVT + qvl;
+      const float* qg = qbase + min(qv, G - 1) * HD;
+      if (q_prod) {
+        const float* bg = P.qb != nullptr ? P.qb + (kh * G + min(qv, G - 1)) * HD : nullptr;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qs[T][e] = produced<HD>(qg, bg, P.qcs, 8 * c8 + e);
+      } else {
+        const float4 a = *reinterpret_cast<const float4*>(qg + 8 * c8);
+        const float4 b = *reinterpret_cast<const float4*>(qg + 8 * c8 + 4);
+        qs[T][0] = a.x; qs[T][1] = a.y; qs[T][2] = a.z; qs[T][3] = a.w;
+        qs[T][4] = b.x; qs[T][5] = b.y; qs[T][6] = b.z; qs[T][7] = b.w;
+      }
+    }
+  };
+
+  // ---- fused decode step (FusedAppend, one head group): the owner wave
+  // stages the new row; waves [0, RW) requantize its K group before their
+  // own chunk and publish it through an LDS count
+  using App = FusedAppend<HD, kI8Dense, PROD>;
+  const int app_rel = app_chunk - split * P.chunks_per_split;
+  const bool app_owner = app_here && wave == app_rel % kWaves;  // wave-uniform
+  const bool app_share = app_here && wave < App::RW;
+  float* app_raw = s_raw[wave < App::RW ? wave : 0];
+  if (app_here) {  // workgroup-uniform
+    if (threadIdx.x == 0) s_kg.done = 0;
+    __syncthreads();
+  }
+  load_q();
+  typename App::ShareIn app_knew{};
+  typename App::RowIn app_in{};
+  if (app_share) App::load_share(A, kh, wave, lane, app_knew);
+  if (app_owner) App::load_row(A, kh, lane, app_in);
+  __builtin_amdgcn_sched_barrier(0);
+  const int ch0 = split * P.chunks_per_split + wave;  // chunk t of this wave: ch0 + t * 8
+  Buf RA, RB;
+  issue(RA, ch0);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (NBUF == 2 && CPW != 1) issue(RB, ch0 + kWaves);
+  __builtin_amdgcn_sched_barrier(0);
+  if (app_share) App::requant_share(A, wave, lane, app_knew, app_raw, s_kg);
+#pragma unroll
+  for (int T = 0; T < NT; ++T)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qs[T][e] = T * QVT + qvl < G ? qs[T][e] * P.qscale : 0.0f;
+
+  // running state: per column tile, the max and the lane's partial sum of its
+  // column's query (QK^T layout), and the PV accumulators (row (query,
+  // block), column = channel of tile t)
+  float M[NT], l[NT];
+  f32x4 o[NT][NTV];
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    M[T] = kMinit;
+    l[T] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NTV; ++t) o[T][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  auto compute = [&](Buf& b, const int ch, const bool first) {
+    // products feeding split3 are rounded to fp32 first (q * ks, as the
+    // reference rounds it; p * vs): no contraction into the split's subtraction
+#pragma clang fp contract(off)
+    const int p0 = ch * CHUNK;
+
+    // ---- the fused step's chunk: its K group and the new V row from LDS
+    if (ch == app_chunk) {  // uniform
+      App::put_row(A, app_in, lane, s_row);
+      if (PROD && A.prod) App::produce_row(A, lane, s_row);
+      App::stage_row(A, lane, s_stage, s_row);
+      App::await_shares(s_kg);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int jp = 0; jp < KL; ++jp) b.k[h][jp] = s_kg.kchunk[(h * KL + jp) * 64 + lane];
+      b.ks[0] = *reinterpret_cast<const float4*>(&s_kg.ks[8 * c8]);
+      b.ks[1] = *reinterpret_cast<const float4*>(&s_kg.ks[8 * c8 + 4]);
+      const int pc = A.slot - p0;  // the row's position in the chunk
+      const int sg = (pc & 15) >> 2, ss = 4 * (pc >> 4) + (pc & 3);
+      if (grp == sg && A.pos >= A.n_sink) {  // (a sink row is masked in the stream)
+        const uint8_t* v8s = reinterpret_cast<const uint8_t*>(s_stage.v8row);
+#pragma unroll
+        for (int tp = 0; tp < VL; ++tp) {
+          uint32_t w[4] = {b.v[tp].x, b.v[tp].y, b.v[tp].z, b.v[tp].w};
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            const uint32_t code = v8s[16 * (2 * tp + tt) + col];
+            const int bi = 8 * tt + ss, sh = 8 * (bi & 3);
+#pragma unroll
+            for (int c4 = 2 * tt; c4 < 2 * tt + 2; ++c4)
+              w[c4] = c4 == (bi >> 2) ? (w[c4] & ~(0xFFu << sh)) | (code << sh) : w[c4];
+          }
+          b.v[tp] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) b.vs[s] = s == ss ? s_stage.vs[col % NBK] : b.vs[s];
+      }
+    }
+
+    // ---- q~ of this chunk's K group, three bf16 parts, into LDS
+    {
+      const float ks8[8] = {b.ks[0].x, b.ks[0].y, b.ks[0].z, b.ks[0].w,
+                            b.ks[1].x, b.ks[1].y, b.ks[1].z, b.ks[1].w};
+#pragma unroll
+      for (int T = 0; T < NT; ++T) {
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = qs[T][e] * ks8[e];
+        uint4 pt[3];
+        split3(x, pt);
+#pragma unroll
+        for (int a = 0; a < 3; ++a) s_qt[wave][T][a][qvl][c8] = pt[a];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- QK^T: scores of column col (query T*QVT + col / NBK) at positions
+    // 16h + 4*grp + i, i < 4
+    f32x4 sc[2][NT];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int T = 0; T < NT; ++T) sc[h][T] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      bf16x8 ak[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint4 w = b.k[h][j / 2];
+        ak[h] = (j & 1) ? codes_bf16(w.z, w.w) : codes_bf16(w.x, w.y);
+      }
+#pragma unroll
+      for (int T = 0; T < NT; ++T)
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+          const uint4 bq = s_qt[wave][T][a][col / NBK][4 * j + grp];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) sc[h][T] = mfma(ak[h], bq, sc[h][T]);
+        }
+    }
+
+    // ---- online softmax per column, then the PV A operand of the lane
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      float s[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int p = p0 + 16 * (k / 4) + 4 * grp + k % 4;
+        const bool valid = p < nkeys && p >= P.n_sink;
+        s[k] = valid ? sc[k / 4][T][k % 4] : -INFINITY;
+      }
+      float mx = s[0];
+#pragma unroll
+      for (int k = 1; k < 8; ++k) mx = fmaxf(mx, s[k]);
+      const float mn = fmaxf(M[T], col_max(mx));
+      const float alpha = first ? 0.0f : fast_exp2(M[T] - mn);
+      M[T] = mn;
+      float w[8], ls = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float pk = fast_exp2(s[k] - mn);
+        ls += pk;
+        // masked slots weigh exactly 0 (their stale V scales may be anything)
+        w[k] = s[k] != -INFINITY ? pk * b.vs[k] : 0.0f;
+      }
+      l[T] = first ? ls : fmaf(l[T], alpha, ls);
+      uint4 aw[3];
+      split3(w, aw);
+      // the row's (query's) rescale factor, from the QK^T lane of that column
+      if (!first) {
+        if constexpr (NBK == 4) {
+          const float ar = __builtin_bit_cast(
+              float, __builtin_amdgcn_ds_bpermute(4 * (4 * grp), __builtin_bit_cast(int, alpha)));
+#pragma unroll
+          for (int t = 0; t < NTV; ++t) o[T][t][t / 2] *= ar;
+        } else {
+          const float a0 = __builtin_bit_cast(
+              float, __builtin_amdgcn_ds_bpermute(4 * (4 * grp), __builtin_bit_cast(int, alpha)));
+          const float a1 = __builtin_bit_cast(
+              float, __builtin_amdgcn_ds_bpermute(4 * (4 * grp + 2), __builtin_bit_cast(int, alpha)));
+#pragma unroll
+          for (int t = 0; t < NTV; ++t) {
+            o[T][t][t / 2] *= a0;
+            o[T][t][2 + t / 2] *= a1;
+          }
+        }
+      }
+      // ---- PV: the chunk's V tiles against the three weight parts
+#pragma unroll
+      for (int t = 0; t < NTV; ++t) {
+        const uint4 vw = b.v[t / 2];
+        const bf16x8 bv = (t & 1) ? codes_bf16(vw.z, vw.w) : codes_bf16(vw.x, vw.y);
+#pragma unroll
+        for (int a = 0; a < 3; ++a) o[T][t] = mfma(aw[a], bv, o[T][t]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  if constexpr (CPW > 0) {
+#pragma unroll
+    for (int t = 0; t < CPW; ++t) {
+      Buf& X = (NBUF == 2 && (t & 1)) ? RB : RA;
+      const int cht = ch0 + t * kWaves;
+      if (cht < c_end) compute(X, cht, t == 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + NBUF < CPW) issue(X, ch0 + (t + NBUF) * kWaves);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    int ch = ch0;
+    bool first = true;
+    while (ch < c_end) {
+      compute(RA, ch, first);
+      first = false;
+      __builtin_amdgcn_sched_barrier(0);
+      issue(RA, ch + NBUF * kWaves);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NBUF == 2) {
+        if (ch + kWaves >= c_end) break;
+        compute(RB, ch + kWaves, false);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(RB, ch + 3 * kWaves);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      ch += NBUF * kWaves;
+    }
+  }
+
+  // ---- wave state to LDS: (m, l) by the lanes of block-0 columns of row
+  // group 0, o by the lane holding (query, channel) (row 4*grp + i of tile t
+  // is query (4*grp + i) / NBK at block (4*grp + i) % NBK; kept when that is
+  // the tile's block t / 2). A wave without a chunk writes (kMinit, 0, 0).
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
+    const float lt = col_sum(l[T]);
+    const int qv = T * QVT + col / NBK;
+    if (grp == 0 && col % NBK == 0 && qv < G) {
+      s_ml[wave][qv][0] = M[T];
+      s_ml[wave][qv][1] = lt;
+    }
+#pragma unroll
+    for (int t = 0; t < NTV; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * grp + i, q = T * QVT + r / NBK;
+        if (r % NBK == t / 2 && q < G) s_o[wave][q][16 * t + col] = o[T][t][i];
+      }
+  }
+
+  // ---- the fp32 sinks (positions < n_sink, model.cpp:612-626), folded into
+  // wave 0's record of split 0 (q~ layout: lane = query qvl, channels
+  // 8*c8..); a fused step's own sink row comes from the step's inputs
+  const int ns = min(P.n_sink, nkeys);
+  if (split == 0 && wave == 0 && ns > 0) {  // wave-uniform
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float* ksb = P.ksink + static_cast<size_t>(kh) * P.n_sink * HD;
+    const float* vsb = P.vsink + static_cast<size_t>(kh) * P.n_sink * HD;
+    const bool fresh_sink = A.slot >= 0 && A.pos < P.n_sink;
+    const float* kin = fresh_sink ? A.k + kh * HD : nullptr;
+    const float* vin = fresh_sink ? A.v + kh * HD : nullptr;
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const int qv = T * QVT + qvl;
+      const bool real = qv < G;
+      float Ms = real ? s_ml[0][qv][0] : kMinit, Ls = real ? s_ml[0][qv][1] : 0.0f, os[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) os[e] = real ? s_o[0][qv][8 * c8 + e] : 0.0f;
+      // blocks of SB sinks, every load of a block in flight at once
+      constexpr int SB = 4;
+      for (int pb = 0; pb < ns; pb += SB) {
+        float kx[SB][8], vx[SB][8];
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const int p = min(pb + u, ns - 1);
+          const float4* ks4 = reinterpret_cast<const float4*>(ksb + p * HD + 8 * c8);
+          const float4* vs4 = reinterpret_cast<const float4*>(vsb + p * HD + 8 * c8);
+          const float4 k0 = ks4[0], k1 = ks4[1], v0 = vs4[0], v1 = vs4[1];
+          kx[u][0] = k0.x; kx[u][1] = k0.y; kx[u][2] = k0.z; kx[u][3] = k0.w;
+          kx[u][4] = k1.x; kx[u][5] = k1.y; kx[u][6] = k1.z; kx[u][7] = k1.w;
+          vx[u][0] = v0.x; vx[u][1] = v0.y; vx[u][2] = v0.z; vx[u][3] = v0.w;
+          vx[u][4] = v1.x; vx[u][5] = v1.y; vx[u][6] = v1.z; vx[u][7] = v1.w;
+          if (fresh_sink && p == A.pos) {  // uniform
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int d = 8 * c8 + e;
+              if (PROD && A.prod) {
+                kx[u][e] = produced<HD>(kin, A.kb != nullptr ? A.kb + kh * HD : nullptr, A.kcs, d);
+                vx[u][e] = produced<HD>(vin, A.vb != nullptr ? A.vb + kh * HD : nullptr, nullptr, d);
+              } else {
+                kx[u][e] = kin[d];
+                vx[u][e] = vin[d];
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          if (pb + u < ns) {  // uniform
+            float sdot = qs[T][0] * kx[u][0];
+#pragma unroll
+            for (int e = 1; e < 8; ++e) sdot += qs[T][e] * kx[u][e];
+            // sum over the LPQ lanes of the query (hd 128: a 16-lane row)
+            if constexpr (LPQ == 16) sdot += dpp<kX8>(sdot);
+            sdot += dpp<kX7>(sdot);
+            sdot += dpp<kX2>(sdot);
+            sdot += dpp<kX1>(sdot);
+            const float mn = fmaxf(Ms, sdot);
+            const float al = fast_exp2(Ms - mn), pw = fast_exp2(sdot - mn);
+            Ms = mn;
+            Ls = fmaf(Ls, al, pw);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) os[e] = fmaf(os[e], al, pw * vx[u][e]);
+          }
+        }
+      }
+      if (real) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s_o[0][qv][8 * c8 + e] = os[e];
+        if (c8 == 0) {
+          s_ml[0][qv][0] = Ms;
+          s_ml[0][qv][1] = Ls;
+        }
+      }
+    }
+  }
+
+  finish<HD, G, G, kWaves>(P, s_o, s_ml, split, kh, qrow);
+  if (!P.direct) {
+    // this thread's record stores have reached the coherence point
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned* cnt = P.cnt + (static_cast<size_t>(qrow) * P.nkv + kh) * kCounterStride;
+      const unsigned before =
+          __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = before == static_cast<unsigned>(P.nsplit - 1);
+      if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (s_last) merge_last<HD, G>(P, kh, qrow, wave, lane);
+  }
+  if (app_owner) App::flush(A, kh, lane, s_stage, &s_kg, s_row);
+}
+
+// CPW: chunks per wave of the plan (1, 2, 4 unrolled; 0 a runtime loop).
+template <int HD, int G, bool PROD>
+void* i8_kernel_cpw(int cpw) {
+  switch (cpw) {
+    case 1: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 1>);
+    case 2: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 2>);
+    case 4: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 4>);
+    default: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 0>);
+  }
+}
+
+template <int HD, bool PROD>
+void* pick_i8(int G, int cpw) {
+  switch (G) {
+    case 1: return i8_kernel_cpw<HD, 1, PROD>(cpw);
+    case 2: return i8_kernel_cpw<HD, 2, PROD>(cpw);
+    case 3: return i8_kernel_cpw<HD, 3, PROD>(cpw);
+    case 4: return i8_kernel_cpw<HD, 4, PROD>(cpw);
+    case 5: return i8_kernel_cpw<HD, 5, PROD>(cpw);
+    case 6: return i8_kernel_cpw<HD, 6, PROD>(cpw);
+    case 7: return i8_kernel_cpw<HD, 7, PROD>(cpw);
+    case 8: return i8_kernel_cpw<HD, 8, PROD>(cpw);
+    default: return nullptr;
+  }
+}
+
+}  // namespace
+}  // namespace dbi

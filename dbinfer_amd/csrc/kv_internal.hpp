@@ -17,6 +17,9 @@
 // capg is the capacity rounded up to a multiple of 64 positions (the reads of
 // the attention and prefill kernels are whole 32- / 64-position pieces).
 //
+// Dense int8 (head dims 64 and 128) uses the matrix-core layout below
+// (k_off_i8d / v_off_i8d); fp32 and the int8 ring use the granule layout.
+//
 // Granule layout (head dims 64 and 128; other head dims are stored row-major
 // [pos][hd]): 16 positions per granule, 16*hd elements. A wave reads one
 // "slot" of a granule per 64 lanes x 8 elements, each load instruction one
@@ -80,14 +83,40 @@ __host__ __device__ inline size_t v_off_tiled(int hd, bool int8, int pos, int d)
   return granule_off(hd, int8, pos, i, r * LPR + (d >> 3), d & 7);
 }
 
+// Dense int8 matrix-core layout, by 32-position chunks (one K group) of
+// 32*hd bytes, so that every 16-byte lane load is a bf16 MFMA operand once
+// converted (v_mfma_f32_16x16x32_bf16: lane m + 16*(k/8) holds k % 8 of row /
+// column m):
+//  K: per granule h (16 positions) hd/64 blocks of 1 KiB, [lane][16 bytes];
+//     lane n + 16*g of block jp holds position 16h + n, channels
+//     64jp + 32*j2 + 8g + e at byte 8*j2 + e (k-steps 2jp and 2jp + 1).
+//  V: hd/32 blocks of 1 KiB, [lane][16 bytes]; lane n + 16*g of block tp
+//     holds channel 16*(2tp + tt) + n at bytes 8*tt + s, s = 0..7 the
+//     positions 16*(s/4) + 4g + s%4 (the positions the lane's QK^T scores
+//     cover, so softmax weights feed the PV product without moving).
+__host__ __device__ inline size_t k_off_i8d(int hd, int pos, int d) {
+  const int p = pos & 31, h = p >> 4, n = p & 15;
+  const int jp = d >> 6, j2 = (d >> 5) & 1, g = (d >> 3) & 3, e = d & 7;
+  return static_cast<size_t>(pos >> 5) * 32 * hd + static_cast<size_t>(h * (hd >> 6) + jp) * 1024 +
+         (n + 16 * g) * 16 + j2 * 8 + e;
+}
+__host__ __device__ inline size_t v_off_i8d(int hd, int pos, int d) {
+  const int p = pos & 31, h = p >> 4, q = p & 15, g = q >> 2, s = 4 * h + (q & 3);
+  const int t = d >> 4, n = d & 15, tp = t >> 1, tt = t & 1;
+  return static_cast<size_t>(pos >> 5) * 32 * hd + static_cast<size_t>(tp) * 1024 +
+         (n + 16 * g) * 16 + tt * 8 + s;
+}
+
 // Offset of element (pos, d) inside one (layer, kv head) K array.
 __host__ __device__ inline size_t k_off(const KvGeom& g, int pos, int d) {
-  return g.tiled ? k_off_tiled(g.hd, g.int8, pos, d) : static_cast<size_t>(pos) * g.hd + d;
+  if (!g.tiled) return static_cast<size_t>(pos) * g.hd + d;
+  return g.int8 && !g.ring ? k_off_i8d(g.hd, pos, d) : k_off_tiled(g.hd, g.int8, pos, d);
 }
 
 // Offset of element (pos, d) inside one (layer, kv head) V array.
 __host__ __device__ inline size_t v_off(const KvGeom& g, int pos, int d) {
-  return g.tiled ? v_off_tiled(g.hd, g.int8, pos, d) : static_cast<size_t>(pos) * g.hd + d;
+  if (!g.tiled) return static_cast<size_t>(pos) * g.hd + d;
+  return g.int8 && !g.ring ? v_off_i8d(g.hd, pos, d) : v_off_tiled(g.hd, g.int8, pos, d);
 }
 
 // Elements of one (layer, kv head) K or V array.
