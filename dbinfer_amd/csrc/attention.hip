@@ -5,12 +5,12 @@
 namespace dbi {
 namespace {
 
-void* pick_kernel(int hd, int kind, int G, bool prod = false, int cpw = 1) {
+void* pick_kernel(int hd, int kind, int G, bool prod = false, int cpw = 1, int nr = 1) {
   switch (kind * 2 + (prod ? 1 : 0)) {
     case 0: return attn_instance_0_0(hd, G, cpw);
     case 1: return attn_instance_0_1(hd, G, cpw);
-    case 2: return attn_instance_1_0(hd, G, cpw);
-    case 3: return attn_instance_1_1(hd, G, cpw);
+    case 2: return attn_instance_1_0(hd, G, cpw, nr);
+    case 3: return attn_instance_1_1(hd, G, cpw, nr);
     case 4: return attn_instance_2_0(hd, G, cpw);
     case 5: return attn_instance_2_1(hd, G, cpw);
     case 6: return attn_instance_3_0(hd, G, cpw);
@@ -32,15 +32,29 @@ constexpr int kTargetBlocks = 256;
 struct Plan {
   int nsplit, chunks_per_split;
   int cpw;     // kernel instance: chunks per wave (1, 2, 4; 0 = runtime loop)
+  int nr;      // query rows per workgroup (dense int8 chunk rows; else 1)
+  int zgroups; // workgroups per (split, kv head): ceil(rows / nr)
   bool merge;  // several splits: the last to finish merges them
 };
+
+// Rows per workgroup of the dense int8 kernel: every row of a group shares
+// the K/V bytes of its chunks (the largest instance up to i8_max_rows).
+int i8_rows(const KvGeom& g, int G, int rows) {
+  const int qvt = 16 / (g.hd / kBlock);
+  int nr = (3 * qvt) / G;
+  if (nr > 4) nr = 4;
+  if (nr > rows) nr = rows;
+  return nr < 1 ? 1 : nr;
+}
 
 Plan plan(const KvGeom& g, const AttnCall& c) {
   const int G = c.n_heads / g.nkv;
   const int chunk = chunk_of(g);
   const int nkeys_max = g.ring ? c.ring.n_res : c.pos0 + c.rows;
   const int nchunks = (nkeys_max + chunk - 1) / chunk;
-  const int units = g.nkv * c.rows;
+  const int nr = g.int8 && !g.ring ? i8_rows(g, G, c.rows) : 1;
+  const int zgroups = (c.rows + nr - 1) / nr;
+  const int units = g.nkv * zgroups;
   // whole waves of workgroups only: a launch of target + a few would run a
   // second, nearly empty round on the CUs
   int want = kTargetBlocks / units;
@@ -53,6 +67,8 @@ Plan plan(const KvGeom& g, const AttnCall& c) {
   if (want > kMaxSplits) want = kMaxSplits;
   if (want < 1) want = 1;
   Plan p;
+  p.nr = nr;
+  p.zgroups = zgroups;
   p.chunks_per_split = (nchunks + want - 1) / want;
   p.nsplit = (nchunks + p.chunks_per_split - 1) / p.chunks_per_split;
   p.merge = p.nsplit > 1;
@@ -86,7 +102,7 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
   const bool prod = c.rows == 1 && (c.q_bias != nullptr || c.k_bias != nullptr ||
                                     c.v_bias != nullptr || c.rope_row != nullptr);
   const Plan pl = plan(g, c);
-  void* fn = pick_kernel(g.hd, kind_of(g), G, prod, pl.cpw);
+  void* fn = pick_kernel(g.hd, kind_of(g), G, prod, pl.cpw, pl.nr);
   if (fn == nullptr || !g.tiled) return hipErrorNotSupported;
   AttnParams p{};
   const size_t layer_heads = static_cast<size_t>(c.layer) * g.nkv;
@@ -168,7 +184,7 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
     }
   }
   void* args[] = {&p, &a};
-  return hipLaunchKernel(fn, dim3(p.nsplit, g.nkv, c.rows), dim3(kThreads), args, 0, st);
+  return hipLaunchKernel(fn, dim3(p.nsplit, g.nkv, pl.zgroups), dim3(kThreads), args, 0, st);
 }
 
 }  // namespace dbi

@@ -1,11 +1,12 @@
-// Kernel instances of the dense int8 layout, raw-projection inputs
-// (matrix-core kernel of attn_mfma.hpp).
+// Kernel instances of the dense int8 layout, raw-projection inputs (decode:
+// one query row; matrix-core kernel of attn_mfma.hpp).
 #include "attn_mfma.hpp"
 
 namespace dbi {
 
-void* attn_instance_1_1(int hd, int G, int cpw) {
-  return hd == 64 ? pick_i8<64, true>(G, cpw) : hd == 128 ? pick_i8<128, true>(G, cpw) : nullptr;
+void* attn_instance_1_1(int hd, int G, int cpw, int nr) {
+  if (nr != 1) return nullptr;
+  return hd == 64 ? pick_i8<64, true, 1>(G, cpw) : hd == 128 ? pick_i8<128, true, 1>(G, cpw) : nullptr;
 }
 
 }  // namespace dbi

@@ -368,14 +368,11 @@ __device__ __forceinline__ void finish(const AttnParams& P, float (&s_o)[kWaves]
 // per record, so one load instruction covers 64 / (HD / 4) splits, every
 // load of the merge in one round. Records are read at device coherence.
 template <int HD, int G>
-__device__ __forceinline__ void merge_last(const AttnParams& P, int kh, int qrow, int wave,
-                                           int lane) {
+__device__ __forceinline__ void merge_head(const AttnParams& P, int kh, int qrow, int g, int lane) {
   constexpr int kSC1 = 16;  // cache policy: agent-coherent load
   constexpr int LPH = HD / 4;       // lanes per record of one head
   constexpr int SPI = 64 / LPH;     // splits per load instruction
   constexpr int NI = kMaxSplits / SPI;
-  if (wave >= G) return;
-  const int g = wave;
   const size_t head_base = static_cast<size_t>(qrow) * P.nkv + kh;
   constexpr int RF = record_floats(G, HD);
   const float* region = P.part + head_base * record_region(P.nsplit, G, HD);
@@ -430,6 +427,11 @@ __device__ __forceinline__ void merge_last(const AttnParams& P, int kh, int qrow
     *reinterpret_cast<float4*>(P.out + h * HD + 4 * lane) =
         make_float4(o4[0] * inv, o4[1] * inv, o4[2] * inv, o4[3] * inv);
   }
+}
+template <int HD, int G>
+__device__ __forceinline__ void merge_last(const AttnParams& P, int kh, int qrow, int wave,
+                                           int lane) {
+  if (wave < G) merge_head<HD, G>(P, kh, qrow, wave, lane);
 }
 
 
@@ -1345,8 +1347,10 @@ void* pick_g(int G, int cpw) {
 // one per layout and producer flag, each in its own translation unit
 void* attn_instance_0_0(int hd, int G, int cpw);
 void* attn_instance_0_1(int hd, int G, int cpw);
-void* attn_instance_1_0(int hd, int G, int cpw);
-void* attn_instance_1_1(int hd, int G, int cpw);
+// dense int8 (matrix-core kernel): nr query rows per workgroup
+void* attn_instance_1_0(int hd, int G, int cpw, int nr);
+void* attn_instance_1_1(int hd, int G, int cpw, int nr);
+void* attn_instance_i8_rows(int hd, int G, int cpw, int nr);
 void* attn_instance_2_0(int hd, int G, int cpw);
 void* attn_instance_2_1(int hd, int G, int cpw);
 void* attn_instance_3_0(int hd, int G, int cpw);

@@ -10,7 +10,9 @@
 //    exactly hi + mid + lo of three bf16 parts (split3), so each score is the
 //    fp32 accumulation of exact products q~_i * k8_i, q~ = (q * scale * log2 e)
 //    * ks (the reference's (q_i * ks_i) * k8_i, per K group), and each output
-//    the fp32 accumulation of exact (p * vs) * v8 products.
+//    the fp32 accumulation of exact (p * vs) * v8 products. (Two parts are not
+//    enough: a 2^-18 weight error times an outlier channel's |v| exceeds the
+//    reference's own fp32 error where the output cancels.)
 //  - QK^T: A = the chunk's K codes (rows: positions, read straight from the
 //    layout of kv_internal.hpp), B = q~ in three parts (columns: (query,
 //    V block) pairs, each query repeated once per 32-channel V block), built
@@ -99,11 +101,49 @@ __device__ __forceinline__ float col_sum(float a) {
   return swap32_sum(a, a);
 }
 
-template <int HD, int G>
+// NQ: query vectors of a workgroup (rows x heads)
+// produced<HD>() of the 8 elements d0..d0+7 (d0 % 8 == 0) of one head row,
+// from vector loads: the elements, their rope partners (d +- hd/2), both
+// biases and the 8 (cos, sin) pairs
+template <int HD>
+__device__ __forceinline__ void produce8(const float* x, const float* bias, const double2* cs,
+                                         int d0, float (&out)[8]) {
+  constexpr int H2 = HD / 2;
+  const int j0 = d0 % H2;
+  const bool hi = d0 >= H2;
+  float a[8], b[8], ba[8], bb[8];
+  auto ld8 = [](const float* p, float (&v)[8]) {
+    const float4 u = reinterpret_cast<const float4*>(p)[0], w = reinterpret_cast<const float4*>(p)[1];
+    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w; v[4] = w.x; v[5] = w.y; v[6] = w.z; v[7] = w.w;
+  };
+  ld8(x + j0, a);
+  ld8(x + j0 + H2, b);
+  if (bias != nullptr) {
+    ld8(bias + j0, ba);
+    ld8(bias + j0 + H2, bb);
+  }
+  double2 c2[8];
+  if (cs != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c2[e] = cs[j0 + e];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float u = a[e], w = b[e];
+    if (bias != nullptr) {
+      u += ba[e];
+      w += bb[e];
+    }
+    if (cs != nullptr) rope_pair(u, w, c2[e]);
+    out[e] = hi ? w : u;
+  }
+}
+
+template <int HD, int NQ>
 struct MCfg {
   static constexpr int NBK = HD / kBlock;      // V blocks per head
   static constexpr int QVT = 16 / NBK;         // query vectors per 16-column tile
-  static constexpr int NT = (G + QVT - 1) / QVT;  // column tiles
+  static constexpr int NT = (NQ + QVT - 1) / QVT;  // column tiles
   static constexpr int LPQ = HD / 8;           // lanes per query in the q~ layout
   static constexpr int NJ = HD / 32;           // QK k-steps (32 channels)
   static constexpr int KL = HD / 64;           // K loads per granule (two k-steps each)
@@ -116,32 +156,99 @@ struct MCfg {
 };
 
 // One chunk's loads.
-template <int HD, int G>
+template <int HD, int NQ>
 struct MBuf {
-  using C = MCfg<HD, G>;
+  using C = MCfg<HD, NQ>;
   uint4 k[2][C::KL];  // K: granule h, load jp
   float4 ks[2];       // the K group's channel scales of this lane's 8 q~ channels
   uint4 v[C::VL];     // V: load tp
   float vs[8];        // V block scale of slot s (position 16(s/4) + 4g + s%4, block col % NBK)
 };
 
-template <int HD, int G, bool PROD, int CPW>
+// finish() for the nr <= NR query rows [row0, row0 + nr) of a workgroup:
+// the cross-wave combine of each (row, head), then the output (single split)
+// or the split's record of each row; every thread combines its head's waves
+// itself, with finish()'s arithmetic.
+template <int HD, int G, int NR>
+__device__ __forceinline__ void finish_rows(const AttnParams& P,
+                                            float (&s_o)[kWaves][NR * G][HD],
+                                            float (&s_ml)[kWaves][NR * G][2], int split, int kh,
+                                            int row0, int nr) {
+  __syncthreads();
+  auto combine = [&](int q, float& M, float (&f)[kWaves], float& L) {
+    float m[kWaves], l[kWaves];
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+      m[i] = s_ml[i][q][0];
+      l[i] = s_ml[i][q][1];
+    }
+    M = kMinit;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) M = fmaxf(M, m[i]);
+    L = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+      f[i] = fast_exp2(m[i] - M);
+      L += l[i] * f[i];
+    }
+  };
+  auto o_of = [&](int q, int d, const float (&f)[kWaves]) {
+    float O = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) O += s_o[i][q][d] * f[i];
+    return O;
+  };
+  if (P.direct) {
+    for (int idx = threadIdx.x; idx < nr * G * HD; idx += kThreads) {
+      const int q = idx / HD, d = idx % HD, r = q / G, g = q % G;
+      float M, f[kWaves], L;
+      combine(q, M, f, L);
+      P.out[((static_cast<size_t>(row0 + r) * P.n_heads + kh * G + g) * HD) + d] = o_of(q, d, f) / L;
+    }
+    return;
+  }
+  constexpr int PR = G * HD + 2 * G;  // floats a row's record receives
+  for (int idx = threadIdx.x; idx < nr * PR; idx += kThreads) {
+    const int r = idx / PR, rem = idx % PR;
+    const size_t head_base = static_cast<size_t>(row0 + r) * P.nkv + kh;
+    float* orec = P.part + head_base * record_region(P.nsplit, G, HD) +
+                  static_cast<size_t>(split) * record_floats(G, HD);
+    const int g = rem < G * HD ? rem / HD : (rem - G * HD) >> 1;
+    float M, f[kWaves], L;
+    combine(r * G + g, M, f, L);
+    if (rem < G * HD) {
+      __hip_atomic_store(orec + rem, o_of(r * G + g, rem % HD, f), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      const int k = rem - G * HD;  // (m, l) of head k / 2
+      __hip_atomic_store(orec + G * HD + k, (k & 1) ? L : M, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// NR: query rows per workgroup (chunk rows: a verify round's rows share
+// every K/V byte and its bf16 conversion; decode and the fused step: 1).
+template <int HD, int G, bool PROD, int CPW, int NR>
 __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, const AppendArgs A) {
-  using C = MCfg<HD, G>;
+  constexpr int NQ = NR * G;
+  using C = MCfg<HD, NQ>;
   constexpr int NBK = C::NBK, QVT = C::QVT, NT = C::NT, LPQ = C::LPQ, NJ = C::NJ;
   constexpr int KL = C::KL, NTV = C::NTV, VL = C::VL, QROW = C::QROW;
   constexpr int CHUNK = kKGroup;
   constexpr int NB = NBK;
 
-  __shared__ float s_o[kWaves][G][HD];
-  __shared__ float s_ml[kWaves][G][2];
-  __shared__ int s_last;
+  static_assert(NR == 1 || !PROD, "raw projections: decode (one row) only");
+  constexpr bool kFuse = NR == 1;  // the fused decode step (one row) only
+  __shared__ float s_o[kWaves][NQ][HD];
+  __shared__ float s_ml[kWaves][NQ][2];
+  __shared__ int s_last[NR];
   __shared__ __align__(16) uint4 s_qt[kWaves][NT][3][QVT][QROW];
   // fused step stages (the single head group's)
   __shared__ __align__(16) AppStage s_stage;
   __shared__ __align__(16) float s_row[PROD ? 768 : 256];
-  __shared__ __align__(16) float s_raw[kWaves / 2][kKGroup * HD / (kWaves / 2)];
-  __shared__ __align__(16) uint8_t s_kgbuf[sizeof(KGroupStage)];
+  __shared__ __align__(16) float s_raw[kFuse ? kWaves / 2 : 1][kFuse ? kKGroup * HD / (kWaves / 2) : 4];
+  __shared__ __align__(16) uint8_t s_kgbuf[kFuse ? sizeof(KGroupStage) : 16];
   KGroupStage& s_kg = *reinterpret_cast<KGroupStage*>(s_kgbuf);
 
   const int lane = threadIdx.x & 63;
@@ -150,13 +257,15 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   const int qvl = lane / LPQ, c8 = lane % LPQ;   // q~ layout: query qvl, channels 8*c8..
   const int split = blockIdx.x;
   const int kh = blockIdx.y;
-  const int qrow = blockIdx.z;
-  const int nkeys = P.pos0 + qrow + 1;
+  const int row0 = blockIdx.z * NR;              // this workgroup's rows [row0, row0 + nr)
+  const int nr = min(NR, P.rows - row0);
+  const int nqv = nr * G;                        // its query vectors (row r, head g: r*G + g)
+  const int nkeys = P.pos0 + row0 + nr;          // keys of its last row
   const int nchunks = (nkeys + CHUNK - 1) / CHUNK;
   const int c_end = min((split + 1) * P.chunks_per_split, nchunks);
   const size_t head = static_cast<size_t>(kh) * P.capg;
   const size_t head_el = head * HD;
-  const int app_chunk = A.slot >= 0 ? A.slot / CHUNK : -1;
+  const int app_chunk = kFuse && A.slot >= 0 ? A.slot / CHUNK : -1;
   const bool app_here = app_chunk >= split * P.chunks_per_split && app_chunk < c_end;
 
   const int kv_bytes = P.capg * HD;
@@ -165,7 +274,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   const rsrc_t rks = make_rsrc(P.ks + static_cast<size_t>(kh) * P.ng * HD, P.ng * HD * 4);
   const rsrc_t rvs = make_rsrc(P.vs + head * NB, P.capg * NB * 4);
 
-  using Buf = MBuf<HD, G>;
+  using Buf = MBuf<HD, NQ>;
   // one chunk buffer: fewer registers, and measured no slower than two (the
   // next chunk's loads wait for the current chunk's math either way)
   constexpr int NBUF = 1;
@@ -196,19 +305,18 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
 
   // ---- q * scale * log2(e) of this lane's 8 channels of query T*QVT + qvl
   // (raw projections: bias, then the fp64 rope, as the producer computes
-  // each element; padding queries >= G are 0)
+  // each element; padding queries >= nqv are 0)
   float qs[NT][8];
-  const float* qbase = P.q + (static_cast<size_t>(qrow) * P.n_heads + kh * G) * HD;
   const bool q_prod = PROD && (P.qb != nullptr || P.qcs != nullptr);
   auto load_q = [&]() {
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
-      const int qv = T * QVT + qvl;
-      const float* qg = qbase + min(qv, G - 1) * HD;
+      const int qv = min(T * QVT + qvl, nqv - 1);
+      const float* qg =
+          P.q + (static_cast<size_t>(row0 + qv / G) * P.n_heads + kh * G + qv % G) * HD;
       if (q_prod) {
-        const float* bg = P.qb != nullptr ? P.qb + (kh * G + min(qv, G - 1)) * HD : nullptr;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qs[T][e] = produced<HD>(qg, bg, P.qcs, 8 * c8 + e);
+        const float* bg = P.qb != nullptr ? P.qb + (kh * G + qv % G) * HD : nullptr;
+        produce8<HD>(qg, bg, P.qcs, 8 * c8, qs[T]);
       } else {
         const float4 a = *reinterpret_cast<const float4*>(qg + 8 * c8);
         const float4 b = *reinterpret_cast<const float4*>(qg + 8 * c8 + 4);
@@ -246,7 +354,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
 #pragma unroll
   for (int T = 0; T < NT; ++T)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qs[T][e] = T * QVT + qvl < G ? qs[T][e] * P.qscale : 0.0f;
+    for (int e = 0; e < 8; ++e) qs[T][e] = T * QVT + qvl < nqv ? qs[T][e] * P.qscale : 0.0f;
 
   // running state: per column tile, the max and the lane's partial sum of its
   // column's query (QK^T layout), and the PV accumulators (row (query,
@@ -268,7 +376,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     const int p0 = ch * CHUNK;
 
     // ---- the fused step's chunk: its K group and the new V row from LDS
-    if (ch == app_chunk) {  // uniform
+    if (kFuse && ch == app_chunk) {  // uniform
       App::put_row(A, app_in, lane, s_row);
       if (PROD && A.prod) App::produce_row(A, lane, s_row);
       App::stage_row(A, lane, s_stage, s_row);
@@ -348,11 +456,13 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     // ---- online softmax per column, then the PV A operand of the lane
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
+      // keys of this column's row (causal: row r attends [0, pos0 + r])
+      const int nk = P.pos0 + row0 + (T * QVT + col / NBK) / G + 1;
       float s[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int p = p0 + 16 * (k / 4) + 4 * grp + k % 4;
-        const bool valid = p < nkeys && p >= P.n_sink;
+        const bool valid = p < nk && p >= P.n_sink;
         s[k] = valid ? sc[k / 4][T][k % 4] : -INFINITY;
       }
       float mx = s[0];
@@ -441,7 +551,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   for (int T = 0; T < NT; ++T) {
     const float lt = col_sum(l[T]);
     const int qv = T * QVT + col / NBK;
-    if (grp == 0 && col % NBK == 0 && qv < G) {
+    if (grp == 0 && col % NBK == 0 && qv < NQ) {
       s_ml[wave][qv][0] = M[T];
       s_ml[wave][qv][1] = lt;
     }
@@ -450,27 +560,28 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * grp + i, q = T * QVT + r / NBK;
-        if (r % NBK == t / 2 && q < G) s_o[wave][q][16 * t + col] = o[T][t][i];
+        if (r % NBK == t / 2 && q < NQ) s_o[wave][q][16 * t + col] = o[T][t][i];
       }
   }
 
   // ---- the fp32 sinks (positions < n_sink, model.cpp:612-626), folded into
   // wave 0's record of split 0 (q~ layout: lane = query qvl, channels
   // 8*c8..); a fused step's own sink row comes from the step's inputs
-  const int ns = min(P.n_sink, nkeys);
+  const int ns = min(P.n_sink, nkeys);  // sinks of the last row (a row r sees pos0 + r + 1 keys)
   if (split == 0 && wave == 0 && ns > 0) {  // wave-uniform
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const float* ksb = P.ksink + static_cast<size_t>(kh) * P.n_sink * HD;
     const float* vsb = P.vsink + static_cast<size_t>(kh) * P.n_sink * HD;
-    const bool fresh_sink = A.slot >= 0 && A.pos < P.n_sink;
+    const bool fresh_sink = kFuse && A.slot >= 0 && A.pos < P.n_sink;
     const float* kin = fresh_sink ? A.k + kh * HD : nullptr;
     const float* vin = fresh_sink ? A.v + kh * HD : nullptr;
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
       const int qv = T * QVT + qvl;
-      const bool real = qv < G;
+      const bool real = qv < nqv;
+      const int nsq = min(P.n_sink, P.pos0 + row0 + (real ? qv / G : 0) + 1);  // this row's sinks
       float Ms = real ? s_ml[0][qv][0] : kMinit, Ls = real ? s_ml[0][qv][1] : 0.0f, os[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) os[e] = real ? s_o[0][qv][8 * c8 + e] : 0.0f;
@@ -513,6 +624,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
             sdot += dpp<kX7>(sdot);
             sdot += dpp<kX2>(sdot);
             sdot += dpp<kX1>(sdot);
+            sdot = pb + u < nsq ? sdot : -INFINITY;
             const float mn = fmaxf(Ms, sdot);
             const float al = fast_exp2(Ms - mn), pw = fast_exp2(sdot - mn);
             Ms = mn;
@@ -533,47 +645,60 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     }
   }
 
-  finish<HD, G, G, kWaves>(P, s_o, s_ml, split, kh, qrow);
+  finish_rows<HD, G, NR>(P, s_o, s_ml, split, kh, row0, nr);
   if (!P.direct) {
     // this thread's record stores have reached the coherence point
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (static_cast<int>(threadIdx.x) < nr) {  // one arrival per row
+      const int qrow = row0 + threadIdx.x;
       unsigned* cnt = P.cnt + (static_cast<size_t>(qrow) * P.nkv + kh) * kCounterStride;
       const unsigned before =
           __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const int last = before == static_cast<unsigned>(P.nsplit - 1);
       if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = last;
+      s_last[threadIdx.x] = last;
     }
     __syncthreads();
-    if (s_last) merge_last<HD, G>(P, kh, qrow, wave, lane);
+    // the (row, head) merges this workgroup owns, one wave each
+    for (int pr = wave; pr < nqv; pr += kWaves)
+      if (s_last[pr / G]) merge_head<HD, G>(P, kh, row0 + pr / G, pr % G, lane);
   }
-  if (app_owner) App::flush(A, kh, lane, s_stage, &s_kg, s_row);
+  if (kFuse && app_owner) App::flush(A, kh, lane, s_stage, &s_kg, s_row);
+}
+
+// The largest rows-per-workgroup a (hd, G) instance serves: its query
+// vectors fill at most three 16-column tiles (registers), and at most 4 rows.
+__host__ __device__ constexpr int i8_max_rows(int HD, int G) {
+  return (3 * (16 / (HD / kBlock))) / G < 4 ? (3 * (16 / (HD / kBlock))) / G : 4;
 }
 
 // CPW: chunks per wave of the plan (1, 2, 4 unrolled; 0 a runtime loop).
-template <int HD, int G, bool PROD>
+template <int HD, int G, bool PROD, int NR>
 void* i8_kernel_cpw(int cpw) {
-  switch (cpw) {
-    case 1: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 1>);
-    case 2: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 2>);
-    case 4: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 4>);
-    default: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 0>);
+  if constexpr (NR > i8_max_rows(HD, G) || (PROD && NR > 1)) {
+    return nullptr;
+  } else {
+    switch (cpw) {
+      case 1: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 1, NR>);
+      case 2: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 2, NR>);
+      case 4: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 4, NR>);
+      default: return reinterpret_cast<void*>(&attn_i8_kernel<HD, G, PROD, 0, NR>);
+    }
   }
 }
 
-template <int HD, bool PROD>
+template <int HD, bool PROD, int NR>
 void* pick_i8(int G, int cpw) {
   switch (G) {
-    case 1: return i8_kernel_cpw<HD, 1, PROD>(cpw);
-    case 2: return i8_kernel_cpw<HD, 2, PROD>(cpw);
-    case 3: return i8_kernel_cpw<HD, 3, PROD>(cpw);
-    case 4: return i8_kernel_cpw<HD, 4, PROD>(cpw);
-    case 5: return i8_kernel_cpw<HD, 5, PROD>(cpw);
-    case 6: return i8_kernel_cpw<HD, 6, PROD>(cpw);
-    case 7: return i8_kernel_cpw<HD, 7, PROD>(cpw);
-    case 8: return i8_kernel_cpw<HD, 8, PROD>(cpw);
+    case 1: return i8_kernel_cpw<HD, 1, PROD, NR>(cpw);
+    case 2: return i8_kernel_cpw<HD, 2, PROD, NR>(cpw);
+    case 3: return i8_kernel_cpw<HD, 3, PROD, NR>(cpw);
+    case 4: return i8_kernel_cpw<HD, 4, PROD, NR>(cpw);
+    case 5: return i8_kernel_cpw<HD, 5, PROD, NR>(cpw);
+    case 6: return i8_kernel_cpw<HD, 6, PROD, NR>(cpw);
+    case 7: return i8_kernel_cpw<HD, 7, PROD, NR>(cpw);
+    case 8: return i8_kernel_cpw<HD, 8, PROD, NR>(cpw);
     default: return nullptr;
   }
 }
