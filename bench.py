@@ -162,18 +162,30 @@ def measure(torch, HipKV, code, name, K, V, q, args, scale):
     return res
 
 
+def host_threads():
+    """(cores this process may run on, threads the CPU baseline uses): every
+    core of the job's share. A GPU box allots each GPU a host share and says
+    so in OMP_NUM_THREADS (16 per GPU); elsewhere the affinity mask is the
+    share."""
+    nproc = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    share = int(env) if env.isdigit() and int(env) > 0 else nproc
+    return nproc, min(nproc, share)
+
+
 def cpu_baseline(budget_s: float):
     """The CPU oracle (the reference's KVCache::append + attend_dense_int8
-    restated, head-parallel like its thread pool) on the same decode step:
-    per layer, quantize-on-append at POS then attention over CTX keys, over
-    CPU_LAYERS layers of a seeded cache of the same shape (filling all L
-    layers through the reference's per-append group requantization alone
-    takes ~30 s of CPU). Steps are timed until the budget is spent; the result
-    is per token and layer."""
+    restated, head-parallel like its thread pool; built -O3
+    -ffp-contract=off) on the same decode step: per layer, quantize-on-append
+    at POS then attention over CTX keys, over CPU_LAYERS layers of a seeded
+    cache of the same shape (filling all L layers through the reference's
+    per-append group requantization alone takes ~30 s of CPU). Timed on all
+    cores of the host share and on 1 core, each the median of >= 5 steps
+    (half the budget each); the result is per token and layer."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle  # checker / baseline only
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    nproc, threads = host_threads()
     rng = np.random.default_rng(7)
     P = NKV * HD
     nl = CPU_LAYERS
@@ -191,24 +203,31 @@ def cpu_baseline(budget_s: float):
     fill_s = time.perf_counter() - t0
     q = rng.standard_normal((nl, NH * HD), dtype=np.float32)
     scale = np.float32(1.0) / np.sqrt(np.float32(HD))
-    steps = []
-    t_end = time.perf_counter() + budget_s
-    while len(steps) < 3 or time.perf_counter() < t_end:
-        t = time.perf_counter()
-        for layer in range(nl):
-            kv.append(layer, POS, rows[layer][0], rows[layer][1])
-            kv.attend(layer, POS, q[layer], NH, scale, n_threads=threads)
-        steps.append(time.perf_counter() - t)
+    def timed(n_threads, budget):
+        steps = []
+        t_end = time.perf_counter() + budget
+        while len(steps) < 5 or time.perf_counter() < t_end:
+            t = time.perf_counter()
+            for layer in range(nl):
+                kv.append(layer, POS, rows[layer][0], rows[layer][1])
+                kv.attend(layer, POS, q[layer], NH, scale, n_threads=n_threads)
+            steps.append(time.perf_counter() - t)
+        return statistics.median(steps) / nl, len(steps)
+
+    med, n_all = timed(threads, budget_s / 2)
+    med1, n_one = timed(1, budget_s / 2)
     kv.close()
-    med = statistics.median(steps) / nl
     return {
         "value": round(1e6 * med, 3),
         "unit": "us/token/layer",
         "cores": threads,
         "kind": "port",
         "sample": (f"oracle append + attend_dense_int8 decode step at pos {POS} over {nl} of the {L} "
-                   f"layers (ctx {CTX}, 24q/8kv, hd 128, 4 sinks), median of {len(steps)} "
-                   f"steps in ~{budget_s:.0f}s, {threads} threads; cache filled in {fill_s:.1f}s"),
+                   f"layers (ctx {CTX}, 24q/8kv, hd 128, 4 sinks), median of {n_all} steps on "
+                   f"{threads} threads and of {n_one} on 1 thread, ~{budget_s / 2:.0f}s each; "
+                   f"cache filled in {fill_s:.1f}s"),
+        "value_1core": round(1e6 * med1, 3),
+        "nproc": nproc,
         "gbs_equiv": round(attn_bytes("int8") / med / 1e9, 3),
         "cpu_model": _cpu_model(),
     }
@@ -535,12 +554,13 @@ def prefix_io(HipKV, code, n_sink, kv, L_, cap, nkv, hd, n_tok):
 
 def config_cpu(K, V, q, name, nh, nkv, hd, dt, ns, win, pos, rows, scale):
     """The CPU oracle on one layer of the same config (head-parallel on the
-    host cores): the decode step (append at pos + attention) and, for the
-    chunk configs, the chunk attention; median of >= 3 runs."""
+    host share, and on 1 core): the decode step (append at pos + attention)
+    and, for the chunk configs, the chunk attention; median of >= 5 runs
+    (the 256-row chunk: 1)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle  # checker / baseline only
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    nproc, threads = host_threads()
     Kh = K.cpu().numpy()
     Vh = V.cpu().numpy()
     qh = q[0].cpu().numpy()
@@ -550,7 +570,7 @@ def config_cpu(K, V, q, name, nh, nkv, hd, dt, ns, win, pos, rows, scale):
     o.append_n(0, 0, Kh[:pos], Vh[:pos])
     fill_s = time.perf_counter() - t0
 
-    def med(fn, n=3):
+    def med(fn, n=5):
         ts = []
         for _ in range(n):
             t = time.perf_counter()
@@ -558,21 +578,26 @@ def config_cpu(K, V, q, name, nh, nkv, hd, dt, ns, win, pos, rows, scale):
             ts.append(time.perf_counter() - t)
         return statistics.median(ts)
 
-    if win:
-        step_s = med(lambda: o.attend_ring(0, pos, qh[: nh * hd], Kh[pos], Vh[pos], nh, scale,
-                                           n_threads=threads))
-    else:
+    def step_time(n_threads):
+        if win:
+            return med(lambda: o.attend_ring(0, pos, qh[: nh * hd], Kh[pos], Vh[pos], nh, scale,
+                                             n_threads=n_threads))
+
         def step():
             o.append(0, pos, Kh[pos], Vh[pos])
-            o.attend(0, pos, qh[: nh * hd], nh, scale, n_threads=threads)
-        step_s = med(step)
+            o.attend(0, pos, qh[: nh * hd], nh, scale, n_threads=n_threads)
+        return med(step)
+
+    step_s = step_time(threads)
+    step1_s = step_time(1)
     out = {"us_per_token_layer": round(1e6 * step_s, 1), "threads": threads,
-           "fill_s": round(fill_s, 2), "kind": "port"}
+           "us_per_token_layer_1core": round(1e6 * step1_s, 1), "nproc": nproc,
+           "cpu_model": _cpu_model(), "fill_s": round(fill_s, 2), "kind": "port"}
     if rows:
         pos0 = 1792 if rows == 256 else pos + 1 - rows
         if dt == "f32" and not win:
             chunk_s = med(lambda: o.attend_chunk(0, pos0, qh[: rows * nh * hd], nh, scale,
-                                                 n_threads=threads), 1 if rows > 16 else 3)
+                                                 n_threads=threads), 1 if rows > 16 else 5)
             out["chunk_us"] = round(1e6 * chunk_s, 1)
     o.close()
     return out
