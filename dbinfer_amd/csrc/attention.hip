@@ -58,10 +58,8 @@ Plan plan(const KvGeom& g, const AttnCall& c) {
   // whole waves of workgroups only: a launch of target + a few would run a
   // second, nearly empty round on the CUs
   int want = kTargetBlocks / units;
-  // waves per head group: wide groups of the VALU kernel split the workgroup
-  // in two; the dense int8 matrix-core kernel serves every head in each wave
-  const bool mfma = g.int8 && !g.ring;
-  const int wpg = (!mfma && G > 4 && g.hd == 128) ? kWaves / 2 : kWaves;
+  // (every wave of both kernels serves all G heads of its chunks)
+  const int wpg = kWaves;
   const int max_by_chunks = (nchunks + wpg - 1) / wpg;  // >= one chunk per wave
   if (want > max_by_chunks) want = max_by_chunks;
   if (want > kMaxSplits) want = kMaxSplits;

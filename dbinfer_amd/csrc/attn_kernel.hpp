@@ -227,10 +227,9 @@ struct Cfg {
   static constexpr int NGC = 1;                 // granules per chunk
   static constexpr int CHUNK = kGranule * NGC;
   static constexpr int NS = NSG * NGC;          // slots per chunk
-  // wide groups split their heads over two halves of the workgroup (each
-  // half streams the same chunks, the second read hitting L1/L2): a wave
-  // then holds q and o of GW <= 4 heads, which keeps them in registers
-  static constexpr int NHG = (G > 4 && HD == 128) ? 2 : 1;
+  // every wave holds q and o of all G heads (up to 8 x 16 registers each):
+  // each chunk is streamed, and for a ring roped, once per kv head
+  static constexpr int NHG = 1;
   static constexpr int GW = (G + NHG - 1) / NHG;  // query heads per wave
   static constexpr int WPG = kWaves / NHG;        // waves per head group
   static constexpr int GP = GW <= 4 ? 4 : 8;      // padded heads of an LDS weight row
