@@ -60,7 +60,13 @@ Plan plan(const KvGeom& g, const AttnCall& c) {
   int want = kTargetBlocks / units;
   // (every wave of both kernels serves all G heads of its chunks)
   const int wpg = kWaves;
-  const int max_by_chunks = (nchunks + wpg - 1) / wpg;  // >= one chunk per wave
+  // at least one chunk per wave; a short context may go down to one chunk
+  // per two waves (more CUs share the stream, some waves idle) while that
+  // keeps the merge within 32 records (measured: 64 records cost the C4
+  // ring more than the wider spread gains)
+  const int strict = (nchunks + wpg - 1) / wpg;
+  const int relaxed = (nchunks + wpg / 2 - 1) / (wpg / 2);
+  const int max_by_chunks = strict > (relaxed < 32 ? relaxed : 32) ? strict : (relaxed < 32 ? relaxed : 32);
   if (want > max_by_chunks) want = max_by_chunks;
   if (want > kMaxSplits) want = kMaxSplits;
   if (want < 1) want = 1;
