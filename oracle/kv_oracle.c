@@ -782,7 +782,9 @@ float ok_f16_to_f32(uint16_t h) {
     memcpy(&bits, &v, 4);
     bits |= sign;
   } else if (e == 31) {
-    bits = sign | 0x7f800000u | (m << 13);
+    /* infinity keeps its sign; every NaN becomes the canonical quiet NaN,
+     * std::numeric_limits<float>::quiet_NaN() (dequant.cpp:27-29) */
+    bits = m == 0 ? (sign | 0x7f800000u) : 0x7fc00000u;
   } else {
     bits = sign | ((e + 112u) << 23) | (m << 13);
   }

@@ -25,6 +25,10 @@ def test_f16_all_values():
     nan = np.isnan(want)
     assert np.array_equal(np.isnan(got), nan)
     assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    # every NaN half (either sign, any payload) converts to the reference's
+    # std::numeric_limits<float>::quiet_NaN(), bits 0x7fc00000 (dequant.cpp:27-29)
+    assert nan.sum() == 2 * 1023
+    assert np.all(got[nan].view(np.uint32) == 0x7FC00000)
 
 
 @pytest.mark.parametrize("f16", [False, True])
