@@ -29,8 +29,14 @@ int chunk_of(const KvGeom& g) { return g.int8 && !g.ring ? 2 * kGranule : kGranu
 // CU).
 constexpr int kTargetBlocks = 256;
 
+// Dense fp32 chunks of two or more rows run on the matrix-core rows kernel
+// (attn_rows.hpp): nvt 16-vector tiles per workgroup, 16 nvt / G rows each.
+bool f32_rows(const KvGeom& g, const AttnCall& c) { return !g.int8 && !g.ring && c.rows > 1; }
+int f32_rows_nvt(int G, int rows) { return rows * G <= 16 ? 1 : 2; }
+
 struct Plan {
   int nsplit, chunks_per_split;
+  int nvt;     // rows kernel: vector tiles per workgroup (0: not the rows kernel)
   int cpw;     // kernel instance: chunks per wave (1, 2, 4; 0 = runtime loop)
   int nr;      // query rows per workgroup (dense int8 chunk rows; else 1)
   int zgroups; // workgroups per (split, kv head): ceil(rows / nr)
@@ -49,10 +55,13 @@ int i8_rows(const KvGeom& g, int G, int rows) {
 
 Plan plan(const KvGeom& g, const AttnCall& c) {
   const int G = c.n_heads / g.nkv;
-  const int chunk = chunk_of(g);
+  const bool rowsk = f32_rows(g, c);
+  const int chunk = rowsk ? kGranule : chunk_of(g);
   const int nkeys_max = g.ring ? c.ring.n_res : c.pos0 + c.rows;
   const int nchunks = (nkeys_max + chunk - 1) / chunk;
-  const int nr = g.int8 && !g.ring ? i8_rows(g, G, c.rows) : 1;
+  const int nvt = rowsk ? f32_rows_nvt(G, c.rows) : 0;
+  int nr = g.int8 && !g.ring ? i8_rows(g, G, c.rows) : 1;
+  if (rowsk) nr = 16 * nvt / G < c.rows ? 16 * nvt / G : c.rows;
   const int zgroups = (c.rows + nr - 1) / nr;
   const int units = g.nkv * zgroups;
   // whole waves of workgroups only: a launch of target + a few would run a
@@ -71,6 +80,7 @@ Plan plan(const KvGeom& g, const AttnCall& c) {
   if (want > kMaxSplits) want = kMaxSplits;
   if (want < 1) want = 1;
   Plan p;
+  p.nvt = nvt;
   p.nr = nr;
   p.zgroups = zgroups;
   p.chunks_per_split = (nchunks + want - 1) / want;
@@ -91,7 +101,8 @@ bool attention_supported(const KvGeom& g, int n_heads) {
 int attention_split_count(const KvGeom& g, const AttnCall& c) { return plan(g, c).nsplit; }
 
 size_t attention_counters_need(const KvGeom& g, const AttnCall& c) {
-  return plan(g, c).merge ? static_cast<size_t>(c.rows) * g.nkv * kCounterStride : 0;
+  const Plan p = plan(g, c);  // (the rows kernel's merge is a second launch: no counters)
+  return p.merge && p.nvt == 0 ? static_cast<size_t>(c.rows) * g.nkv * kCounterStride : 0;
 }
 
 size_t attention_workspace_need(const KvGeom& g, const AttnCall& c) {
@@ -106,7 +117,8 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
   const bool prod = c.rows == 1 && (c.q_bias != nullptr || c.k_bias != nullptr ||
                                     c.v_bias != nullptr || c.rope_row != nullptr);
   const Plan pl = plan(g, c);
-  void* fn = pick_kernel(g.hd, kind_of(g), G, prod, pl.cpw, pl.nr);
+  void* fn = pl.nvt > 0 ? attn_instance_f32_rows(g.hd, G, pl.nvt)
+                        : pick_kernel(g.hd, kind_of(g), G, prod, pl.cpw, pl.nr);
   if (fn == nullptr || !g.tiled) return hipErrorNotSupported;
   AttnParams p{};
   const size_t layer_heads = static_cast<size_t>(c.layer) * g.nkv;
@@ -188,6 +200,15 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
     }
   }
   void* args[] = {&p, &a};
+  if (pl.nvt > 0) {  // rows kernel: records, then the merge launch
+    void* rargs[] = {&p};
+    const hipError_t e =
+        hipLaunchKernel(fn, dim3(p.nsplit, g.nkv, pl.zgroups), dim3(kThreads), rargs, 0, st);
+    if (e != hipSuccess || !pl.merge) return e;
+    void* mfn = attn_instance_f32_rows_merge(g.hd, G);
+    if (mfn == nullptr) return hipErrorNotSupported;
+    return hipLaunchKernel(mfn, dim3(c.rows * c.n_heads), dim3(64), rargs, 0, st);
+  }
   return hipLaunchKernel(fn, dim3(p.nsplit, g.nkv, pl.zgroups), dim3(kThreads), args, 0, st);
 }
 

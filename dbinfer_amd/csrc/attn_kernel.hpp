@@ -59,7 +59,6 @@ namespace {
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxSplits = 64;  // one split per lane in the merge
-constexpr int kMergeBatch = 32;  // split records the merge loads per round
 // split-arrival counters sit 256 bytes apart: the atomics of different
 // (row, kv head) pairs never share a cache line
 constexpr int kCounterStride = 64;
@@ -1350,6 +1349,9 @@ void* attn_instance_0_1(int hd, int G, int cpw);
 void* attn_instance_1_0(int hd, int G, int cpw, int nr);
 void* attn_instance_1_1(int hd, int G, int cpw, int nr);
 void* attn_instance_i8_rows(int hd, int G, int cpw, int nr);
+// dense fp32 chunk rows (matrix-core kernel): nvt 16-vector tiles per workgroup
+void* attn_instance_f32_rows(int hd, int G, int nvt);
+void* attn_instance_f32_rows_merge(int hd, int G);
 void* attn_instance_2_0(int hd, int G, int cpw);
 void* attn_instance_2_1(int hd, int G, int cpw);
 void* attn_instance_3_0(int hd, int G, int cpw);
