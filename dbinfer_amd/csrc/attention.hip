@@ -5,12 +5,12 @@
 namespace dbi {
 namespace {
 
-void* pick_kernel(int hd, int kind, int G, bool prod = false, int cpw = 1, int nr = 1) {
+void* pick_kernel(int hd, int kind, int G, bool prod = false, int cpw = 1) {
   switch (kind * 2 + (prod ? 1 : 0)) {
     case 0: return attn_instance_0_0(hd, G, cpw);
     case 1: return attn_instance_0_1(hd, G, cpw);
-    case 2: return attn_instance_1_0(hd, G, cpw, nr);
-    case 3: return attn_instance_1_1(hd, G, cpw, nr);
+    case 2: return attn_instance_1_0(hd, G, cpw);
+    case 3: return attn_instance_1_1(hd, G, cpw);
     case 4: return attn_instance_2_0(hd, G, cpw);
     case 5: return attn_instance_2_1(hd, G, cpw);
     case 6: return attn_instance_3_0(hd, G, cpw);
@@ -29,39 +29,29 @@ int chunk_of(const KvGeom& g) { return g.int8 && !g.ring ? 2 * kGranule : kGranu
 // CU).
 constexpr int kTargetBlocks = 256;
 
-// Dense fp32 chunks of two or more rows run on the matrix-core rows kernel
-// (attn_rows.hpp): nvt 16-vector tiles per workgroup, 16 nvt / G rows each.
-bool f32_rows(const KvGeom& g, const AttnCall& c) { return !g.int8 && !g.ring && c.rows > 1; }
-int f32_rows_nvt(int G, int rows) { return rows * G <= 16 ? 1 : 2; }
+// Dense chunks of two or more rows run on the matrix-core rows kernels
+// (attn_rows.hpp for fp32, attn_i8_rows.hpp for int8): nvt 16-vector tiles
+// per workgroup, 16 nvt / G rows each.
+bool rows_kernel(const KvGeom& g, const AttnCall& c) { return !g.ring && c.rows > 1; }
+int rows_nvt(int G, int rows) { return rows * G <= 16 ? 1 : 2; }
 
 struct Plan {
   int nsplit, chunks_per_split;
   int nvt;     // rows kernel: vector tiles per workgroup (0: not the rows kernel)
   int cpw;     // kernel instance: chunks per wave (1, 2, 4; 0 = runtime loop)
-  int nr;      // query rows per workgroup (dense int8 chunk rows; else 1)
+  int nr;      // query rows per workgroup (rows kernels; else 1)
   int zgroups; // workgroups per (split, kv head): ceil(rows / nr)
   bool merge;  // several splits: the last to finish merges them
 };
 
-// Rows per workgroup of the dense int8 kernel: every row of a group shares
-// the K/V bytes of its chunks (the largest instance up to i8_max_rows).
-int i8_rows(const KvGeom& g, int G, int rows) {
-  const int qvt = 16 / (g.hd / kBlock);
-  int nr = (3 * qvt) / G;
-  if (nr > 4) nr = 4;
-  if (nr > rows) nr = rows;
-  return nr < 1 ? 1 : nr;
-}
-
 Plan plan(const KvGeom& g, const AttnCall& c) {
   const int G = c.n_heads / g.nkv;
-  const bool rowsk = f32_rows(g, c);
-  const int chunk = rowsk ? kGranule : chunk_of(g);
+  const bool rowsk = rows_kernel(g, c);
+  const int chunk = rowsk && !g.int8 ? kGranule : chunk_of(g);
   const int nkeys_max = g.ring ? c.ring.n_res : c.pos0 + c.rows;
   const int nchunks = (nkeys_max + chunk - 1) / chunk;
-  const int nvt = rowsk ? f32_rows_nvt(G, c.rows) : 0;
-  int nr = g.int8 && !g.ring ? i8_rows(g, G, c.rows) : 1;
-  if (rowsk) nr = 16 * nvt / G < c.rows ? 16 * nvt / G : c.rows;
+  const int nvt = rowsk ? rows_nvt(G, c.rows) : 0;
+  const int nr = rowsk ? (16 * nvt / G < c.rows ? 16 * nvt / G : c.rows) : 1;
   const int zgroups = (c.rows + nr - 1) / nr;
   const int units = g.nkv * zgroups;
   // whole waves of workgroups only: a launch of target + a few would run a
@@ -117,8 +107,9 @@ hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, co
   const bool prod = c.rows == 1 && (c.q_bias != nullptr || c.k_bias != nullptr ||
                                     c.v_bias != nullptr || c.rope_row != nullptr);
   const Plan pl = plan(g, c);
-  void* fn = pl.nvt > 0 ? attn_instance_f32_rows(g.hd, G, pl.nvt)
-                        : pick_kernel(g.hd, kind_of(g), G, prod, pl.cpw, pl.nr);
+  void* fn = pl.nvt > 0 ? (g.int8 ? attn_instance_i8_rows(g.hd, G, pl.nvt)
+                                  : attn_instance_f32_rows(g.hd, G, pl.nvt))
+                        : pick_kernel(g.hd, kind_of(g), G, prod, pl.cpw);
   if (fn == nullptr || !g.tiled) return hipErrorNotSupported;
   AttnParams p{};
   const size_t layer_heads = static_cast<size_t>(c.layer) * g.nkv;

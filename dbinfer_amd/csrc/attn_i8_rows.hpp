@@ -1,0 +1,409 @@
+// Dense int8 GQA attention of a few query rows at once on the matrix cores
+// (attend_dense_int8's arithmetic, model.cpp:600-661, for the causal chunk
+// rows of decode_layer_chunk, model.cpp:956-981: a speculative verify
+// round's k + 1 rows, speculative.cpp:64). Instantiated by
+// attn_inst_i8_rows.hip.
+//
+// Design (CDNA4, wave64, v_mfma_f32_16x16x32_bf16, exact bf16 products as
+// attn_mfma.hpp: codes are exact in bf16, fp32 factors are split into three
+// bf16 parts):
+//  - Grid (split, kv head, row group), 8 waves per workgroup, 32-position
+//    chunks (one K group each), chunk t -> wave t % 8. A workgroup serves
+//    NQ = 16 * NVT query vectors (row r, head g: r * G + g) of up to
+//    NR = NQ / G rows, so a C5 verify round (5 rows x 4 heads) streams the
+//    cache once.
+//  - Matrix columns are query vectors (the decode kernel's columns are
+//    (query, V block) pairs, which fill a tile with its few queries but
+//    repeat each one per block): QK^T has A = the chunk's K codes (rows:
+//    positions), B = q~ = (q * scale * log2 e) * ks in three parts, built by
+//    each lane for exactly its own operand (query lane % 16, channels
+//    32 j + 8 (lane / 16) + e) from the scaled q in LDS.
+//  - Softmax on the scores as they leave the matrix core (lane n + 16 g holds
+//    query n at positions 16 h + 4 g + i, a column's max and sum are lane-
+//    local plus two permlane swaps); those 8 positions are exactly the lane's
+//    PV A operand, so the weight of each V block b, w_b = p * vs[pos][b], is
+//    built in place (three parts) and multiplies the V codes of the two
+//    16-channel tiles of block b.
+//  - PV output: lane (channel n, group g) holds queries 4 g .. 4 g + 3; their
+//    rescale factors come from the QK lanes of those columns (ds_bpermute).
+//  - The fp32 sinks (positions < n_sink, model.cpp:612-626) are attended by
+//    wave 0 of split 0 in the epilogue; split records are merged by the rows
+//    merge launch (attn_rows.hpp).
+#pragma once
+
+#include "attn_rows.hpp"
+
+namespace dbi {
+namespace {
+
+template <int HD, int G, int NVT>
+struct I8RCfg {
+  static constexpr int NQ = 16 * NVT;       // query vectors per workgroup (padded)
+  static constexpr int NR = NQ / G;         // rows per workgroup
+  static constexpr int NBK = HD / kBlock;   // V blocks per head
+  static constexpr int NJ = HD / 32;        // QK k-steps (32 channels)
+  static constexpr int KL = HD / 64;        // K loads per granule (two k-steps each)
+  static constexpr int NTV = HD / 16;       // PV channel tiles
+  static constexpr int VL = HD / 32;        // V loads per chunk (two tiles each)
+  static constexpr int LPQ = HD / 8;        // lanes per query in the sink pass
+  static constexpr int QPP = 64 / LPQ;      // queries per sink pass
+  static constexpr int OP = HD + 4;         // LDS row pitch of a wave's outputs
+  static_assert(HD == 64 || HD == 128, "head dim");
+  static_assert(G >= 1 && G <= NQ, "query heads per kv head");
+};
+
+template <int HD, int G, int NVT>
+__global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams P) {
+  using C = I8RCfg<HD, G, NVT>;
+  constexpr int NQ = C::NQ, NR = C::NR, NBK = C::NBK, NJ = C::NJ, KL = C::KL;
+  constexpr int NTV = C::NTV, VL = C::VL, LPQ = C::LPQ, QPP = C::QPP, OP = C::OP;
+  constexpr int CHUNK = kKGroup;
+
+  __shared__ __align__(16) float s_q[NQ][HD];  // q * scale * log2 e (0 past the queries)
+  __shared__ __align__(16) float s_o[kWaves][16][OP];
+  __shared__ float s_ml[kWaves][16][2];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;  // matrix column / row group of this lane
+  const int split = blockIdx.x;
+  const int kh = blockIdx.y;
+  const int row0 = blockIdx.z * NR;            // this workgroup's rows [row0, row0 + nr)
+  const int nr = min(NR, P.rows - row0);
+  const int nqv = nr * G;                      // its query vectors
+  const int nkeys = P.pos0 + row0 + nr;        // keys of its last row
+  const int nchunks = (nkeys + CHUNK - 1) / CHUNK;
+  const int c_end = min((split + 1) * P.chunks_per_split, nchunks);
+  const size_t head = static_cast<size_t>(kh) * P.capg;
+  const int kv_bytes = P.capg * HD;
+  const rsrc_t rk = make_rsrc(P.k8 + head * HD, kv_bytes);
+  const rsrc_t rv = make_rsrc(P.v8 + head * HD, kv_bytes);
+  const int ks_bytes = P.ng * HD * 4;
+  const rsrc_t rks = make_rsrc(P.ks + static_cast<size_t>(kh) * P.ng * HD, ks_bytes);
+  const int vs_bytes = P.capg * NBK * 4;
+  const rsrc_t rvs = make_rsrc(P.vs + head * NBK, vs_bytes);
+
+  // ---- the workgroup's queries, scaled, into LDS
+  for (int idx = threadIdx.x; idx < NQ * HD / 4; idx += kThreads) {
+    const int q = idx / (HD / 4), d4 = idx % (HD / 4);
+    float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (q < nqv) {
+      x = *reinterpret_cast<const float4*>(
+          P.q + (static_cast<size_t>(row0 + q / G) * P.n_heads + kh * G + q % G) * HD + 4 * d4);
+      x.x *= P.qscale;
+      x.y *= P.qscale;
+      x.z *= P.qscale;
+      x.w *= P.qscale;
+    }
+    *reinterpret_cast<float4*>(&s_q[q][4 * d4]) = x;
+  }
+
+  // ---- one chunk's loads (K codes and the lane's K channel scales; V codes
+  // and the V block scales of the lane's 8 positions). A chunk past c_end
+  // reads at offsets past num_records: the reads return 0 and fetch nothing.
+  uint4 kc[2][KL], vc[VL];
+  float4 ksc[NJ][2];
+  float vsc[8][NBK];
+  auto issue_k = [&](int ch) {
+    const bool live = ch < c_end;
+    const int base = live ? ch * CHUNK * HD : kv_bytes;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int jp = 0; jp < KL; ++jp)
+        kc[h][jp] = __builtin_bit_cast(uint4, stream_b128(rk, base + lane * 16 + (h * KL + jp) * 1024, 0));
+    const int sb = live ? ch * HD * 4 : ks_bytes;  // the chunk's K group row of scales
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      ksc[j][0] = load_b128(rks, sb + (32 * j + 8 * grp) * 4, 0);
+      ksc[j][1] = load_b128(rks, sb + (32 * j + 8 * grp + 4) * 4, 0);
+    }
+  };
+  auto issue_v = [&](int ch) {
+    const bool live = ch < c_end;
+    const int base = live ? ch * CHUNK * HD : kv_bytes;
+#pragma unroll
+    for (int tp = 0; tp < VL; ++tp)
+      vc[tp] = __builtin_bit_cast(uint4, stream_b128(rv, base + lane * 16 + tp * 1024, 0));
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int vo = live ? ((ch * CHUNK + 16 * (s / 4) + 4 * grp + s % 4) * NBK) * 4 : vs_bytes;
+      if constexpr (NBK == 4) {
+        const float4 t = load_b128(rvs, vo, 0);
+        vsc[s][0] = t.x;
+        vsc[s][1] = t.y;
+        vsc[s][2] = t.z;
+        vsc[s][3] = t.w;
+      } else {
+        const float2 t = load_b64(rvs, vo, 0);
+        vsc[s][0] = t.x;
+        vsc[s][1] = t.y;
+      }
+    }
+  };
+
+  const int ch0 = split * P.chunks_per_split + wave;  // chunk t of this wave: ch0 + 8 t
+  issue_k(ch0);
+  issue_v(ch0);
+  __syncthreads();  // s_q
+
+  float M[NVT], l[NVT];
+  f32x4 o[NVT][NTV];
+#pragma unroll
+  for (int T = 0; T < NVT; ++T) {
+    M[T] = kMinit;
+    l[T] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NTV; ++t) o[T][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  for (int ch = ch0; ch < c_end; ch += kWaves) {
+    // products feeding split3 are rounded to fp32 first (q * ks, as the
+    // reference rounds it; p * vs): no contraction into the split's subtraction
+#pragma clang fp contract(off)
+    const int p0 = ch * CHUNK;
+    // ---- QK^T: scores of query T * 16 + col at positions 16 h + 4 grp + i
+    f32x4 sc[2][NVT];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int T = 0; T < NVT; ++T) sc[h][T] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      bf16x8 ak[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint4 w = kc[h][j / 2];
+        ak[h] = (j & 1) ? codes_bf16(w.z, w.w) : codes_bf16(w.x, w.y);
+      }
+      const float ks8[8] = {ksc[j][0].x, ksc[j][0].y, ksc[j][0].z, ksc[j][0].w,
+                            ksc[j][1].x, ksc[j][1].y, ksc[j][1].z, ksc[j][1].w};
+#pragma unroll
+      for (int T = 0; T < NVT; ++T) {
+        const float4 qa = *reinterpret_cast<const float4*>(&s_q[T * 16 + col][32 * j + 8 * grp]);
+        const float4 qb = *reinterpret_cast<const float4*>(&s_q[T * 16 + col][32 * j + 8 * grp + 4]);
+        const float q8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = q8[e] * ks8[e];
+        uint4 pt[3];
+        split3(x, pt);
+#pragma unroll
+        for (int a = 0; a < 3; ++a)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) sc[h][T] = mfma(ak[h], pt[a], sc[h][T]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    issue_k(ch + kWaves);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- online softmax per column, then the block weights (PV A operands)
+#pragma unroll
+    for (int T = 0; T < NVT; ++T) {
+      // keys of this column's row (causal: row r attends [0, pos0 + r]); the
+      // sinks (positions < n_sink) are attended from their fp32 copies
+      const int nk = P.pos0 + row0 + min(T * 16 + col, nqv - 1) / G + 1;
+      float s[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int p = p0 + 16 * (k / 4) + 4 * grp + k % 4;
+        const bool valid = p < nk && p >= P.n_sink;
+        s[k] = valid ? sc[k / 4][T][k % 4] : -INFINITY;
+      }
+      float mx = s[0];
+#pragma unroll
+      for (int k = 1; k < 8; ++k) mx = fmaxf(mx, s[k]);
+      const float mn = fmaxf(M[T], col_max(mx));
+      const float alpha = fast_exp2(M[T] - mn);
+      M[T] = mn;
+      float pk[8], ls = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        pk[k] = fast_exp2(s[k] - mn);
+        ls += pk[k];
+      }
+      l[T] = fmaf(l[T], alpha, ls);
+      // rescale of the output rows (queries 4 grp + i of this tile): the
+      // factor of column 4 grp + i, from that column's lane
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ar = __builtin_bit_cast(
+            float, __builtin_amdgcn_ds_bpermute(4 * (4 * grp + i), __builtin_bit_cast(int, alpha)));
+#pragma unroll
+        for (int t = 0; t < NTV; ++t) o[T][t][i] *= ar;
+      }
+      // ---- PV per V block: w_b = p * vs[pos][b] (masked slots exactly 0:
+      // their stale scales may be anything), three parts, against the V codes
+      // of the block's two channel tiles
+#pragma unroll
+      for (int b = 0; b < NBK; ++b) {
+        float w[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) w[k] = s[k] != -INFINITY ? pk[k] * vsc[k][b] : 0.0f;
+        uint4 aw[3];
+        split3(w, aw);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const int t = 2 * b + tt;
+          const uint4 vw = vc[t / 2];
+          const bf16x8 bv = (t & 1) ? codes_bf16(vw.z, vw.w) : codes_bf16(vw.x, vw.y);
+#pragma unroll
+          for (int a = 0; a < 3; ++a) o[T][t] = mfma(aw[a], bv, o[T][t]);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    issue_v(ch + kWaves);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // ---- per query tile: wave states to LDS, the fp32 sinks (split 0, wave 0),
+  // the cross-wave combine, then the output (single split) or the records
+  const int ns = min(P.n_sink, nkeys);  // sinks of the last row
+#pragma unroll
+  for (int T = 0; T < NVT; ++T) {
+    const float lt = col_sum(l[T]);
+    if (grp == 0) {
+      s_ml[wave][col][0] = M[T];
+      s_ml[wave][col][1] = lt;
+    }
+    // lane holds query 4 grp + i at channel 16 t + col
+#pragma unroll
+    for (int t = 0; t < NTV; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_o[wave][4 * grp + i][16 * t + col] = o[T][t][i];
+    const int q0 = T * 16;
+    const int nq = min(16, nqv - q0);  // vectors of this tile (uniform)
+    if (split == 0 && wave == 0 && ns > 0 && nq > 0) {  // wave-uniform
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const float* ksb = P.ksink + static_cast<size_t>(kh) * P.n_sink * HD;
+      const float* vsb = P.vsink + static_cast<size_t>(kh) * P.n_sink * HD;
+      const int qvl = lane / LPQ, c8 = lane % LPQ;  // query qvl of a pass, channels 8 c8 ..
+      for (int pass = 0; pass < 16; pass += QPP) {
+        const int ql = pass + qvl;
+        const bool real = ql < nq;
+        const int qc = min(ql, nq - 1);
+        const int nsq = min(P.n_sink, P.pos0 + row0 + (q0 + qc) / G + 1);  // this row's sinks
+        float qx[8], os[8];
+        {
+          const float4 a = *reinterpret_cast<const float4*>(&s_q[q0 + qc][8 * c8]);
+          const float4 b = *reinterpret_cast<const float4*>(&s_q[q0 + qc][8 * c8 + 4]);
+          qx[0] = a.x; qx[1] = a.y; qx[2] = a.z; qx[3] = a.w;
+          qx[4] = b.x; qx[5] = b.y; qx[6] = b.z; qx[7] = b.w;
+        }
+        float Ms = s_ml[0][qc][0], Ls = s_ml[0][qc][1];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) os[e] = s_o[0][qc][8 * c8 + e];
+        for (int p = 0; p < ns; ++p) {  // uniform
+          const float4* k4 = reinterpret_cast<const float4*>(ksb + p * HD + 8 * c8);
+          const float4* v4 = reinterpret_cast<const float4*>(vsb + p * HD + 8 * c8);
+          const float4 k0 = k4[0], k1 = k4[1], v0 = v4[0], v1 = v4[1];
+          const float kx[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+          const float vx[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+          float sdot = qx[0] * kx[0];
+#pragma unroll
+          for (int e = 1; e < 8; ++e) sdot += qx[e] * kx[e];
+          // sum over the LPQ lanes of the query (hd 128: a 16-lane row)
+          if constexpr (LPQ == 16) sdot += dpp<kX8>(sdot);
+          sdot += dpp<kX7>(sdot);
+          sdot += dpp<kX2>(sdot);
+          sdot += dpp<kX1>(sdot);
+          sdot = p < nsq ? sdot : -INFINITY;
+          const float mn = fmaxf(Ms, sdot);
+          const float al = fast_exp2(Ms - mn), pw = fast_exp2(sdot - mn);
+          Ms = mn;
+          Ls = fmaf(Ls, al, pw);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) os[e] = fmaf(os[e], al, pw * vx[e]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();  // every lane has read its state before any writes
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (real) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s_o[0][ql][8 * c8 + e] = os[e];
+          if (c8 == 0) {
+            s_ml[0][ql][0] = Ms;
+            s_ml[0][ql][1] = Ls;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    auto combine = [&](int ql, float& Mx, float (&f)[kWaves], float& L) {
+      float m[kWaves], lw[kWaves];
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i) {
+        m[i] = s_ml[i][ql][0];
+        lw[i] = s_ml[i][ql][1];
+      }
+      Mx = kMinit;
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i) Mx = fmaxf(Mx, m[i]);
+      L = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i) {
+        f[i] = fast_exp2(m[i] - Mx);
+        L += lw[i] * f[i];
+      }
+    };
+    auto o_of = [&](int ql, int d, const float (&f)[kWaves]) {
+      float O = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i) O += s_o[i][ql][d] * f[i];
+      return O;
+    };
+    if (nq > 0) {
+      if (P.direct) {
+        for (int idx = threadIdx.x; idx < nq * HD; idx += kThreads) {
+          const int ql = idx / HD, d = idx % HD, q = q0 + ql;
+          float Mx, f[kWaves], L;
+          combine(ql, Mx, f, L);
+          P.out[(static_cast<size_t>(row0 + q / G) * P.n_heads + kh * G + q % G) * HD + d] =
+              o_of(ql, d, f) / L;
+        }
+      } else {
+        for (int idx = threadIdx.x; idx < nq * (HD + 2); idx += kThreads) {
+          const int ql = idx < nq * HD ? idx / HD : (idx - nq * HD) >> 1;
+          const int q = q0 + ql, r = q / G, g = q % G;
+          const size_t head_base = static_cast<size_t>(row0 + r) * P.nkv + kh;
+          float* orec = P.part + head_base * record_region(P.nsplit, G, HD) +
+                        static_cast<size_t>(split) * record_floats(G, HD);
+          float Mx, f[kWaves], L;
+          combine(ql, Mx, f, L);
+          if (idx < nq * HD) {
+            const int d = idx % HD;
+            __hip_atomic_store(orec + g * HD + d, o_of(ql, d, f), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+          } else {
+            const int k = (idx - nq * HD) & 1;  // m, then l
+            __hip_atomic_store(orec + G * HD + 2 * g + k, k ? L : Mx, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+    }
+    __syncthreads();  // s_o / s_ml are rewritten by the next query tile
+  }
+}
+
+template <int HD, int NVT>
+void* pick_i8_rows_g(int G) {
+  switch (G) {
+    case 1: return reinterpret_cast<void*>(&attn_i8_rows_kernel<HD, 1, NVT>);
+    case 2: return reinterpret_cast<void*>(&attn_i8_rows_kernel<HD, 2, NVT>);
+    case 3: return reinterpret_cast<void*>(&attn_i8_rows_kernel<HD, 3, NVT>);
+    case 4: return reinterpret_cast<void*>(&attn_i8_rows_kernel<HD, 4, NVT>);
+    case 5: return reinterpret_cast<void*>(&attn_i8_rows_kernel<HD, 5, NVT>);
+    case 6: return reinterpret_cast<void*>(&attn_i8_rows_kernel<HD, 6, NVT>);
+    case 7: return reinterpret_cast<void*>(&attn_i8_rows_kernel<HD, 7, NVT>);
+    case 8: return reinterpret_cast<void*>(&attn_i8_rows_kernel<HD, 8, NVT>);
+    default: return nullptr;
+  }
+}
+
+}  // namespace
+}  // namespace dbi

@@ -4,8 +4,7 @@
 
 namespace dbi {
 
-void* attn_instance_1_0(int hd, int G, int cpw, int nr) {
-  if (nr != 1) return attn_instance_i8_rows(hd, G, cpw, nr);
+void* attn_instance_1_0(int hd, int G, int cpw) {
   return hd == 64 ? pick_i8<64, false, 1>(G, cpw) : hd == 128 ? pick_i8<128, false, 1>(G, cpw) : nullptr;
 }
 

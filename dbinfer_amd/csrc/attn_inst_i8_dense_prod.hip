@@ -4,8 +4,7 @@
 
 namespace dbi {
 
-void* attn_instance_1_1(int hd, int G, int cpw, int nr) {
-  if (nr != 1) return nullptr;
+void* attn_instance_1_1(int hd, int G, int cpw) {
   return hd == 64 ? pick_i8<64, true, 1>(G, cpw) : hd == 128 ? pick_i8<128, true, 1>(G, cpw) : nullptr;
 }
 

@@ -1345,10 +1345,11 @@ void* pick_g(int G, int cpw) {
 // one per layout and producer flag, each in its own translation unit
 void* attn_instance_0_0(int hd, int G, int cpw);
 void* attn_instance_0_1(int hd, int G, int cpw);
-// dense int8 (matrix-core kernel): nr query rows per workgroup
-void* attn_instance_1_0(int hd, int G, int cpw, int nr);
-void* attn_instance_1_1(int hd, int G, int cpw, int nr);
-void* attn_instance_i8_rows(int hd, int G, int cpw, int nr);
+// dense int8 (matrix-core kernel, one query row per workgroup)
+void* attn_instance_1_0(int hd, int G, int cpw);
+void* attn_instance_1_1(int hd, int G, int cpw);
+// dense int8 chunk rows (matrix-core kernel): nvt 16-vector tiles per workgroup
+void* attn_instance_i8_rows(int hd, int G, int nvt);
 // dense fp32 chunk rows (matrix-core kernel): nvt 16-vector tiles per workgroup
 void* attn_instance_f32_rows(int hd, int G, int nvt);
 void* attn_instance_f32_rows_merge(int hd, int G);

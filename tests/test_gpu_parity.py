@@ -292,8 +292,9 @@ def test_chunk_attention(dtype, nh, nkv, hd, pos0, n):
     assert_close(got, want, what=f"chunk dtype{dtype} pos0 {pos0} n {n}")
 
 
+@pytest.mark.parametrize("dtype", [F32, INT8])
 @pytest.mark.parametrize("nh,nkv,hd,pos0,n", [
-    (32, 8, 128, 0, 3),        # one tile, one split: direct output
+    (32, 8, 128, 0, 3),        # one chunk, one split: direct output; int8: rows see 1..3 sinks
     (16, 8, 128, 17, 2),       # gqa 2: one 16-vector tile
     (40, 8, 64, 33, 6),        # gqa 5: 30 vectors in two tiles
     (28, 4, 128, 4000, 5),     # gqa 7: two row groups (4 + 1)
@@ -301,15 +302,16 @@ def test_chunk_attention(dtype, nh, nkv, hd, pos0, n):
     (8, 8, 64, 5, 63),         # gqa 1: two row groups (32 + 31)
     (32, 8, 128, 16379, 5),    # config 5's verify round at 16k (32 splits)
 ])
-def test_chunk_rows_f32(nh, nkv, hd, pos0, n):
-    """Dense fp32 chunks of 2..63 rows run on the matrix-core rows kernel
-    (model.cpp:956-981); every row group, split plan and the direct path."""
-    g, o = pair(1, pos0 + n + 64, nkv, hd, n_sink=4, dtype=F32)
-    fill_both(g, o, 1, pos0 + n, 70 + n)
+def test_chunk_rows(dtype, nh, nkv, hd, pos0, n):
+    """Dense chunks of 2..63 rows (model.cpp:956-981) run on the matrix-core
+    rows kernels (fp32; int8 with 4 fp32 sinks and 1% outlier channels x8);
+    every row group, split plan and the direct path."""
+    g, o = pair(1, pos0 + n + 64, nkv, hd, n_sink=4, dtype=dtype)
+    fill_both(g, o, 1, pos0 + n, 70 + n, outlier=dtype == INT8)
     q = normal(71, n, nh * hd)
     got = g.attend_chunk(0, pos0, q, nh, scale_of(hd))
     want = o.attend_chunk(0, pos0, q, nh, scale_of(hd), n_threads=8)
-    assert_close(got, want, what=f"rows pos0 {pos0} n {n} gqa {nh // nkv}")
+    assert_close(got, want, what=f"rows dtype {dtype} pos0 {pos0} n {n} gqa {nh // nkv}")
     # a second call on the same workspace (split counters back at zero)
     again = g.attend_chunk(0, pos0, q, nh, scale_of(hd))
     assert np.array_equal(again, got)
