@@ -75,7 +75,8 @@ Plan plan(const KvGeom& g, const AttnCall& c) {
   p.zgroups = zgroups;
   p.chunks_per_split = (nchunks + want - 1) / want;
   p.nsplit = (nchunks + p.chunks_per_split - 1) / p.chunks_per_split;
-  p.merge = p.nsplit > 1;
+  // (dense int8 rows: the merge launch also attends the fp32 sinks)
+  p.merge = p.nsplit > 1 || (rowsk && g.int8 && g.n_sink > 0);
   const int per_wave = (p.chunks_per_split + wpg - 1) / wpg;
   p.cpw = per_wave <= 1 ? 1 : per_wave <= 2 ? 2 : per_wave <= 4 ? 4 : 0;
   return p;

@@ -26,9 +26,9 @@
 //    16-channel tiles of block b.
 //  - PV output: lane (channel n, group g) holds queries 4 g .. 4 g + 3; their
 //    rescale factors come from the QK lanes of those columns (ds_bpermute).
-//  - The fp32 sinks (positions < n_sink, model.cpp:612-626) are attended by
-//    wave 0 of split 0 in the epilogue; split records are merged by the rows
-//    merge launch (attn_rows.hpp).
+//  - The fp32 sinks (positions < n_sink, model.cpp:612-626) are masked in
+//    the stream and attended by the rows merge launch (attn_rows.hpp), which
+//    merges the split records; with sinks there is always a merge launch.
 #pragma once
 
 #include "attn_rows.hpp"
@@ -45,8 +45,6 @@ struct I8RCfg {
   static constexpr int KL = HD / 64;        // K loads per granule (two k-steps each)
   static constexpr int NTV = HD / 16;       // PV channel tiles
   static constexpr int VL = HD / 32;        // V loads per chunk (two tiles each)
-  static constexpr int LPQ = HD / 8;        // lanes per query in the sink pass
-  static constexpr int QPP = 64 / LPQ;      // queries per sink pass
   static constexpr int OP = HD + 4;         // LDS row pitch of a wave's outputs
   static_assert(HD == 64 || HD == 128, "head dim");
   static_assert(G >= 1 && G <= NQ, "query heads per kv head");
@@ -56,7 +54,7 @@ template <int HD, int G, int NVT>
 __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams P) {
   using C = I8RCfg<HD, G, NVT>;
   constexpr int NQ = C::NQ, NR = C::NR, NBK = C::NBK, NJ = C::NJ, KL = C::KL;
-  constexpr int NTV = C::NTV, VL = C::VL, LPQ = C::LPQ, QPP = C::QPP, OP = C::OP;
+  constexpr int NTV = C::NTV, VL = C::VL, OP = C::OP;
   constexpr int CHUNK = kKGroup;
 
   __shared__ __align__(16) float s_q[NQ][HD];  // q * scale * log2 e (0 past the queries)
@@ -101,6 +99,9 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
   // ---- one chunk's loads (K codes and the lane's K channel scales; V codes
   // and the V block scales of the lane's 8 positions). A chunk past c_end
   // reads at offsets past num_records: the reads return 0 and fetch nothing.
+  // So do the V scales of sink positions and of positions past the group's
+  // last key: their weights are then exactly 0 (the masked scores give p = 0,
+  // and a stale scale there may be anything).
   uint4 kc[2][KL], vc[VL];
   float4 ksc[NJ][2];
   float vsc[8][NBK];
@@ -127,7 +128,8 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
       vc[tp] = __builtin_bit_cast(uint4, stream_b128(rv, base + lane * 16 + tp * 1024, 0));
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const int vo = live ? ((ch * CHUNK + 16 * (s / 4) + 4 * grp + s % 4) * NBK) * 4 : vs_bytes;
+      const int p = ch * CHUNK + 16 * (s / 4) + 4 * grp + s % 4;
+      const int vo = live && p >= P.n_sink && p < nkeys ? p * NBK * 4 : vs_bytes;
       if constexpr (NBK == 4) {
         const float4 t = load_b128(rvs, vo, 0);
         vsc[s][0] = t.x;
@@ -233,14 +235,14 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
 #pragma unroll
         for (int t = 0; t < NTV; ++t) o[T][t][i] *= ar;
       }
-      // ---- PV per V block: w_b = p * vs[pos][b] (masked slots exactly 0:
-      // their stale scales may be anything), three parts, against the V codes
-      // of the block's two channel tiles
+      // ---- PV per V block: w_b = p * vs[pos][b] (masked slots: p = 0, and
+      // outside the group's keys vs = 0), three parts, against the V codes of
+      // the block's two channel tiles
 #pragma unroll
       for (int b = 0; b < NBK; ++b) {
         float w[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) w[k] = s[k] != -INFINITY ? pk[k] * vsc[k][b] : 0.0f;
+        for (int k = 0; k < 8; ++k) w[k] = pk[k] * vsc[k][b];
         uint4 aw[3];
         split3(w, aw);
 #pragma unroll
@@ -258,9 +260,8 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // ---- per query tile: wave states to LDS, the fp32 sinks (split 0, wave 0),
-  // the cross-wave combine, then the output (single split) or the records
-  const int ns = min(P.n_sink, nkeys);  // sinks of the last row
+  // ---- per query tile: wave states to LDS, the cross-wave combine, then the
+  // output (single split, no sinks) or the records
 #pragma unroll
   for (int T = 0; T < NVT; ++T) {
     const float lt = col_sum(l[T]);
@@ -275,63 +276,6 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
       for (int i = 0; i < 4; ++i) s_o[wave][4 * grp + i][16 * t + col] = o[T][t][i];
     const int q0 = T * 16;
     const int nq = min(16, nqv - q0);  // vectors of this tile (uniform)
-    if (split == 0 && wave == 0 && ns > 0 && nq > 0) {  // wave-uniform
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const float* ksb = P.ksink + static_cast<size_t>(kh) * P.n_sink * HD;
-      const float* vsb = P.vsink + static_cast<size_t>(kh) * P.n_sink * HD;
-      const int qvl = lane / LPQ, c8 = lane % LPQ;  // query qvl of a pass, channels 8 c8 ..
-      for (int pass = 0; pass < 16; pass += QPP) {
-        const int ql = pass + qvl;
-        const bool real = ql < nq;
-        const int qc = min(ql, nq - 1);
-        const int nsq = min(P.n_sink, P.pos0 + row0 + (q0 + qc) / G + 1);  // this row's sinks
-        float qx[8], os[8];
-        {
-          const float4 a = *reinterpret_cast<const float4*>(&s_q[q0 + qc][8 * c8]);
-          const float4 b = *reinterpret_cast<const float4*>(&s_q[q0 + qc][8 * c8 + 4]);
-          qx[0] = a.x; qx[1] = a.y; qx[2] = a.z; qx[3] = a.w;
-          qx[4] = b.x; qx[5] = b.y; qx[6] = b.z; qx[7] = b.w;
-        }
-        float Ms = s_ml[0][qc][0], Ls = s_ml[0][qc][1];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) os[e] = s_o[0][qc][8 * c8 + e];
-        for (int p = 0; p < ns; ++p) {  // uniform
-          const float4* k4 = reinterpret_cast<const float4*>(ksb + p * HD + 8 * c8);
-          const float4* v4 = reinterpret_cast<const float4*>(vsb + p * HD + 8 * c8);
-          const float4 k0 = k4[0], k1 = k4[1], v0 = v4[0], v1 = v4[1];
-          const float kx[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-          const float vx[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-          float sdot = qx[0] * kx[0];
-#pragma unroll
-          for (int e = 1; e < 8; ++e) sdot += qx[e] * kx[e];
-          // sum over the LPQ lanes of the query (hd 128: a 16-lane row)
-          if constexpr (LPQ == 16) sdot += dpp<kX8>(sdot);
-          sdot += dpp<kX7>(sdot);
-          sdot += dpp<kX2>(sdot);
-          sdot += dpp<kX1>(sdot);
-          sdot = p < nsq ? sdot : -INFINITY;
-          const float mn = fmaxf(Ms, sdot);
-          const float al = fast_exp2(Ms - mn), pw = fast_exp2(sdot - mn);
-          Ms = mn;
-          Ls = fmaf(Ls, al, pw);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) os[e] = fmaf(os[e], al, pw * vx[e]);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();  // every lane has read its state before any writes
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (real) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) s_o[0][ql][8 * c8 + e] = os[e];
-          if (c8 == 0) {
-            s_ml[0][ql][0] = Ms;
-            s_ml[0][ql][1] = Ls;
-          }
-        }
-      }
-    }
     __syncthreads();
     auto combine = [&](int ql, float& Mx, float (&f)[kWaves], float& L) {
       float m[kWaves], lw[kWaves];

@@ -365,7 +365,10 @@ __device__ __forceinline__ void finish(const AttnParams& P, float (&s_o)[kWaves]
 // (DPP max / sum); the o records are read 16 bytes per lane, HD / 4 lanes
 // per record, so one load instruction covers 64 / (HD / 4) splits, every
 // load of the merge in one round. Records are read at device coherence.
-template <int HD, int G>
+// SINKS: the dense int8 fp32 sinks (positions < n_sink, model.cpp:612-626)
+// of this row are attended here too (the rows kernels leave them to the
+// merge): their scores join the split maxima, their V rows the sum.
+template <int HD, int G, bool SINKS = false>
 __device__ __forceinline__ void merge_head(const AttnParams& P, int kh, int qrow, int g, int lane) {
   constexpr int kSC1 = 16;  // cache policy: agent-coherent load
   constexpr int LPH = HD / 4;       // lanes per record of one head
@@ -391,9 +394,50 @@ __device__ __forceinline__ void merge_head(const AttnParams& P, int kh, int qrow
                                                         kSC1));
     }
   }
-  const float M = wave_max(on ? ml.x : kMinit);
+  // the sinks' scores (uniform): q * scale * log2 e (as the kernels scale it)
+  // against each sink's K row, dims lane and lane + 64 of each lane
+  constexpr int SB = 4;  // sinks whose loads go out together and stay in registers
+  constexpr int DPL = HD / 64;
+  const int nsq = SINKS ? min(P.n_sink, P.pos0 + qrow + 1) : 0;  // this row's sinks
+  const float* ksb = SINKS ? P.ksink + static_cast<size_t>(kh) * P.n_sink * HD : nullptr;
+  const float* vsb = SINKS ? P.vsink + static_cast<size_t>(kh) * P.n_sink * HD : nullptr;
+  float Ms = kMinit;
+  float qd[DPL];
+  float sd0[SB];   // scores of the first SB sinks (uniform), their V rows (dims 4 lane ..)
+  float4 vx0[SB];
+  auto sink_dot = [&](const float (&kx)[DPL]) {
+    float sd = qd[0] * kx[0];
+#pragma unroll
+    for (int u = 1; u < DPL; ++u) sd += qd[u] * kx[u];
+    return wave_sum(sd);
+  };
+  if constexpr (SINKS) {
+    const float* qp = P.q + (static_cast<size_t>(qrow) * P.n_heads + kh * G + g) * HD;
+#pragma unroll
+    for (int u = 0; u < DPL; ++u) qd[u] = qp[lane + 64 * u] * P.qscale;
+    float kx[SB][DPL];
+#pragma unroll
+    for (int b = 0; b < SB; ++b) {
+      const int p = min(b, nsq - 1);
+#pragma unroll
+      for (int u = 0; u < DPL; ++u) kx[b][u] = ksb[p * HD + lane + 64 * u];
+      vx0[b] = *reinterpret_cast<const float4*>(vsb + p * HD + 4 * (lane % LPH));
+    }
+#pragma unroll
+    for (int b = 0; b < SB; ++b) {
+      sd0[b] = sink_dot(kx[b]);
+      if (b < nsq) Ms = fmaxf(Ms, sd0[b]);
+    }
+    for (int pb = SB; pb < nsq; ++pb) {  // further sinks (uniform), one at a time
+      float ky[DPL];
+#pragma unroll
+      for (int u = 0; u < DPL; ++u) ky[u] = ksb[pb * HD + lane + 64 * u];
+      Ms = fmaxf(Ms, sink_dot(ky));
+    }
+  }
+  const float M = fmaxf(wave_max(on ? ml.x : kMinit), Ms);
   const float w = on ? fast_exp2(ml.x - M) : 0.0f;  // splits past nsplit weigh 0
-  const float L = wave_sum(on ? ml.y * w : 0.0f);
+  float L = wave_sum(on ? ml.y * w : 0.0f);
   float4 acc[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
   auto lane_w = [&](int sp) {  // weight of split sp (scalar: readlane)
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), sp));
@@ -418,6 +462,27 @@ __device__ __forceinline__ void merge_head(const AttnParams& P, int kh, int qrow
   for (int e = 0; e < 4; ++e) {
     o4[e] = swap32_sum(o4[e], o4[e]);
     if constexpr (SPI == 4) o4[e] = swap16_sum(o4[e], o4[e]);
+  }
+  if constexpr (SINKS) {
+    // the sinks' weights against M, and their V rows (dims 4 lane .. of the
+    // lanes holding the output)
+    auto add_sink = [&](float sd, const float4& v) {
+      const float pw = fast_exp2(sd - M);
+      L += pw;
+      o4[0] = fmaf(pw, v.x, o4[0]);
+      o4[1] = fmaf(pw, v.y, o4[1]);
+      o4[2] = fmaf(pw, v.z, o4[2]);
+      o4[3] = fmaf(pw, v.w, o4[3]);
+    };
+#pragma unroll
+    for (int b = 0; b < SB; ++b)
+      if (b < nsq) add_sink(sd0[b], vx0[b]);
+    for (int pb = SB; pb < nsq; ++pb) {  // further sinks: scores recomputed as above
+      float ky[DPL];
+#pragma unroll
+      for (int u = 0; u < DPL; ++u) ky[u] = ksb[pb * HD + lane + 64 * u];
+      add_sink(sink_dot(ky), *reinterpret_cast<const float4*>(vsb + pb * HD + 4 * (lane % LPH)));
+    }
   }
   if (lane < LPH) {
     const size_t h = static_cast<size_t>(qrow) * P.n_heads + kh * G + g;

@@ -313,15 +313,19 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P)
 }
 
 // The split merge of a rows launch, as a second launch: one wave per (row,
-// head) pair, merge_head() over the pair's split records. The records of a
-// row group come from workgroups on every XCD, and one workgroup merging all
-// of them (as the decode kernel's last arriver does) is bound by the
-// bandwidth of its single CU; one workgroup per pair spreads the reads.
+// head) pair, merge_head() over the pair's split records (and, dense int8,
+// the row's fp32 sinks). The records of a row group come from workgroups on
+// every XCD, and one workgroup merging all of them (as the decode kernel's
+// last arriver does) is bound by the bandwidth of its single CU; one
+// workgroup per pair spreads the reads.
 template <int HD, int G>
 __global__ __launch_bounds__(64) void attn_rows_merge(const AttnParams P) {
   const int pr = blockIdx.x;  // (row, kv head, head) pair
   const int g = pr % G, kh = (pr / G) % P.nkv, qrow = pr / (G * P.nkv);
-  merge_head<HD, G>(P, kh, qrow, g, threadIdx.x);
+  if (P.n_sink > 0)
+    merge_head<HD, G, true>(P, kh, qrow, g, threadIdx.x);
+  else
+    merge_head<HD, G, false>(P, kh, qrow, g, threadIdx.x);
 }
 
 template <int HD, int NVT>

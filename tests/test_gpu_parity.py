@@ -293,20 +293,21 @@ def test_chunk_attention(dtype, nh, nkv, hd, pos0, n):
 
 
 @pytest.mark.parametrize("dtype", [F32, INT8])
-@pytest.mark.parametrize("nh,nkv,hd,pos0,n", [
-    (32, 8, 128, 0, 3),        # one chunk, one split: direct output; int8: rows see 1..3 sinks
-    (16, 8, 128, 17, 2),       # gqa 2: one 16-vector tile
-    (40, 8, 64, 33, 6),        # gqa 5: 30 vectors in two tiles
-    (28, 4, 128, 4000, 5),     # gqa 7: two row groups (4 + 1)
-    (32, 4, 64, 1000, 40),     # gqa 8: ten row groups
-    (8, 8, 64, 5, 63),         # gqa 1: two row groups (32 + 31)
-    (32, 8, 128, 16379, 5),    # config 5's verify round at 16k (32 splits)
+@pytest.mark.parametrize("nh,nkv,hd,pos0,n,ns", [
+    (32, 8, 128, 0, 3, 4),        # one chunk, one split: direct output; int8: rows see 1..3 sinks
+    (16, 8, 128, 17, 2, 4),       # gqa 2: one 16-vector tile
+    (40, 8, 64, 33, 6, 4),        # gqa 5: 30 vectors in two tiles
+    (28, 4, 128, 4000, 5, 4),     # gqa 7: two row groups (4 + 1)
+    (32, 4, 64, 1000, 40, 4),     # gqa 8: ten row groups
+    (8, 8, 64, 5, 63, 4),         # gqa 1: two row groups (32 + 31)
+    (32, 8, 128, 16379, 5, 4),    # config 5's verify round at 16k (32 splits)
+    (32, 8, 128, 4, 6, 9),        # int8: rows see 5..9 sinks (more than the merge holds at once)
 ])
-def test_chunk_rows(dtype, nh, nkv, hd, pos0, n):
+def test_chunk_rows(dtype, nh, nkv, hd, pos0, n, ns):
     """Dense chunks of 2..63 rows (model.cpp:956-981) run on the matrix-core
-    rows kernels (fp32; int8 with 4 fp32 sinks and 1% outlier channels x8);
+    rows kernels (fp32; int8 with fp32 sinks and 1% outlier channels x8);
     every row group, split plan and the direct path."""
-    g, o = pair(1, pos0 + n + 64, nkv, hd, n_sink=4, dtype=dtype)
+    g, o = pair(1, pos0 + n + 64, nkv, hd, n_sink=ns, dtype=dtype)
     fill_both(g, o, 1, pos0 + n, 70 + n, outlier=dtype == INT8)
     q = normal(71, n, nh * hd)
     got = g.attend_chunk(0, pos0, q, nh, scale_of(hd))
