@@ -24,7 +24,7 @@ DBI_ERR_FORMAT = 6
 
 DBI_KV_F32 = 0
 DBI_KV_INT8 = 1
-DBI_W_F32, DBI_W_F16, DBI_W_Q8_0 = 0, 1, 8
+DBI_W_F32, DBI_W_F16, DBI_W_Q4_0, DBI_W_Q8_0 = 0, 1, 2, 8
 
 EXPORT = {
     "k": 0, "v": 1, "k8": 2, "v8": 3, "k_scale": 4, "v_scale": 5,
@@ -49,6 +49,25 @@ _u32 = ctypes.c_uint32
 _f32 = ctypes.c_float
 _vp = ctypes.c_void_p
 _st = ctypes.c_int32
+
+
+class Weight(ctypes.Structure):
+    """dbi_weight: device data and its type (DBI_W_*)."""
+    _fields_ = [("data", _vp), ("type", _u32)]
+
+
+class LayerWeights(ctypes.Structure):
+    """dbi_layer_weights (backend::LayerQ's pointers), device memory."""
+    _fields_ = [("attn_norm", _vp), ("ffn_norm", _vp),
+                ("wq", Weight), ("wk", Weight), ("wv", Weight), ("wo", Weight),
+                ("wgate", Weight), ("wup", Weight), ("wdown", Weight),
+                ("bq", _vp), ("bk", _vp), ("bv", _vp)]
+
+
+class OffloadConfig(ctypes.Structure):
+    """dbi_offload_config."""
+    _fields_ = [("dim", _u32), ("ff", _u32), ("n_heads", _u32), ("rms_eps", _f32),
+                ("output_norm", _vp), ("lm_head", Weight), ("vocab", _u32)]
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -81,6 +100,10 @@ SIGNATURES = {
     "dbi_spec_verify_async": (_st, [_vp, _u32, _u32, _vp, _vp, _vp, _vp]),
     "dbi_kv_verify_commit": (_st, [_vp, _u32, _u32, _u32, _vp, _vp, _vp, _vp]),
     "dbi_oproj_residual_async": (_st, [_vp, _u32, _vp, _vp, _vp, _u32, _u32]),
+    "dbi_offload_setup": (_st, [_vp, ctypes.POINTER(OffloadConfig), ctypes.POINTER(LayerWeights),
+                                _u32]),
+    "dbi_decode_token_async": (_st, [_vp, _vp, _u32]),
+    "dbi_decode_token_full_async": (_st, [_vp, _vp, _u32, _vp]),
     "dbi_kv_prefix_save": (_st, [_vp, ctypes.c_char_p, _vp, _u32]),
     "dbi_kv_prefix_load": (_st, [_vp, ctypes.c_char_p, _vp, _u32, ctypes.POINTER(_u32)]),
     "dbi_kv_export_bytes": (ctypes.c_size_t, [_vp, _u32]),

@@ -10,11 +10,21 @@
 
 #include "kv_internal.hpp"
 
+// The full-layer offload's bound blocks and scratch rows (dbi_offload_setup).
+struct OffloadState {
+  dbi_offload_config cfg{};
+  std::vector<dbi_layer_weights> layers;
+  float* buf = nullptr;  // one allocation: the rows below
+  float *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
+  float *gate = nullptr, *up = nullptr;
+};
+
 struct dbi_kv {
   dbi_kv_config cfg{};
   dbi::KvGeom geom{};
   dbi::KvStore store{};
   dbi::Workspace ws{};
+  OffloadState off;
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;
   uint32_t n_seen = 0;
@@ -400,6 +410,81 @@ dbi_status decode_qkv_impl(dbi_kv* kv, uint32_t layer, uint32_t pos, uint32_t n_
   return DBI_OK;
 }
 
+// matvec arguments of dbi_oproj_residual_async and the offload: weight type,
+// alignment (fp32/f16 16 bytes, Q8_0/Q4_0 4), in a multiple of 8 (32 for the
+// quantized types, whose activation row sits in LDS: in <= 32768), the
+// activation 16-byte aligned (x == nullptr: the handle's own rows)
+dbi_status check_matvec(uint32_t wtype, const void* w, const void* x, uint32_t out, uint32_t in,
+                        const char* what) {
+  if (w == nullptr) return fail(DBI_ERR_INVALID, std::string(what) + ": null weight");
+  if (wtype != DBI_W_F32 && wtype != DBI_W_F16 && wtype != DBI_W_Q8_0 && wtype != DBI_W_Q4_0)
+    return fail(DBI_ERR_UNSUPPORTED,
+                std::string(what) + ": the matvecs serve fp32, f16, Q8_0 and Q4_0 weights only");
+  const bool quant = wtype == DBI_W_Q8_0 || wtype == DBI_W_Q4_0;
+  const uint32_t mult = quant ? 32 : 8;
+  const uint32_t max_in = quant ? (uint32_t(1) << 15) : (uint32_t(1) << 24);
+  if (out == 0 || in == 0 || in % mult != 0 || out > (uint32_t(1) << 30) || in > max_in)
+    return fail(DBI_ERR_INVALID, std::string(what) +
+                                     ": needs dim in [1, 2^30] and in a positive multiple of " +
+                                     std::to_string(mult) + " (at most " +
+                                     std::to_string(max_in) + ")");
+  const uintptr_t walign = quant ? 3 : 15;
+  if ((reinterpret_cast<uintptr_t>(w) & walign) != 0 ||
+      (x != nullptr && (reinterpret_cast<uintptr_t>(x) & 15) != 0))
+    return fail(DBI_ERR_INVALID, std::string(what) +
+                                     ": needs aligned weights (16 bytes; Q8_0, Q4_0: 4) and a "
+                                     "16-byte aligned activation row");
+  return DBI_OK;
+}
+
+hipError_t run_matvec(dbi_kv* kv, const dbi_weight& w, const float* x, float* y, uint32_t out,
+                      uint32_t in, bool accumulate) {
+  dbi::OprojCall c{};
+  c.w = w.data;
+  c.attn = x;
+  c.x = y;
+  c.dim = static_cast<int>(out);
+  c.in = static_cast<int>(in);
+  c.f16 = w.type == DBI_W_F16;
+  c.q8 = w.type == DBI_W_Q8_0;
+  c.q4 = w.type == DBI_W_Q4_0;
+  c.overwrite = !accumulate;
+  return dbi::launch_oproj(c, kv->stream);
+}
+
+// Model::decode_layer (model.cpp:730-787) for every bound block at pos, on
+// the handle's stream. All checks come first; the q/k/v step is the
+// producer's fused decode (decode_qkv_impl).
+dbi_status decode_token_impl(dbi_kv* kv, float* x, uint32_t pos) {
+  const OffloadState& o = kv->off;
+  if (o.layers.empty()) return fail(DBI_ERR_INVALID, "decode_token needs dbi_offload_setup first");
+  if (x == nullptr || (reinterpret_cast<uintptr_t>(x) & 15) != 0)
+    return fail(DBI_ERR_INVALID, "decode_token needs a 16-byte aligned residual row");
+  if (dbi_status st = check_rows(kv, pos, 1)) return st;
+  const uint32_t hd = kv->cfg.head_dim, nkv = kv->cfg.n_kv_heads, nh = o.cfg.n_heads;
+  const uint32_t dim = o.cfg.dim, ff = o.cfg.ff, qn = nh * hd, kvn = nkv * hd;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+  hipStream_t st = kv->stream;
+  for (uint32_t l = 0; l < o.layers.size(); ++l) {
+    const dbi_layer_weights& L = o.layers[l];
+    HIP_TRY(dbi::launch_rmsnorm(x, L.attn_norm, o.cfg.rms_eps, o.normed, int(dim), st),
+            "rmsnorm launch");
+    HIP_TRY(run_matvec(kv, L.wq, o.normed, o.q, qn, dim, false), "q matvec launch");
+    HIP_TRY(run_matvec(kv, L.wk, o.normed, o.k, kvn, dim, false), "k matvec launch");
+    HIP_TRY(run_matvec(kv, L.wv, o.normed, o.v, kvn, dim, false), "v matvec launch");
+    const RawQkv r{o.q, o.k, o.v, L.bq, L.bk, L.bv};
+    if (dbi_status s2 = decode_qkv_impl(kv, l, pos, nh, scale, r, o.attn)) return s2;
+    HIP_TRY(run_matvec(kv, L.wo, o.attn, x, dim, qn, true), "o_proj launch");
+    HIP_TRY(dbi::launch_rmsnorm(x, L.ffn_norm, o.cfg.rms_eps, o.normed, int(dim), st),
+            "rmsnorm launch");
+    HIP_TRY(run_matvec(kv, L.wgate, o.normed, o.gate, ff, dim, false), "gate matvec launch");
+    HIP_TRY(run_matvec(kv, L.wup, o.normed, o.up, ff, dim, false), "up matvec launch");
+    HIP_TRY(dbi::launch_silu_mul(o.gate, o.up, int(ff), st), "silu launch");
+    HIP_TRY(run_matvec(kv, L.wdown, o.gate, x, dim, ff, true), "down matvec launch");
+  }
+  return DBI_OK;
+}
+
 // decode_layer_chunk (model.cpp:933-981) from the projections: produce all n
 // rows, append them, then the causal chunk attention.
 dbi_status chunk_qkv_impl(dbi_kv* kv, uint32_t layer, uint32_t pos0, uint32_t n,
@@ -622,6 +707,7 @@ void dbi_kv_destroy(dbi_kv* kv) {
   (void)hipStreamSynchronize(kv->stream);
   free_store(kv->store);
   free_ws(kv->ws);
+  if (kv->off.buf) (void)hipFree(kv->off.buf);
   if (kv->own_stream) (void)hipStreamDestroy(kv->own_stream);
   delete kv;
 }
@@ -1361,32 +1447,103 @@ dbi_status dbi_oproj_residual_async(dbi_kv* kv, uint32_t wtype, const void* w_de
   if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
   if (w_dev == nullptr || attn_dev == nullptr || x_dev == nullptr)
     return fail(DBI_ERR_INVALID, "null output-projection argument");
-  if (wtype != DBI_W_F32 && wtype != DBI_W_F16 && wtype != DBI_W_Q8_0)
-    return fail(DBI_ERR_UNSUPPORTED,
-                "output projection serves fp32, f16 and Q8_0 weights only");
-  // Q8_0 keeps the quantized activation row in LDS (36 bytes per 32 floats):
-  // at most 36 KB, within a launch's default dynamic LDS
-  const uint32_t mult = wtype == DBI_W_Q8_0 ? 32 : 8;
-  const uint32_t max_in = wtype == DBI_W_Q8_0 ? (uint32_t(1) << 15) : (uint32_t(1) << 24);
-  if (dim == 0 || in == 0 || in % mult != 0 || dim > (uint32_t(1) << 30) || in > max_in)
+  if (dbi_status st = check_matvec(wtype, w_dev, attn_dev, dim, in, "output projection"))
+    return st;
+  HIP_TRY(run_matvec(kv, dbi_weight{w_dev, wtype}, attn_dev, x_dev, dim, in, true),
+          "output projection launch");
+  return DBI_OK;
+}
+
+// ---------------------------------------------------------------------------
+// full-layer offload (backend.hpp:133-157; model.cpp:730-787, 896-917)
+
+dbi_status dbi_offload_setup(dbi_kv* kv, const dbi_offload_config* cfg,
+                             const dbi_layer_weights* layers, uint32_t n_layers) {
+  if (kv == nullptr || cfg == nullptr || layers == nullptr)
+    return fail(DBI_ERR_INVALID, "null offload argument");
+  const uint32_t nkv = kv->cfg.n_kv_heads, hd = kv->cfg.head_dim;
+  if (n_layers == 0 || n_layers > kv->cfg.n_layers)
+    return fail(DBI_ERR_INVALID, "offload needs 1 to n_layers blocks");
+  if (cfg->dim == 0 || cfg->ff == 0 || cfg->n_heads == 0 || cfg->n_heads % nkv != 0 ||
+      cfg->dim > (uint32_t(1) << 20) || cfg->ff > (uint32_t(1) << 20) ||
+      cfg->n_heads > 4096)
     return fail(DBI_ERR_INVALID,
-                "output projection needs dim in [1, 2^30] and in a positive multiple of " +
-                    std::to_string(mult) + " (at most " + std::to_string(max_in) + ")");
-  const uintptr_t walign = wtype == DBI_W_Q8_0 ? 3 : 15;
-  if ((reinterpret_cast<uintptr_t>(w_dev) & walign) != 0 ||
-      (reinterpret_cast<uintptr_t>(attn_dev) & 15) != 0)
-    return fail(DBI_ERR_INVALID,
-                "output projection needs aligned weights (16 bytes; Q8_0: 4) and a 16-byte "
-                "aligned attn");
-  dbi::OprojCall c{};
-  c.w = w_dev;
-  c.attn = attn_dev;
-  c.x = x_dev;
-  c.dim = static_cast<int>(dim);
-  c.in = static_cast<int>(in);
-  c.f16 = wtype == DBI_W_F16;
-  c.q8 = wtype == DBI_W_Q8_0;
-  HIP_TRY(dbi::launch_oproj(c, kv->stream), "output projection launch");
+                "offload needs dim, ff in [1, 2^20] and n_heads a multiple of n_kv_heads");
+  if (!dbi::attention_supported(kv->geom, static_cast<int>(cfg->n_heads)))
+    return fail(DBI_ERR_UNSUPPORTED, "no attention kernel for this shape");
+  if (!(kv->cfg.rope_theta > 0.0f) && !kv->geom.ring)
+    return fail(DBI_ERR_INVALID, "offload of a dense cache needs rope_theta > 0");
+  const uint32_t qn = cfg->n_heads * hd, kvn = nkv * hd;
+  for (uint32_t l = 0; l < n_layers; ++l) {
+    const dbi_layer_weights& L = layers[l];
+    if (L.attn_norm == nullptr || L.ffn_norm == nullptr)
+      return fail(DBI_ERR_INVALID, "offload block " + std::to_string(l) + ": null norm weight");
+    struct {
+      const dbi_weight& w;
+      uint32_t out, in;
+      const char* name;
+    } ws[] = {{L.wq, qn, cfg->dim, "wq"},      {L.wk, kvn, cfg->dim, "wk"},
+              {L.wv, kvn, cfg->dim, "wv"},      {L.wo, cfg->dim, qn, "wo"},
+              {L.wgate, cfg->ff, cfg->dim, "wgate"}, {L.wup, cfg->ff, cfg->dim, "wup"},
+              {L.wdown, cfg->dim, cfg->ff, "wdown"}};
+    for (const auto& w : ws) {
+      // (the activation rows are the handle's own, 16-byte aligned)
+      const std::string what = "offload block " + std::to_string(l) + " " + w.name;
+      if (dbi_status st = check_matvec(w.w.type, w.w.data, nullptr, w.out, w.in, what.c_str()))
+        return st;
+    }
+  }
+  if (cfg->lm_head.data != nullptr) {
+    if (cfg->output_norm == nullptr || cfg->vocab == 0)
+      return fail(DBI_ERR_INVALID, "offload tail needs output_norm and vocab");
+    if (dbi_status st =
+            check_matvec(cfg->lm_head.type, cfg->lm_head.data, nullptr, cfg->vocab, cfg->dim,
+                         "lm_head"))
+      return st;
+  }
+  if (dbi_status st = refuse_capture(kv, "the offload scratch")) return st;
+  HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+  OffloadState& o = kv->off;
+  if (o.buf) (void)hipFree(o.buf);
+  o.buf = nullptr;
+  // rows rounded up to 64 floats: every row stays 256-byte aligned
+  auto r64 = [](size_t n) { return (n + 63) / 64 * 64; };
+  const size_t total = r64(cfg->dim) + 2 * r64(qn) + 2 * r64(kvn) + 2 * r64(cfg->ff);
+  if (hipMalloc(reinterpret_cast<void**>(&o.buf), total * sizeof(float)) != hipSuccess) {
+    o.layers.clear();
+    return fail(DBI_ERR_NOMEM, "offload scratch allocation failed");
+  }
+  float* p = o.buf;
+  o.normed = p; p += r64(cfg->dim);
+  o.q = p; p += r64(qn);
+  o.attn = p; p += r64(qn);
+  o.k = p; p += r64(kvn);
+  o.v = p; p += r64(kvn);
+  o.gate = p; p += r64(cfg->ff);
+  o.up = p;
+  o.cfg = *cfg;
+  o.layers.assign(layers, layers + n_layers);
+  return DBI_OK;
+}
+
+dbi_status dbi_decode_token_async(dbi_kv* kv, float* x_dev, uint32_t pos) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  return decode_token_impl(kv, x_dev, pos);
+}
+
+dbi_status dbi_decode_token_full_async(dbi_kv* kv, float* x_dev, uint32_t pos,
+                                       float* logits_dev) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  const OffloadState& o = kv->off;
+  if (o.cfg.lm_head.data == nullptr)
+    return fail(DBI_ERR_INVALID, "decode_token_full needs an offload tail (lm_head)");
+  if (logits_dev == nullptr) return fail(DBI_ERR_INVALID, "null logits");
+  if (dbi_status st = decode_token_impl(kv, x_dev, pos)) return st;
+  const int dim = static_cast<int>(o.cfg.dim);
+  HIP_TRY(dbi::launch_rmsnorm(x_dev, o.cfg.output_norm, o.cfg.rms_eps, o.normed, dim, kv->stream),
+          "rmsnorm launch");
+  HIP_TRY(run_matvec(kv, o.cfg.lm_head, o.normed, logits_dev, o.cfg.vocab, o.cfg.dim, false),
+          "lm_head launch");
   return DBI_OK;
 }
 

@@ -265,16 +265,21 @@ struct VerifyCall {
 };
 hipError_t launch_verify(const VerifyCall& c, hipStream_t st);
 
-// Output projection + residual add of decode_layer (oproj.hip):
-// x[o] += sum_i w[o][i] * attn[i], w fp32 or f16 [dim][in] (in % 8 == 0) or
-// Q8_0 blocks [dim][in/32] (in % 32 == 0).
+// The matvecs of decode_layer (oproj.hip): x[o] += sum_i w[o][i] * attn[i]
+// (or x[o] = ... with overwrite), w fp32 or f16 [dim][in] (in % 8 == 0) or
+// Q8_0 / Q4_0 blocks [dim][in/32] (in % 32 == 0).
 struct OprojCall {
   const void* w;
   const float* attn;
   float* x;
   int dim, in;
-  bool f16, q8;
+  bool f16, q8, q4;
+  bool overwrite;
 };
 hipError_t launch_oproj(const OprojCall& c, hipStream_t st);
+// rmsnorm of one row (ops.cpp:7-17) and silu(g) * u in place (model.cpp:781-782)
+hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* out, int dim,
+                          hipStream_t st);
+hipError_t launch_silu_mul(float* g, const float* u, int n, hipStream_t st);
 
 }  // namespace dbi

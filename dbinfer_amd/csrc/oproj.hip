@@ -1,13 +1,16 @@
-// The step after attention in decode_layer (model.cpp:773-774): the output
-// projection of the attention row and the residual add,
-//   proj = W_o · attn   (tensor::matvec_quant, [dim][in] row-major weights)
-//   x[o] += proj[o]
+// The matvecs of decode_layer (model.cpp:738-785) and forward's lm_head
+// (:915): tensor::matvec_quant ([out][in] row-major weights) of one
+// activation row,
+//   y[o] = W[o] · x          (q, k, v, gate, up, lm_head)
+//   y[o] += W[o] · x         (o_proj and down, the residual adds)
 // for fp32 weights (tensor::matvec, matmul.cpp:36-43), f16 weights
 // (tensor::matvec_f16, matmul.cpp:45-54; every f16 weight converts exactly to
-// fp32 and is fused-multiply-added) and Q8_0 blocks (matvec_q8_0_scalar,
-// matmul.cpp:56-75, with the activation row quantized to Q8_0 first,
-// quantize_row_q8_0, dequant.cpp:80-97). The other GGUF block formats are not
-// served.
+// fp32 and is fused-multiply-added), Q8_0 blocks (matvec_q8_0_scalar,
+// matmul.cpp:56-75) and Q4_0 blocks (matvec_q4_0_scalar, :77-99), the
+// quantized types with the activation row quantized to Q8_0 first
+// (quantize_row_q8_0, dequant.cpp:80-97). The other GGUF block formats are
+// not served. The layer's rmsnorm (ops.cpp:7-17) and silu(gate) * up
+// (model.cpp:781-782, ops.cpp:54-56) are here too.
 //
 // One wave per output row: each lane accumulates its share of the row with
 // fused multiply-adds, the wave sums the lanes, and lane 0 adds the result to
@@ -31,9 +34,16 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 struct OprojArgs {
   const void* w;      // [dim][in], fp32 or f16
   const float* attn;  // [in]
-  float* x;           // [dim], residual, updated in place
+  float* x;           // [dim]: x[o] += proj (acc) or x[o] = proj
   int dim, in;
+  int acc;
 };
+
+// the row's result into the output (two roundings with acc, as proj[o] then
+// x[o] + proj[o])
+__device__ inline void put_row(const OprojArgs& a, int row, float proj) {
+  a.x[row] = a.acc ? a.x[row] + proj : proj;
+}
 
 __device__ inline float wave_sum64(float v) {
 #pragma unroll
@@ -96,7 +106,7 @@ __global__ __launch_bounds__(kThreads) void oproj_kernel(OprojArgs a) {
     }
   }
   const float proj = wave_sum64(acc);
-  if (lane == 0) a.x[row] = a.x[row] + proj;
+  if (lane == 0) put_row(a, row, proj);
 }
 
 // Q8_0: a block is an f16 scale then 32 int8 codes (34 bytes). Each
@@ -121,31 +131,44 @@ __device__ inline uint32_t pack4(int8_t a, int8_t b, int8_t c, int8_t d) {
          (static_cast<uint32_t>(static_cast<uint8_t>(d)) << 24);
 }
 
-__global__ __launch_bounds__(kThreads) void oproj_q8_kernel(OprojArgs a) {
-  extern __shared__ uint32_t s_xq[];  // [nbk][kQStride]
-  const int nbk = a.in / 32;
+// The activation row to Q8_0 blocks in LDS (quantize_row_q8_0's arithmetic,
+// one thread per block): 8 code dwords, the f16 scale as a float, and (for
+// Q4_0) the block's code sum, kQStride4 dwords per block.
+constexpr int kQStride4 = 10;
+__device__ inline void quantize_act(const float* x, int nbk, uint32_t* s_xq, int stride) {
   for (int b = threadIdx.x; b < nbk; b += kThreads) {
-    const float4* xb = reinterpret_cast<const float4*>(a.attn + static_cast<size_t>(b) * 32);
-    float x[32];
+    const float4* xb = reinterpret_cast<const float4*>(x + static_cast<size_t>(b) * 32);
+    float v[32];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float4 t = xb[i];
-      x[4 * i] = t.x;
-      x[4 * i + 1] = t.y;
-      x[4 * i + 2] = t.z;
-      x[4 * i + 3] = t.w;
+      v[4 * i] = t.x;
+      v[4 * i + 1] = t.y;
+      v[4 * i + 2] = t.z;
+      v[4 * i + 3] = t.w;
     }
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) amax = max_f(amax, fabsf(x[i]));
+    for (int i = 0; i < 32; ++i) amax = max_f(amax, fabsf(v[i]));
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    int sum = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      s_xq[b * kQStride + i] = pack4(quant_code(x[4 * i], id), quant_code(x[4 * i + 1], id),
-                                     quant_code(x[4 * i + 2], id), quant_code(x[4 * i + 3], id));
-    s_xq[b * kQStride + 8] = __float_as_uint(static_cast<float>(static_cast<_Float16>(d)));
+    for (int i = 0; i < 8; ++i) {
+      const int8_t c0 = quant_code(v[4 * i], id), c1 = quant_code(v[4 * i + 1], id);
+      const int8_t c2 = quant_code(v[4 * i + 2], id), c3 = quant_code(v[4 * i + 3], id);
+      s_xq[b * stride + i] = pack4(c0, c1, c2, c3);
+      sum += c0 + c1 + c2 + c3;
+    }
+    s_xq[b * stride + 8] = __float_as_uint(static_cast<float>(static_cast<_Float16>(d)));
+    if (stride > 9) s_xq[b * stride + 9] = static_cast<uint32_t>(sum);
   }
+}
+
+__global__ __launch_bounds__(kThreads) void oproj_q8_kernel(OprojArgs a) {
+  extern __shared__ uint32_t s_xq[];  // [nbk][kQStride]
+  const int nbk = a.in / 32;
+  quantize_act(a.attn, nbk, s_xq, kQStride);
   __syncthreads();
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) * kQRows;
@@ -186,7 +209,95 @@ __global__ __launch_bounds__(kThreads) void oproj_q8_kernel(OprojArgs a) {
       }
     }
     const float proj = wave_sum64(acc);
-    if (lane == 0) a.x[row] = a.x[row] + proj;
+    if (lane == 0) put_row(a, row, proj);
+  }
+}
+
+// Q4_0: a block is an f16 scale then 16 bytes of nibbles (18 bytes); element
+// j of the block is the low nibble of byte j, element j + 16 its high
+// nibble, each minus 8. Per block the integer sum is exact: the nibbles
+// (0..15, positive as signed bytes) dot the activation codes with
+// v_dot4_i32_i8, minus 8 times the block's code sum; the term is
+// (f16(dw) * f16(dx)) * sumi as matvec_q4_0_scalar writes it. A block's 18
+// bytes are read as the 5 aligned dwords around them (blocks start 2-byte
+// aligned; the last dword can reach 2 bytes past the matrix, inside the
+// same aligned dword).
+__global__ __launch_bounds__(kThreads) void oproj_q4_kernel(OprojArgs a) {
+  extern __shared__ uint32_t s_xq4[];  // [nbk][kQStride4]
+  const int nbk = a.in / 32;
+  quantize_act(a.attn, nbk, s_xq4, kQStride4);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6)) * kQRows;
+  for (int rr = 0; rr < kQRows; ++rr) {
+    const int row = row0 + rr;
+    if (row >= a.dim) break;  // wave-uniform
+    const uintptr_t wrow =
+        reinterpret_cast<uintptr_t>(a.w) + static_cast<size_t>(row) * nbk * 18;
+    float acc = 0.0f;
+    for (int b0 = lane; b0 < nbk; b0 += 64 * kQBlocks) {
+      uint32_t wd[kQBlocks][5];
+      uint32_t off[kQBlocks];
+#pragma unroll
+      for (int q = 0; q < kQBlocks; ++q) {
+        const int b = min(b0 + 64 * q, nbk - 1);
+        const uintptr_t p = wrow + static_cast<size_t>(b) * 18;
+        off[q] = static_cast<uint32_t>(p & 2);
+        const uint32_t* base = reinterpret_cast<const uint32_t*>(p & ~static_cast<uintptr_t>(3));
+#pragma unroll
+        for (int i = 0; i < 5; ++i) wd[q][i] = base[i];
+      }
+#pragma unroll
+      for (int q = 0; q < kQBlocks; ++q) {
+        const int b = min(b0 + 64 * q, nbk - 1);
+        const uint32_t* xq = s_xq4 + b * kQStride4;
+        const bool hi = off[q] != 0;  // block starts 2 bytes into its first dword
+        const uint16_t dbits = static_cast<uint16_t>(hi ? wd[q][0] >> 16 : wd[q][0] & 0xffffu);
+        const float dw = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
+        int sumi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t c = hi ? wd[q][i + 1] : ((wd[q][i] >> 16) | (wd[q][i + 1] << 16));
+          const uint32_t lo = c & 0x0F0F0F0Fu, hn = (c >> 4) & 0x0F0F0F0Fu;
+          sumi = __builtin_amdgcn_sdot4(static_cast<int>(lo), static_cast<int>(xq[i]), sumi, false);
+          sumi = __builtin_amdgcn_sdot4(static_cast<int>(hn), static_cast<int>(xq[4 + i]), sumi,
+                                        false);
+        }
+        sumi -= 8 * static_cast<int>(xq[9]);
+        const float term = (dw * __uint_as_float(xq[8])) * static_cast<float>(sumi);
+        acc = b0 + 64 * q < nbk ? acc + term : acc;
+      }
+    }
+    const float proj = wave_sum64(acc);
+    if (lane == 0) put_row(a, row, proj);
+  }
+}
+
+// rmsnorm of one row (ops.cpp:7-17): the sum of squares over the workgroup
+// (a tree, so it agrees with the reference's sequential sum to a rounding),
+// scale = 1 / sqrt(sumsq / dim + eps), out[i] = x[i] * scale * w[i].
+constexpr int kNormThreads = 1024;
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, const float* w,
+                                                               float eps, float* out, int dim) {
+  __shared__ float s_part[kNormThreads / 64];
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < dim; i += kNormThreads) ss += x[i] * x[i];
+  ss = wave_sum64(ss);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) tot += s_part[i];
+  const float scale = 1.0f / sqrtf(tot / static_cast<float>(dim) + eps);
+  for (int i = threadIdx.x; i < dim; i += kNormThreads) out[i] = x[i] * scale * w[i];
+}
+
+// silu(gate) then gate *= up (model.cpp:781-782, ops.cpp:54-56)
+__global__ __launch_bounds__(256) void silu_mul_kernel(float* g, const float* u, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) {
+    const float x = g[i];
+    g[i] = (x / (1.0f + expf(-x))) * u[i];
   }
 }
 
@@ -199,8 +310,14 @@ hipError_t launch_oproj(const OprojCall& c, hipStream_t st) {
   a.x = c.x;
   a.dim = c.dim;
   a.in = c.in;
+  a.acc = c.overwrite ? 0 : 1;
   const dim3 grid((c.dim + kRowsPerBlock - 1) / kRowsPerBlock);
-  if (c.q8) {
+  if (c.q4) {
+    const int rows_per_block = kRowsPerBlock * kQRows;
+    const size_t lds = static_cast<size_t>(c.in / 32) * kQStride4 * sizeof(uint32_t);
+    hipLaunchKernelGGL(oproj_q4_kernel, dim3((c.dim + rows_per_block - 1) / rows_per_block),
+                       dim3(kThreads), lds, st, a);
+  } else if (c.q8) {
     const int rows_per_block = kRowsPerBlock * kQRows;
     const size_t lds = static_cast<size_t>(c.in / 32) * kQStride * sizeof(uint32_t);
     hipLaunchKernelGGL(oproj_q8_kernel, dim3((c.dim + rows_per_block - 1) / rows_per_block),
@@ -209,6 +326,17 @@ hipError_t launch_oproj(const OprojCall& c, hipStream_t st) {
     hipLaunchKernelGGL(oproj_kernel<true>, grid, dim3(kThreads), 0, st, a);
   else
     hipLaunchKernelGGL(oproj_kernel<false>, grid, dim3(kThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* out, int dim,
+                          hipStream_t st) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, st, x, w, eps, out, dim);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(float* g, const float* u, int n, hipStream_t st) {
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, st, g, u, n);
   return hipGetLastError();
 }
 

@@ -22,6 +22,7 @@ INT8 = _lib.DBI_KV_INT8
 W_F32 = _lib.DBI_W_F32
 W_F16 = _lib.DBI_W_F16
 W_Q8_0 = _lib.DBI_W_Q8_0
+W_Q4_0 = _lib.DBI_W_Q4_0
 
 
 class DbiError(RuntimeError):
@@ -273,6 +274,31 @@ class HipKV:
                              n_in: int) -> None:
         _check(self._lib, self._lib.dbi_oproj_residual_async(self._h, wtype, w_dev, attn_dev,
                                                              x_dev, dim, n_in))
+
+    # ---- full-layer offload (backend.hpp:133-157)
+    def offload_setup(self, dim: int, ff: int, n_heads: int, rms_eps: float, layers: list,
+                      output_norm: int | None = None, lm_head: tuple | None = None,
+                      vocab: int = 0) -> None:
+        """layers: per block a dict of device pointers attn_norm, ffn_norm,
+        bq/bk/bv (or None) and (data_ptr, wtype) tuples wq wk wv wo wgate wup
+        wdown; lm_head: (data_ptr, wtype) or None."""
+        arr = (_lib.LayerWeights * len(layers))()
+        for i, L in enumerate(layers):
+            a = arr[i]
+            a.attn_norm, a.ffn_norm = L["attn_norm"], L["ffn_norm"]
+            for name in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown"):
+                ptr, wt = L[name]
+                setattr(a, name, _lib.Weight(ptr, wt))
+            a.bq, a.bk, a.bv = L.get("bq"), L.get("bk"), L.get("bv")
+        cfg = _lib.OffloadConfig(dim, ff, n_heads, rms_eps, output_norm,
+                                 _lib.Weight(*(lm_head if lm_head else (None, 0))), vocab)
+        _check(self._lib, self._lib.dbi_offload_setup(self._h, ctypes.byref(cfg), arr, len(layers)))
+
+    def decode_token_async(self, x_dev: int, pos: int) -> None:
+        _check(self._lib, self._lib.dbi_decode_token_async(self._h, x_dev, pos))
+
+    def decode_token_full_async(self, x_dev: int, pos: int, logits_dev: int) -> None:
+        _check(self._lib, self._lib.dbi_decode_token_full_async(self._h, x_dev, pos, logits_dev))
 
     # ---- prefix cache
     def save_prefix(self, path: str, tokens) -> None:

@@ -242,20 +242,23 @@ dbi_status dbi_kv_verify_commit(dbi_kv* kv, uint32_t pos, uint32_t k, uint32_t v
                                 const float* logits_dev, const int32_t* draft, int32_t* merged,
                                 uint32_t* accepted);
 
-/* Weight types of dbi_oproj_residual_async, numbered as GgmlType. */
-enum { DBI_W_F32 = 0, DBI_W_F16 = 1, DBI_W_Q8_0 = 8 };
+/* Weight types of the matvecs (dbi_oproj_residual_async, the layer offload),
+ * numbered as GgmlType. */
+enum { DBI_W_F32 = 0, DBI_W_F16 = 1, DBI_W_Q4_0 = 2, DBI_W_Q8_0 = 8 };
 
 /* The step after attention in Model::decode_layer (model.cpp:773-774):
  * matvec_quant(attn_output, attn, proj, dim, nh*hd) then x[i] += proj[i],
  * for fp32 weights (tensor::matvec, matmul.cpp:36-43), f16 weights
- * (tensor::matvec_f16, matmul.cpp:45-54) and Q8_0 blocks
- * (matvec_q8_0_scalar, matmul.cpp:56-75, after quantize_row_q8_0 of attn,
- * dequant.cpp:80-97). w_dev: device [dim][in] row-major (Q8_0: [dim][in/32]
- * blocks of an f16 scale and 32 int8 codes, 34 bytes); attn_dev: device [in]
- * (the attention row, in = n_heads*head_dim); x_dev: device [dim], the
- * residual stream, updated in place. in must be a multiple of 8, at most
- * 2^24 (Q8_0: a multiple of 32, at most 32768);
- * w_dev 16-byte aligned (Q8_0: 4), attn_dev 16-byte aligned. Each row's terms
+ * (tensor::matvec_f16, matmul.cpp:45-54), Q8_0 blocks (matvec_q8_0_scalar,
+ * matmul.cpp:56-75) and Q4_0 blocks (matvec_q4_0_scalar, :77-99), the
+ * quantized types after quantize_row_q8_0 of attn (dequant.cpp:80-97).
+ * w_dev: device [dim][in] row-major (Q8_0: [dim][in/32] blocks of an f16
+ * scale and 32 int8 codes, 34 bytes; Q4_0: of an f16 scale and 16 bytes of
+ * nibbles, 18 bytes); attn_dev: device [in] (the attention row, in =
+ * n_heads*head_dim); x_dev: device [dim], the residual stream, updated in
+ * place. in must be a multiple of 8, at most 2^24 (Q8_0, Q4_0: a multiple of
+ * 32, at most 32768); w_dev 16-byte aligned (Q8_0, Q4_0: 4), attn_dev
+ * 16-byte aligned. Each row's terms
  * are summed in a tree, so proj agrees with the reference's sequential sum
  * to the rounding of a dot product, not bit for bit (the Q8_0 codes and
  * per-block integer sums are exact). Other GGUF block types return
@@ -263,6 +266,74 @@ enum { DBI_W_F32 = 0, DBI_W_F16 = 1, DBI_W_Q8_0 = 8 };
 dbi_status dbi_oproj_residual_async(dbi_kv* kv, uint32_t wtype, const void* w_dev,
                                     const float* attn_dev, float* x_dev, uint32_t dim,
                                     uint32_t in);
+
+/* ---- Full-layer offload: the whole of Model::decode_layer on the device
+ * (replaces backend::Backend::setup_offload / decode_token /
+ * decode_token_full, backend.hpp:133-157, and the offload branch of
+ * Model::forward, model.cpp:896-917). */
+
+/* one matmul weight: device data and its type (DBI_W_*) */
+typedef struct dbi_weight {
+  const void* data;
+  uint32_t type;
+} dbi_weight;
+
+/* one transformer block (backend::LayerQ, backend.hpp:29-48): device
+ * pointers; attn_norm, ffn_norm [dim]; wq [n_heads*hd][dim], wk and wv
+ * [n_kv*hd][dim], wo [dim][n_heads*hd], wgate and wup [ff][dim], wdown
+ * [dim][ff]; biases [n_heads*hd] / [n_kv*hd] or NULL. Alignment as
+ * dbi_oproj_residual_async's w_dev. */
+typedef struct dbi_layer_weights {
+  const float* attn_norm;
+  const float* ffn_norm;
+  dbi_weight wq, wk, wv, wo, wgate, wup, wdown;
+  const float* bq;
+  const float* bk;
+  const float* bv;
+} dbi_layer_weights;
+
+/* the shape shared by every block (LayerQ's dim, ff, n_heads, rms_eps; the
+ * kv heads, head_dim and rope_theta are the cache's), and the tail of
+ * decode_token_full: output_norm [dim] and lm_head [vocab][dim] (device), or
+ * lm_head.data == NULL for no tail. */
+typedef struct dbi_offload_config {
+  uint32_t dim, ff, n_heads;
+  float rms_eps;
+  const float* output_norm;
+  dbi_weight lm_head;
+  uint32_t vocab;
+} dbi_offload_config;
+
+/* Backend::setup_offload (backend.hpp:133-143): binds n_layers blocks (the
+ * first n_layers of the cache's layers) and the tail; the weights are the
+ * caller's device memory, used in place until the next setup or destroy.
+ * Allocates the layer's scratch rows; not under graph capture. The cache may
+ * be any layout (the reference offloads dense fp32 only, main.cpp:241-244):
+ * dense fp32 and int8 attend after rope + append at pos, a ring through its
+ * own attention (model.cpp:757-771). dim, ff and n_heads*head_dim must be
+ * multiples of 32 for Q8_0 / Q4_0 weights (of 8 otherwise). */
+dbi_status dbi_offload_setup(dbi_kv* kv, const dbi_offload_config* cfg,
+                             const dbi_layer_weights* layers, uint32_t n_layers);
+
+/* Backend::decode_token (backend.hpp:145-149): every bound block of one
+ * token at position pos, on the handle's stream, per block exactly
+ * decode_layer's sequence: rmsnorm, q/k/v matvecs, biases, rope, append,
+ * attention (the fused decode step), o_proj + residual, rmsnorm, gate/up,
+ * silu(gate) * up, down + residual. x_dev: device [dim] (16-byte aligned),
+ * the residual stream, updated in place. Allocates nothing; capturable
+ * after the handle's first producer call (which builds its rope table).
+ * Each matvec sums in a tree and rmsnorm's sum of squares too, so results
+ * agree with the reference to the rounding of those sums; with Q8_0 / Q4_0
+ * weights a rounding difference can move an activation code across a
+ * quantization boundary (the reference's own result depends on its
+ * compiler's contraction of rmsnorm's sum in the same way). */
+dbi_status dbi_decode_token_async(dbi_kv* kv, float* x_dev, uint32_t pos);
+
+/* Backend::decode_token_full (backend.hpp:151-157): dbi_decode_token_async,
+ * then the final rmsnorm with output_norm and the lm_head matvec into
+ * logits_dev [vocab] (Model::forward, model.cpp:914-915). Needs a tail. */
+dbi_status dbi_decode_token_full_async(dbi_kv* kv, float* x_dev, uint32_t pos,
+                                       float* logits_dev);
 
 /* Model::save_kv_prefix (model.hpp:292-293, model.cpp:1072-1107): writes the
  * DBKVCACH v1 file of positions [0, len) with the token ids from a dense

@@ -842,19 +842,21 @@ void ok_quantize_row_q8_0(const float* x, size_t n, uint8_t* out) {
   }
 }
 
-void ok_oproj_residual(const void* w, int wtype, const float* attn, float* x, size_t dim,
-                       size_t in) {
+/* tensor::matvec_quant (matmul.cpp:275-281, matvec_rows :225-272): Q8_0
+ * and Q4_0 weights quantize the activation once (quantize_activation,
+ * :27-32) and take the scalar kernels; every row is a sequential fp32 sum. */
+void ok_matvec(const void* w, int wtype, const float* x, float* y, size_t out, size_t in) {
   uint8_t* xq = NULL;
-  if (wtype == 8) {
+  if (wtype == 8 || wtype == 2) {
     xq = (uint8_t*)malloc(in / 32 * 34);
-    ok_quantize_row_q8_0(attn, in, xq);
+    ok_quantize_row_q8_0(x, in, xq);
   }
-  for (size_t o = 0; o < dim; ++o) {
+  for (size_t o = 0; o < out; ++o) {
     float acc = 0.0f;
-    if (wtype == 1) {
+    if (wtype == 1) { /* matvec_f16, matmul.cpp:45-54: explicit fma */
       const uint16_t* row = (const uint16_t*)w + o * in;
-      for (size_t i = 0; i < in; ++i) acc = fmaf(ok_f16_to_f32(row[i]), attn[i], acc);
-    } else if (wtype == 8) {
+      for (size_t i = 0; i < in; ++i) acc = fmaf(ok_f16_to_f32(row[i]), x[i], acc);
+    } else if (wtype == 8) { /* matvec_q8_0_scalar, matmul.cpp:56-75 */
       const uint8_t* row = (const uint8_t*)w + o * (in / 32) * 34;
       for (size_t b = 0; b < in / 32; ++b) {
         const uint8_t* wb = row + b * 34;
@@ -866,11 +868,110 @@ void ok_oproj_residual(const void* w, int wtype, const float* attn, float* x, si
         for (int i = 0; i < 32; ++i) sumi += (int32_t)(int8_t)wb[2 + i] * (int32_t)(int8_t)ab[2 + i];
         acc += ok_f16_to_f32(dw) * ok_f16_to_f32(dx) * (float)sumi;
       }
-    } else {
+    } else if (wtype == 2) { /* matvec_q4_0_scalar, matmul.cpp:77-99: 18-byte blocks */
+      const uint8_t* row = (const uint8_t*)w + o * (in / 32) * 18;
+      for (size_t b = 0; b < in / 32; ++b) {
+        const uint8_t* wb = row + b * 18;
+        const uint8_t* ab = xq + b * 34;
+        uint16_t dw, dx;
+        memcpy(&dw, wb, 2);
+        memcpy(&dx, ab, 2);
+        int32_t sumi = 0;
+        for (int j = 0; j < 16; ++j) {
+          const uint8_t q = wb[2 + j];
+          sumi += ((int32_t)(q & 0x0Fu) - 8) * (int32_t)(int8_t)ab[2 + j];
+          sumi += ((int32_t)(q >> 4) - 8) * (int32_t)(int8_t)ab[2 + j + 16];
+        }
+        acc += ok_f16_to_f32(dw) * ok_f16_to_f32(dx) * (float)sumi;
+      }
+    } else { /* tensor::matvec, matmul.cpp:36-43 */
       const float* row = (const float*)w + o * in;
-      for (size_t i = 0; i < in; ++i) acc += row[i] * attn[i];
+      for (size_t i = 0; i < in; ++i) acc += row[i] * x[i];
     }
-    x[o] += acc;
+    y[o] = acc;
   }
   free(xq);
+}
+
+void ok_oproj_residual(const void* w, int wtype, const float* attn, float* x, size_t dim,
+                       size_t in) {
+  float* proj = (float*)malloc(dim * sizeof(float));
+  ok_matvec(w, wtype, attn, proj, dim, in);
+  for (size_t o = 0; o < dim; ++o) x[o] += proj[o];
+  free(proj);
+}
+
+/* ------------------------------------------------------------------ */
+/* the whole decode layer (model.cpp:730-787)                          */
+/* ------------------------------------------------------------------ */
+
+/* ops.cpp:7-17, one row */
+void ok_rmsnorm(const float* x, const float* weight, float eps, float* out, size_t dim) {
+  float sumsq = 0.0f;
+  for (size_t i = 0; i < dim; ++i) sumsq += x[i] * x[i];
+  const float scale = 1.0f / sqrtf(sumsq / (float)dim + eps);
+  for (size_t i = 0; i < dim; ++i) out[i] = x[i] * scale * weight[i];
+}
+
+/* ops.cpp:54-56 */
+void ok_silu(const float* in, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = in[i] / (1.0f + expf(-in[i]));
+}
+
+void okv_decode_layer(okv* kv, size_t layer, float* x, int32_t pos, const ok_layer* L,
+                      size_t dim, size_t ff, size_t n_heads, float eps, float theta,
+                      int n_threads) {
+  const size_t hd = kv->head_dim, nkv = kv->n_kv_heads;
+  float* normed = (float*)malloc(dim * sizeof(float));
+  float* q = (float*)malloc(n_heads * hd * sizeof(float));
+  float* k = (float*)malloc(nkv * hd * sizeof(float));
+  float* v = (float*)malloc(nkv * hd * sizeof(float));
+  float* attn = (float*)malloc(n_heads * hd * sizeof(float));
+  float* proj = (float*)malloc(dim * sizeof(float));
+  float* gate = (float*)malloc(ff * sizeof(float));
+  float* up = (float*)malloc(ff * sizeof(float));
+
+  ok_rmsnorm(x, L->attn_norm, eps, normed, dim);
+  ok_matvec(L->w[0], L->wtype[0], normed, q, n_heads * hd, dim);
+  ok_matvec(L->w[1], L->wtype[1], normed, k, nkv * hd, dim);
+  ok_matvec(L->w[2], L->wtype[2], normed, v, nkv * hd, dim);
+  if (L->bq)
+    for (size_t i = 0; i < n_heads * hd; ++i) q[i] += L->bq[i];
+  if (L->bk)
+    for (size_t i = 0; i < nkv * hd; ++i) k[i] += L->bk[i];
+  if (L->bv)
+    for (size_t i = 0; i < nkv * hd; ++i) v[i] += L->bv[i];
+  const float scale = 1.0f / sqrtf((float)hd);
+  if (!okv_is_ring(kv)) {
+    const int32_t p = pos;
+    ok_rope(q, &p, theta, n_heads, 1, hd);
+    ok_rope(k, &p, theta, nkv, 1, hd);
+    okv_append(kv, layer, (size_t)pos, k, v);
+    if (okv_is_int8(kv))
+      okv_attend_dense_int8(kv, layer, (size_t)pos, n_heads, scale, q, attn, n_threads);
+    else
+      okv_attend_dense_f32(kv, layer, (size_t)pos, n_heads, scale, q, attn, n_threads);
+  } else {
+    okv_attend_ring(kv, layer, (size_t)pos, n_heads, scale, theta, q, k, v, attn, n_threads);
+  }
+  ok_matvec(L->w[3], L->wtype[3], attn, proj, dim, n_heads * hd);
+  for (size_t i = 0; i < dim; ++i) x[i] += proj[i];
+
+  ok_rmsnorm(x, L->ffn_norm, eps, normed, dim);
+  ok_matvec(L->w[4], L->wtype[4], normed, gate, ff, dim);
+  ok_matvec(L->w[5], L->wtype[5], normed, up, ff, dim);
+  ok_silu(gate, gate, ff);
+  for (size_t i = 0; i < ff; ++i) gate[i] *= up[i];
+  ok_matvec(L->w[6], L->wtype[6], gate, proj, dim, ff);
+  for (size_t i = 0; i < dim; ++i) x[i] += proj[i];
+
+  free(normed); free(q); free(k); free(v); free(attn); free(proj); free(gate); free(up);
+}
+
+void ok_logits(const float* x, const float* output_norm, const void* lm_head, int wtype,
+               float eps, float* logits, size_t dim, size_t vocab) {
+  float* normed = (float*)malloc(dim * sizeof(float));
+  ok_rmsnorm(x, output_norm, eps, normed, dim);
+  ok_matvec(lm_head, wtype, normed, logits, vocab, dim);
+  free(normed);
 }

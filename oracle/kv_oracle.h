@@ -41,6 +41,13 @@
  *   ok_oproj_residual  exact on small-integer data (every partial sum is an
  *                      integer below 2^24, so any order is exact); fp64 dot
  *                      product within the sequential-sum rounding bound
+ *   ok_matvec          the same checks per type; Q4_0 and Q8_0 against an
+ *                      integer (numpy int64) restatement of each block's sum
+ *                      and the reference's term expression
+ *   ok_rmsnorm, ok_silu  bit for bit against the reference's ops.cpp (oracle/_ref)
+ *   okv_decode_layer   composed of the pinned functions above; checked
+ *                      against a numpy restatement of model.cpp:730-787 built
+ *                      from them, and with identity weights against its parts
  */
 #ifndef DBI_KV_ORACLE_H
 #define DBI_KV_ORACLE_H
@@ -168,6 +175,38 @@ void ok_quantize_row_q8_0(const float* x, size_t n, uint8_t* out);
  * sequential sum over the row, then x[o] += proj[o]. */
 void ok_oproj_residual(const void* w, int wtype, const float* attn, float* x, size_t dim,
                        size_t in);
+/* tensor::matvec_quant (matmul.cpp:225-281): y[o] = row o . x, a sequential
+ * fp32 sum; wtype 0 fp32, 1 f16, 2 Q4_0 (matvec_q4_0_scalar, :77-99: 18-byte
+ * blocks of an f16 scale and 16 bytes of nibbles, element j the low nibble
+ * of byte j, element j + 16 its high nibble, value nibble - 8), 8 Q8_0; the
+ * quantized types quantize x with ok_quantize_row_q8_0 first. */
+void ok_matvec(const void* w, int wtype, const float* x, float* y, size_t out, size_t in);
+/* ops.cpp:7-17 (one row) and :54-56 */
+void ok_rmsnorm(const float* x, const float* weight, float eps, float* out, size_t dim);
+void ok_silu(const float* in, float* out, size_t n);
+
+/* one transformer block's weights for okv_decode_layer: w / wtype in the
+ * order q, k, v, o, gate, up, down; biases may be NULL */
+typedef struct {
+  const float* attn_norm;
+  const float* ffn_norm;
+  const void* w[7];
+  int wtype[7];
+  const float* bq;
+  const float* bk;
+  const float* bv;
+} ok_layer;
+/* Model::decode_layer (model.cpp:730-787): rmsnorm, q/k/v matvecs, biases,
+ * rope + append + attention of the cache's layout (dense: rope at pos then
+ * append, attend_dense_f32/int8; ring: attend_ring), o_proj + residual,
+ * rmsnorm, gate/up, silu(gate) * up, down + residual. x [dim] in place. */
+void okv_decode_layer(okv* kv, size_t layer, float* x, int32_t pos, const ok_layer* L,
+                      size_t dim, size_t ff, size_t n_heads, float eps, float theta,
+                      int n_threads);
+/* Model::forward's tail (model.cpp:914-915): rmsnorm with output_norm, then
+ * the lm_head matvec into logits [vocab] */
+void ok_logits(const float* x, const float* output_norm, const void* lm_head, int wtype,
+               float eps, float* logits, size_t dim, size_t vocab);
 
 #ifdef __cplusplus
 }

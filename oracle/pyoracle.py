@@ -69,6 +69,12 @@ _SIGS = {
     "ok_oproj_residual": (None, [_vp, ctypes.c_int, _vp, _vp, _sz, _sz]),
     "ok_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
     "ok_quantize_row_q8_0": (None, [_vp, _sz, _vp]),
+    "ok_matvec": (None, [_vp, ctypes.c_int, _vp, _vp, _sz, _sz]),
+    "ok_rmsnorm": (None, [_vp, _vp, ctypes.c_float, _vp, _sz]),
+    "ok_silu": (None, [_vp, _vp, _sz]),
+    "okv_decode_layer": (None, [_P, _sz, _vp, ctypes.c_int32, _vp, _sz, _sz, _sz, ctypes.c_float,
+                                ctypes.c_float, ctypes.c_int]),
+    "ok_logits": (None, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_float, _vp, _sz, _sz]),
 }
 
 _LIB = None
@@ -98,6 +104,11 @@ def load_ref():
         lib.ref_rope.argtypes = [_vp, _vp, ctypes.c_float, _sz, _sz, _sz]
         lib.ref_softmax.restype = None
         lib.ref_softmax.argtypes = [_vp, _vp, _sz]
+        if hasattr(lib, "ref_rmsnorm"):
+            lib.ref_rmsnorm.restype = None
+            lib.ref_rmsnorm.argtypes = [_vp, _vp, ctypes.c_float, _vp, _sz, _sz]
+            lib.ref_silu.restype = None
+            lib.ref_silu.argtypes = [_vp, _vp, _sz]
         _REF = lib
     return _REF
 
@@ -168,6 +179,49 @@ def oproj_residual(w, attn, x, q8_0: bool = False):
     wtype = 8 if q8_0 else (1 if wc.dtype == np.float16 else 0)
     load().ok_oproj_residual(wc.ctypes.data, wtype, a.ctypes.data, out.ctypes.data, out.size,
                              a.size)
+    return out
+
+
+# weight types, numbered as GgmlType (gguf.hpp)
+W_F32, W_F16, W_Q4_0, W_Q8_0 = 0, 1, 2, 8
+
+
+def matvec(w, wtype: int, x, out: int) -> np.ndarray:
+    """tensor::matvec_quant of w (fp32 / f16 [out][in], or uint8 Q4_0 / Q8_0
+    blocks [out][in/32*18|34]) against x [in]."""
+    wc = np.ascontiguousarray(w)
+    xa = _f32(x)
+    y = np.zeros(out, np.float32)
+    load().ok_matvec(wc.ctypes.data, wtype, xa.ctypes.data, y.ctypes.data, out, xa.size)
+    return y
+
+
+def rmsnorm(x, weight, eps: float) -> np.ndarray:
+    xa, wa = _f32(x), _f32(weight)
+    out = np.zeros_like(xa)
+    load().ok_rmsnorm(xa.ctypes.data, wa.ctypes.data, eps, out.ctypes.data, xa.size)
+    return out
+
+
+def silu(x) -> np.ndarray:
+    xa = _f32(x)
+    out = np.zeros_like(xa)
+    load().ok_silu(xa.ctypes.data, out.ctypes.data, xa.size)
+    return out
+
+
+class _OkLayer(ctypes.Structure):
+    _fields_ = [("attn_norm", _vp), ("ffn_norm", _vp), ("w", _vp * 7), ("wtype", ctypes.c_int * 7),
+                ("bq", _vp), ("bk", _vp), ("bv", _vp)]
+
+
+def logits(x, output_norm, lm_head, wtype: int, eps: float, vocab: int) -> np.ndarray:
+    """Model::forward's tail (model.cpp:914-915)."""
+    xa, na = _f32(x), _f32(output_norm)
+    lm = np.ascontiguousarray(lm_head)
+    out = np.zeros(vocab, np.float32)
+    load().ok_logits(xa.ctypes.data, na.ctypes.data, lm.ctypes.data, wtype, eps, out.ctypes.data,
+                     xa.size, vocab)
     return out
 
 
@@ -273,6 +327,33 @@ class OracleKV:
         self._lib.okv_attend_chunk(self._p, layer, pos0, n, n_heads, scale, q.ctypes.data,
                                    out.ctypes.data, n_threads)
         return out
+
+    def decode_layer(self, layer: int, x, pos: int, lw: dict, dim: int, ff: int, n_heads: int,
+                     eps: float, n_threads: int = 1) -> np.ndarray:
+        """Model::decode_layer (model.cpp:730-787) on a copy of x. lw holds
+        attn_norm, ffn_norm, w (7 arrays: q k v o gate up down), wtype (7 ints)
+        and optional bq, bk, bv."""
+        keep = []
+
+        def ptr(a, dt=None):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a, dtype=dt) if dt else np.ascontiguousarray(a)
+            keep.append(a)
+            return a.ctypes.data
+        L = _OkLayer()
+        L.attn_norm = ptr(lw["attn_norm"], np.float32)
+        L.ffn_norm = ptr(lw["ffn_norm"], np.float32)
+        for i in range(7):
+            L.w[i] = ptr(lw["w"][i])
+            L.wtype[i] = int(lw["wtype"][i])
+        L.bq = ptr(lw.get("bq"), np.float32)
+        L.bk = ptr(lw.get("bk"), np.float32)
+        L.bv = ptr(lw.get("bv"), np.float32)
+        xa = _f32(x).copy()
+        self._lib.okv_decode_layer(self._p, layer, xa.ctypes.data, pos, ctypes.byref(L), dim, ff,
+                                   n_heads, eps, self.rope_theta, n_threads)
+        return xa
 
     def save_prefix(self, path: str, tokens) -> None:
         t = np.ascontiguousarray(tokens, dtype=np.int32)

@@ -1,0 +1,169 @@
+"""The full-layer offload (backend.hpp:133-157): every
+bound block of a token on the device through `dbi_decode_token_async` /
+`dbi_decode_token_full_async`, against the oracle's Model::decode_layer
+(`okv_decode_layer`, model.cpp:730-787) and forward's tail (`ok_logits`,
+model.cpp:914-915), token after token, for dense fp32 (the reference's only
+offload layout), dense int8 and ring caches and the four weight types.
+
+Tolerance. fp32 / f16 weights: the device sums matvec rows, rmsnorm's squares
+and attention in trees, the reference in sequence, so every value agrees to
+the rounding of its sums: |a - b| <= 1e-5 + 1e-4 |b| on the residual stream
+and the logits. Q8_0 / Q4_0 weights quantize each activation row to Q8_0
+first (quantize_row_q8_0); an activation a rounding away from a code
+boundary can land on the other code (the reference's own result moves the
+same way with its compiler's contraction of rmsnorm's sum), which moves a
+matvec output by up to d_w * 127 * d_x, here ~2e-3; those layers are checked
+to 3e-3 (absolute and relative). The synthetic weights have the float ones'
+spread (std ~0.05: every matvec's gain is below 1), so a flip in one layer
+is not amplified by the next; with hotter random weights (gain ~1.5 per
+matvec, a residual stream of |x| ~ 20) one layer-0 flip of 0.0017 grew to
+0.13 after two layers, in the oracle's own sensitivity, not a device error. The matvec kernels themselves are checked
+on identical activations in test_gpu_oproj.py (Q8_0, Q4_0: the integer block
+sums are exact).
+"""
+import numpy as np
+import pytest
+
+import pyoracle
+from dbinfer_amd.kv import F32, INT8, DbiError, HipKV
+from helpers import normal
+from pyoracle import W_F16, W_F32, W_Q4_0, W_Q8_0
+from test_oracle_layer import layer_weights
+
+pytestmark = pytest.mark.gpu
+
+DIM, FF, NH, NKV, HD, EPS, L, VOCAB = 256, 512, 4, 2, 64, 1e-5, 2, 300
+
+
+@pytest.fixture(scope="module")
+def torch():
+    return pytest.importorskip("torch")
+
+
+def dev(torch, a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.float16:
+        a = a.view(np.uint16)
+    return torch.from_numpy(a.copy()).cuda()
+
+
+def bind(torch, kv, lws, head=None):
+    keep, layers = [], []
+    for lw in lws:
+        d = {}
+        for name in ("attn_norm", "ffn_norm"):
+            t = dev(torch, lw[name])
+            keep.append(t)
+            d[name] = t.data_ptr()
+        for i, name in enumerate(("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")):
+            t = dev(torch, lw["w"][i])
+            keep.append(t)
+            d[name] = (t.data_ptr(), lw["wtype"][i])
+        for name in ("bq", "bk", "bv"):
+            if lw[name] is None:
+                d[name] = None
+            else:
+                t = dev(torch, lw[name])
+                keep.append(t)
+                d[name] = t.data_ptr()
+        layers.append(d)
+    if head is None:
+        kv.offload_setup(DIM, FF, NH, EPS, layers)
+    else:
+        on, lm, wt = dev(torch, head[0]), dev(torch, head[1]), head[2]
+        keep += [on, lm]
+        kv.offload_setup(DIM, FF, NH, EPS, layers, on.data_ptr(), (lm.data_ptr(), wt), VOCAB)
+    return keep
+
+
+LAYOUTS = {"f32": dict(n_sink=0, window=0, dtype=F32),
+           "int8": dict(n_sink=2, window=0, dtype=INT8),
+           "ring": dict(n_sink=2, window=4, dtype=F32)}
+
+
+@pytest.mark.parametrize("layout", ["f32", "int8", "ring"])
+@pytest.mark.parametrize("wt,bias", [(W_F32, True), (W_F16, False), (W_Q8_0, True),
+                                     (W_Q4_0, False)])
+def test_decode_token_matches_decode_layer(torch, layout, wt, bias):
+    rng = np.random.default_rng(41 + wt)
+    lws = [layer_weights(rng, DIM, FF, NH, NKV, HD, wt, bias) for _ in range(L)]
+    cap = 16
+    g = HipKV(L, cap, NKV, HD, rope_theta=1e4, **LAYOUTS[layout])
+    o = pyoracle.OracleKV(L, cap, NKV, HD, rope_theta=1e4, **LAYOUTS[layout])
+    keep = bind(torch, g, lws)
+    g.set_stream(torch.cuda.current_stream().cuda_stream)
+    tol = 3e-3 if wt in (W_Q8_0, W_Q4_0) else None
+    for pos in range(9):  # the ring's window of 4 wraps twice
+        x = normal(300 + pos, DIM)
+        xt = dev(torch, x)
+        g.decode_token_async(xt.data_ptr(), pos)
+        torch.cuda.synchronize()
+        got = xt.cpu().numpy().astype(np.float64)
+        want = x.copy()
+        for layer in range(L):
+            want = o.decode_layer(layer, want, pos, lws[layer], DIM, FF, NH, EPS)
+        o.mark_position(pos)
+        want = want.astype(np.float64)
+        bound = (1e-5 + 1e-4 * np.abs(want)) if tol is None else tol * (1 + np.abs(want))
+        err = np.abs(got - want)
+        assert np.all(err <= bound), (f"{layout} wt {wt} pos {pos}: worst "
+                                      f"{float((err - bound).max()):.3e}")
+        assert g.n_seen == pos + 1
+    del keep
+    g.close()
+
+
+@pytest.mark.parametrize("wt", [W_F16, W_Q8_0])
+def test_decode_token_full_logits(torch, wt):
+    rng = np.random.default_rng(7 + wt)
+    lws = [layer_weights(rng, DIM, FF, NH, NKV, HD, wt, True) for _ in range(L)]
+    onorm = (1.0 + 0.1 * rng.standard_normal(DIM)).astype(np.float32)
+    lm = layer_weights(rng, DIM, VOCAB, NH, NKV, HD, wt, False)["w"][4]  # [VOCAB][DIM]
+    g = HipKV(L, 8, NKV, HD, rope_theta=1e4)
+    o = pyoracle.OracleKV(L, 8, NKV, HD, rope_theta=1e4)
+    keep = bind(torch, g, lws, (onorm, lm, wt))
+    g.set_stream(torch.cuda.current_stream().cuda_stream)
+    logits = torch.zeros(VOCAB, device="cuda")
+    tol = 3e-3 if wt == W_Q8_0 else None
+    for pos in range(4):
+        x = normal(500 + pos, DIM)
+        xt = dev(torch, x)
+        g.decode_token_full_async(xt.data_ptr(), pos, logits.data_ptr())
+        torch.cuda.synchronize()
+        want = x.copy()
+        for layer in range(L):
+            want = o.decode_layer(layer, want, pos, lws[layer], DIM, FF, NH, EPS)
+        o.mark_position(pos)
+        wl = pyoracle.logits(want, onorm, lm, wt, EPS, VOCAB).astype(np.float64)
+        got = logits.cpu().numpy().astype(np.float64)
+        bound = (1e-5 + 1e-4 * np.abs(wl)) if tol is None else tol * (1 + np.abs(wl))
+        assert np.all(np.abs(got - wl) <= bound), f"pos {pos}"
+    del keep
+    g.close()
+
+
+def test_offload_errors(torch):
+    g = HipKV(2, 8, NKV, HD, rope_theta=1e4)
+    x = torch.zeros(DIM, device="cuda")
+    with pytest.raises(DbiError) as e:
+        g.decode_token_async(x.data_ptr(), 0)
+    assert "dbi_offload_setup first" in e.value.message
+    rng = np.random.default_rng(3)
+    lw = layer_weights(rng, DIM, FF, NH, NKV, HD, W_F32, False)
+    bad = dict(lw, wtype=[W_F32] * 6 + [6])  # Q5_0 down projection
+    with pytest.raises(DbiError) as e:
+        bind(torch, g, [bad])
+    assert "Q4_0 weights only" in e.value.message
+    with pytest.raises(DbiError) as e:  # three blocks on a two-layer cache
+        bind(torch, g, [lw, lw, lw])
+    assert "n_layers blocks" in e.value.message
+    keep = bind(torch, g, [lw])
+    with pytest.raises(DbiError):
+        g.decode_token_full_async(x.data_ptr(), 0, x.data_ptr())  # no tail bound
+    with pytest.raises(DbiError):
+        g.decode_token_async(x.data_ptr() + 4, 0)  # unaligned residual row
+    with pytest.raises(DbiError):
+        g.decode_token_async(x.data_ptr(), 8)  # past capacity
+    assert g.n_seen == 0
+    del keep
+    g.close()

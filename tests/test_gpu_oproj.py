@@ -15,7 +15,8 @@ import numpy as np
 import pytest
 
 import pyoracle
-from dbinfer_amd.kv import W_F16, W_F32, W_Q8_0, DbiError, HipKV
+from dbinfer_amd.kv import W_F16, W_F32, W_Q4_0, W_Q8_0, DbiError, HipKV
+from test_oracle_layer import q4_blocks
 from test_oracle_oproj import q8_blocks
 
 pytestmark = pytest.mark.gpu
@@ -81,7 +82,7 @@ def test_oproj_errors(torch, kv):
     x = torch.zeros(64, device="cuda")
     for args, msg in [((W_F32, w.data_ptr(), a.data_ptr(), x.data_ptr(), 64, 60), "multiple of 8"),
                       ((W_F32, w.data_ptr(), a.data_ptr(), x.data_ptr(), 0, 64), "dim"),
-                      ((2, w.data_ptr(), a.data_ptr(), x.data_ptr(), 64, 64), "fp32, f16"),
+                      ((6, w.data_ptr(), a.data_ptr(), x.data_ptr(), 64, 64), "fp32, f16"),
                       ((W_F32, w.data_ptr() + 4, a.data_ptr(), x.data_ptr(), 8, 56), "aligned"),
                       ((W_F32, 0, a.data_ptr(), x.data_ptr(), 64, 64), "null")]:
         with pytest.raises(DbiError) as e:
@@ -119,12 +120,12 @@ def test_oproj_graph_replay(torch):
     kv.close()
 
 
-def run_q8(torch, kv, w, a, x, dim, n_in):
+def run_q8(torch, kv, w, a, x, dim, n_in, wtype=W_Q8_0):
     wt = torch.from_numpy(np.ascontiguousarray(w)).cuda()
     at = torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
     xt = torch.from_numpy(np.array(x, np.float32)).cuda()
     kv.set_stream(torch.cuda.current_stream().cuda_stream)
-    kv.oproj_residual_async(W_Q8_0, wt.data_ptr(), at.data_ptr(), xt.data_ptr(), dim, n_in)
+    kv.oproj_residual_async(wtype, wt.data_ptr(), at.data_ptr(), xt.data_ptr(), dim, n_in)
     torch.cuda.synchronize()
     return xt.cpu().numpy()
 
@@ -180,9 +181,49 @@ def test_q8_0_errors(torch, kv):
     with pytest.raises(DbiError) as e:
         kv.oproj_residual_async(W_Q8_0, w.data_ptr() + 2, a.data_ptr(), x.data_ptr(), 2, 32)
     assert "aligned" in e.value.message
-    with pytest.raises(DbiError) as e:
-        kv.oproj_residual_async(2, w.data_ptr(), a.data_ptr(), x.data_ptr(), 2, 32)
-    assert "Q8_0 weights only" in e.value.message
+    with pytest.raises(DbiError) as e:  # Q5_0 (GgmlType 6) is not served
+        kv.oproj_residual_async(6, w.data_ptr(), a.data_ptr(), x.data_ptr(), 2, 32)
+    assert "Q4_0 weights only" in e.value.message
     with pytest.raises(DbiError) as e:  # the quantized row must fit the LDS stage
         kv.oproj_residual_async(W_Q8_0, w.data_ptr(), a.data_ptr(), x.data_ptr(), 1, 32800)
     assert "at most 32768" in e.value.message
+
+
+# ---- Q4_0 (matvec_q4_0_scalar, matmul.cpp:77-99): 18-byte blocks; the block
+# sum is an exact integer, so the same dot-product bound holds
+
+
+@pytest.mark.parametrize("dim,n_in", Q8_SHAPES)
+def test_q4_0_integer_data_bit_exact(torch, kv, dim, n_in):
+    rng = np.random.default_rng(dim * 13 + n_in)
+    nb = n_in // 32
+    a = rng.integers(-127, 128, n_in)
+    a[::32] = 127  # d = 1: the activation codes are its values
+    vals = rng.integers(-8, 8, (dim, nb, 32))
+    w = q4_blocks(vals, np.ones((dim, nb), np.float32))
+    x = rng.integers(-100, 101, dim).astype(np.float32)
+    got = run_q8(torch, kv, w, a.astype(np.float32), x, dim, n_in, W_Q4_0)
+    want = (vals.reshape(dim, n_in) @ a + x.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("dim,n_in", Q8_SHAPES + [(2, 32768)])
+def test_q4_0_random_within_dot_tolerance(torch, kv, dim, n_in):
+    rng = np.random.default_rng(dim * 17 + n_in)
+    nb = n_in // 32
+    a = rng.standard_normal(n_in).astype(np.float32)
+    vals = rng.integers(-8, 8, (dim, nb, 32))
+    scales = np.exp(rng.uniform(-7, -2, (dim, nb))).astype(np.float32)
+    w = q4_blocks(vals, scales)
+    x = rng.standard_normal(dim).astype(np.float32)
+    got = run_q8(torch, kv, w, a, x, dim, n_in, W_Q4_0).astype(np.float64)
+    want = (x + pyoracle.matvec(w, W_Q4_0, a, dim)).astype(np.float64)
+    aq = pyoracle.quantize_row_q8_0(a).reshape(nb, 34)
+    dx = aq[:, :2].copy().view(np.float16).astype(np.float64).ravel()
+    xc = aq[:, 2:].view(np.int8).astype(np.int64)
+    dw = scales.astype(np.float16).astype(np.float64)
+    sumi = np.einsum("dbi,bi->db", vals, xc)
+    mag = np.abs(dw * dx[None, :] * sumi).sum(axis=1)
+    bound = 1e-5 + 1e-4 * np.abs(want) + 2 * nb * 2.0 ** -24 * mag
+    err = np.abs(got - want)
+    assert np.all(err <= bound), f"worst {float((err - bound).max()):.3e}"
