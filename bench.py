@@ -470,6 +470,98 @@ def run_oproj(torch, HipKV, args):
     kv.close()
 
 
+# Full-layer offload shapes: the configs' models, Q8_0
+# weights (the reference's offload reads F16 / Q8_0 / Q4_0, backend.hpp:17-18)
+LAYER_CONFIGS = [
+    # name, layers, dim, ff, nh, nkv, hd, kv dtype, n_sink, position decoded, vocab
+    ("Llama-3.2-3B (C3 model), int8 KV at 8k", 28, 3072, 8192, 24, 8, 128, "int8", 4, 8191,
+     128256),
+    ("Qwen2.5-7B (C4 model), dense fp32 KV at 4k", 28, 3584, 18944, 28, 4, 128, "f32", 0, 4095,
+     152064),
+]
+
+
+def q8_weight(torch, out: int, n_in: int, gen):
+    """Random Q8_0 blocks [out][n_in/32][34]: codes uniform in [-127, 127],
+    every block scale f16(0.5 / sqrt(n_in) / 73), so a matvec's gain stays
+    about 1/2 (no overflow through the layers)."""
+    w = torch.randint(-127, 128, (out, n_in // 32, 34), dtype=torch.int8, device="cuda",
+                      generator=gen).view(torch.uint8)
+    sc = torch.full((out, n_in // 32), 0.5 / np.sqrt(n_in) / 73.0, dtype=torch.float16,
+                    device="cuda")
+    w[..., :2] = sc.view(torch.uint8).view(out, n_in // 32, 2)
+    return w
+
+
+def run_layer(torch, HipKV, F32, INT8, args):
+    """The full-layer offload (dbi_decode_token_full_async): every layer of
+    one token (rmsnorm, q/k/v, the fused produce + append + attention, o_proj,
+    gate/up, silu*up, down) and the lm_head, replayed from a graph; per token
+    its time and the algorithmic bytes it streams (the weights once, the
+    layer's KV attention bytes) against the HBM peak."""
+    from dbinfer_amd.kv import W_Q8_0
+
+    for (name, L_, dim, ff, nh, nkv, hd, dt, ns, pos, vocab) in LAYER_CONFIGS:
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(9)
+        stream = torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            qn, kvn = nh * hd, nkv * hd
+            ws, layers = [], []
+            for _ in range(L_):
+                m = {"wq": q8_weight(torch, qn, dim, gen), "wk": q8_weight(torch, kvn, dim, gen),
+                     "wv": q8_weight(torch, kvn, dim, gen), "wo": q8_weight(torch, dim, qn, gen),
+                     "wgate": q8_weight(torch, ff, dim, gen), "wup": q8_weight(torch, ff, dim, gen),
+                     "wdown": q8_weight(torch, dim, ff, gen)}
+                ws.append(m)
+            ones = torch.ones(dim, device="cuda")
+            for m in ws:
+                layers.append({"attn_norm": ones.data_ptr(), "ffn_norm": ones.data_ptr(),
+                               **{k: (v.data_ptr(), W_Q8_0) for k, v in m.items()}})
+            lm = q8_weight(torch, vocab, dim, gen)
+            wbytes = sum(v.numel() for m in ws for v in m.values()) + lm.numel()
+            kv = HipKV(L_, pos + 1, nkv, hd, ns, 0, INT8 if dt == "int8" else F32, 1e6)
+            kv.set_stream(stream.cuda_stream)
+            P = nkv * hd
+            K = torch.randn(pos, P, device="cuda", generator=gen)
+            V = torch.randn(pos, P, device="cuda", generator=gen)
+            for layer in range(L_):
+                kv.append_async(layer, 0, pos, K.data_ptr(), V.data_ptr())
+            del K, V
+            kv.offload_setup(dim, ff, nh, 1e-5, layers, ones.data_ptr(), (lm.data_ptr(), W_Q8_0),
+                             vocab)
+            x0 = torch.randn(dim, device="cuda", generator=gen)
+            x = torch.empty_like(x0)
+            logits = torch.empty(vocab, device="cuda")
+            torch.cuda.synchronize()
+
+            def step(s_):
+                kv.set_stream(s_.cuda_stream)
+                x.copy_(x0)
+                kv.decode_token_full_async(x.data_ptr(), pos, logits.data_ptr())
+
+            g = capture(torch, step)
+            for _ in range(3):
+                g.replay()
+            ms = time_graph(torch, g, max(5, args.config_steps // 2))
+            kvb = L_ * config_bytes(dt, nkv, hd, pos + 1, ns, False)
+            tot = wbytes + kvb
+            finite = bool(torch.isfinite(logits).all().item())
+            print(json.dumps({"layer_offload": name, "layers": L_, "dim": dim, "ff": ff,
+                              "n_heads": nh, "n_kv_heads": nkv, "weights": "q8_0",
+                              "kv": dt, "pos": pos, "vocab": vocab,
+                              "us_per_token": round(1000.0 * ms, 1),
+                              "us_per_layer": round(1000.0 * ms / L_, 2),
+                              "weight_bytes_per_token": int(wbytes), "kv_bytes_per_token": int(kvb),
+                              "GBs": round(tot / (ms * 1e-3) / 1e9, 1),
+                              "frac_of_peak": round(tot / (ms * 1e-3) / 1e9 / PEAK_GBS, 4),
+                              "logits_finite": finite}), flush=True)
+            del g
+            kv.close()
+            del ws, layers, lm
+        torch.cuda.synchronize()
+
+
 def run_ctx_sweep(torch, HipKV, F32, INT8, args):
     """Config 3's shape over the target context range (8k-32k): one JSON line
     per (context, KV dtype) with the fused decode step and the attention-only
@@ -629,6 +721,8 @@ def main():
                     help="time the output projection + residual add at the configs' shapes")
     ap.add_argument("--verify", action="store_true",
                     help="time the verify round's token side (argmax + merge) at C5's shape")
+    ap.add_argument("--layer", action="store_true",
+                    help="time the full-layer offload (decode_token_full) at the configs' models")
     ap.add_argument("--ctx-sweep", action="store_true",
                     help="instead of the bench line, config 3's shape at ctx 8k, 16k, 32k")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -661,6 +755,9 @@ def main():
         return
     if args.oproj:
         run_oproj(torch, HipKV, args)
+        return
+    if args.layer:
+        run_layer(torch, HipKV, F32, INT8, args)
         return
     if args.verify:
         # C5's verify round, token side, at k = 4 and 8 (Qwen3's vocabulary)
