@@ -437,8 +437,41 @@ dbi_status check_matvec(uint32_t wtype, const void* w, const void* x, uint32_t o
   return DBI_OK;
 }
 
+bool quant_weight(uint32_t type) { return type == DBI_W_Q8_0 || type == DBI_W_Q4_0; }
+
+// the fused quantized matvec kernels take rows of an even block count
+bool fused_matvec(uint32_t type, uint32_t in) { return quant_weight(type) && in % 64 == 0; }
+
+// y = W x, or y += W x with accumulate. With norm_w the activation is
+// rmsnorm(x, norm_w) (eps of the offload): quantized weights normalize inside
+// the matvec launch; float weights read the handle's normalized row, written
+// once per activation (*normed tracks that).
 hipError_t run_matvec(dbi_kv* kv, const dbi_weight& w, const float* x, float* y, uint32_t out,
-                      uint32_t in, bool accumulate) {
+                      uint32_t in, bool accumulate, const float* norm_w = nullptr,
+                      bool* normed = nullptr) {
+  if (fused_matvec(w.type, in)) {
+    dbi::MatvecCall c{};
+    c.x = x;
+    c.norm_w = norm_w;
+    c.eps = kv->off.cfg.rms_eps;
+    c.in = static_cast<int>(in);
+    c.q4 = w.type == DBI_W_Q4_0;
+    c.nseg = 1;
+    c.w[0] = w.data;
+    c.y[0] = y;
+    c.rows[0] = static_cast<int>(out);
+    c.acc = accumulate;
+    return dbi::launch_matvec_q(c, kv->stream);
+  }
+  if (norm_w != nullptr) {
+    if (!*normed) {
+      hipError_t e = dbi::launch_rmsnorm(x, norm_w, kv->off.cfg.rms_eps, kv->off.normed,
+                                         static_cast<int>(in), kv->stream);
+      if (e != hipSuccess) return e;
+      *normed = true;
+    }
+    x = kv->off.normed;
+  }
   dbi::OprojCall c{};
   c.w = w.data;
   c.attn = x;
@@ -454,7 +487,10 @@ hipError_t run_matvec(dbi_kv* kv, const dbi_weight& w, const float* x, float* y,
 
 // Model::decode_layer (model.cpp:730-787) for every bound block at pos, on
 // the handle's stream. All checks come first; the q/k/v step is the
-// producer's fused decode (decode_qkv_impl).
+// producer's fused decode (decode_qkv_impl). With quantized weights of one
+// type and dim, ff multiples of 64 a block is five launches: rmsnorm + q/k/v
+// matvecs, the fused decode, o_proj + residual, rmsnorm + gate/up + silu *
+// up, down + residual.
 dbi_status decode_token_impl(dbi_kv* kv, float* x, uint32_t pos) {
   const OffloadState& o = kv->off;
   if (o.layers.empty()) return fail(DBI_ERR_INVALID, "decode_token needs dbi_offload_setup first");
@@ -464,22 +500,62 @@ dbi_status decode_token_impl(dbi_kv* kv, float* x, uint32_t pos) {
   const uint32_t hd = kv->cfg.head_dim, nkv = kv->cfg.n_kv_heads, nh = o.cfg.n_heads;
   const uint32_t dim = o.cfg.dim, ff = o.cfg.ff, qn = nh * hd, kvn = nkv * hd;
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+  const uint32_t nr = static_cast<uint32_t>(dbi::matvec_rows_per_task());
   hipStream_t st = kv->stream;
   for (uint32_t l = 0; l < o.layers.size(); ++l) {
     const dbi_layer_weights& L = o.layers[l];
-    HIP_TRY(dbi::launch_rmsnorm(x, L.attn_norm, o.cfg.rms_eps, o.normed, int(dim), st),
-            "rmsnorm launch");
-    HIP_TRY(run_matvec(kv, L.wq, o.normed, o.q, qn, dim, false), "q matvec launch");
-    HIP_TRY(run_matvec(kv, L.wk, o.normed, o.k, kvn, dim, false), "k matvec launch");
-    HIP_TRY(run_matvec(kv, L.wv, o.normed, o.v, kvn, dim, false), "v matvec launch");
+    bool normed = false;
+    if (fused_matvec(L.wq.type, dim) && L.wk.type == L.wq.type && L.wv.type == L.wq.type &&
+        qn % nr == 0 && kvn % nr == 0) {
+      dbi::MatvecCall c{};
+      c.x = x;
+      c.norm_w = L.attn_norm;
+      c.eps = o.cfg.rms_eps;
+      c.in = static_cast<int>(dim);
+      c.q4 = L.wq.type == DBI_W_Q4_0;
+      c.nseg = 3;
+      c.w[0] = L.wq.data;
+      c.w[1] = L.wk.data;
+      c.w[2] = L.wv.data;
+      c.y[0] = o.q;
+      c.y[1] = o.k;
+      c.y[2] = o.v;
+      c.rows[0] = static_cast<int>(qn);
+      c.rows[1] = c.rows[2] = static_cast<int>(kvn);
+      HIP_TRY(dbi::launch_matvec_q(c, st), "q/k/v matvec launch");
+    } else {
+      HIP_TRY(run_matvec(kv, L.wq, x, o.q, qn, dim, false, L.attn_norm, &normed),
+              "q matvec launch");
+      HIP_TRY(run_matvec(kv, L.wk, x, o.k, kvn, dim, false, L.attn_norm, &normed),
+              "k matvec launch");
+      HIP_TRY(run_matvec(kv, L.wv, x, o.v, kvn, dim, false, L.attn_norm, &normed),
+              "v matvec launch");
+    }
     const RawQkv r{o.q, o.k, o.v, L.bq, L.bk, L.bv};
     if (dbi_status s2 = decode_qkv_impl(kv, l, pos, nh, scale, r, o.attn)) return s2;
     HIP_TRY(run_matvec(kv, L.wo, o.attn, x, dim, qn, true), "o_proj launch");
-    HIP_TRY(dbi::launch_rmsnorm(x, L.ffn_norm, o.cfg.rms_eps, o.normed, int(dim), st),
-            "rmsnorm launch");
-    HIP_TRY(run_matvec(kv, L.wgate, o.normed, o.gate, ff, dim, false), "gate matvec launch");
-    HIP_TRY(run_matvec(kv, L.wup, o.normed, o.up, ff, dim, false), "up matvec launch");
-    HIP_TRY(dbi::launch_silu_mul(o.gate, o.up, int(ff), st), "silu launch");
+    normed = false;
+    if (fused_matvec(L.wgate.type, dim) && L.wup.type == L.wgate.type) {
+      dbi::MatvecCall c{};
+      c.x = x;
+      c.norm_w = L.ffn_norm;
+      c.eps = o.cfg.rms_eps;
+      c.in = static_cast<int>(dim);
+      c.q4 = L.wgate.type == DBI_W_Q4_0;
+      c.nseg = 2;
+      c.w[0] = L.wgate.data;
+      c.w[1] = L.wup.data;
+      c.y[0] = c.y[1] = o.gate;
+      c.rows[0] = c.rows[1] = static_cast<int>(ff);
+      c.pair = true;
+      HIP_TRY(dbi::launch_matvec_q(c, st), "gate/up matvec launch");
+    } else {
+      HIP_TRY(run_matvec(kv, L.wgate, x, o.gate, ff, dim, false, L.ffn_norm, &normed),
+              "gate matvec launch");
+      HIP_TRY(run_matvec(kv, L.wup, x, o.up, ff, dim, false, L.ffn_norm, &normed),
+              "up matvec launch");
+      HIP_TRY(dbi::launch_silu_mul(o.gate, o.up, int(ff), st), "silu launch");
+    }
     HIP_TRY(run_matvec(kv, L.wdown, o.gate, x, dim, ff, true), "down matvec launch");
   }
   return DBI_OK;
@@ -1539,10 +1615,9 @@ dbi_status dbi_decode_token_full_async(dbi_kv* kv, float* x_dev, uint32_t pos,
     return fail(DBI_ERR_INVALID, "decode_token_full needs an offload tail (lm_head)");
   if (logits_dev == nullptr) return fail(DBI_ERR_INVALID, "null logits");
   if (dbi_status st = decode_token_impl(kv, x_dev, pos)) return st;
-  const int dim = static_cast<int>(o.cfg.dim);
-  HIP_TRY(dbi::launch_rmsnorm(x_dev, o.cfg.output_norm, o.cfg.rms_eps, o.normed, dim, kv->stream),
-          "rmsnorm launch");
-  HIP_TRY(run_matvec(kv, o.cfg.lm_head, o.normed, logits_dev, o.cfg.vocab, o.cfg.dim, false),
+  bool normed = false;
+  HIP_TRY(run_matvec(kv, o.cfg.lm_head, x_dev, logits_dev, o.cfg.vocab, o.cfg.dim, false,
+                     o.cfg.output_norm, &normed),
           "lm_head launch");
   return DBI_OK;
 }

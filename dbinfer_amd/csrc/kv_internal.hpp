@@ -265,18 +265,39 @@ struct VerifyCall {
 };
 hipError_t launch_verify(const VerifyCall& c, hipStream_t st);
 
-// The matvecs of decode_layer (oproj.hip): x[o] += sum_i w[o][i] * attn[i]
-// (or x[o] = ... with overwrite), w fp32 or f16 [dim][in] (in % 8 == 0) or
-// Q8_0 / Q4_0 blocks [dim][in/32] (in % 32 == 0).
+// The unfused matvecs of decode_layer (oproj.hip): x[o] += sum_i w[o][i] *
+// attn[i] (or x[o] = ... with overwrite), w fp32 or f16 [dim][in] (in % 8 ==
+// 0), or Q8_0 / Q4_0 blocks [dim][in/32] with in % 64 == 32 (the even block
+// counts run launch_matvec_q).
 struct OprojCall {
   const void* w;
   const float* attn;
   float* x;
   int dim, in;
-  bool f16, q8, q4;
+  bool f16, q8, q4;  // else fp32
   bool overwrite;
 };
 hipError_t launch_oproj(const OprojCall& c, hipStream_t st);
+// Quantized matvecs (Q8_0 / Q4_0 weights, the activation quantized to Q8_0
+// in each workgroup), optionally with rmsnorm(x, norm_w) in front. Plain:
+// nseg matrices of rows[s] rows over the same activation, y[s] = W_s x (or
+// y[s] += W_s x with acc); every segment but the last needs a multiple of
+// matvec_rows_per_task() rows. Pair: w[0] gate and w[1] up of rows[0] rows,
+// y[0] = silu(gate x) * (up x).
+struct MatvecCall {
+  const float* x;
+  const float* norm_w;
+  float eps;
+  int in;
+  bool q4;
+  int nseg;
+  const void* w[3];
+  float* y[3];
+  int rows[3];
+  bool pair, acc;
+};
+hipError_t launch_matvec_q(const MatvecCall& c, hipStream_t st);
+int matvec_rows_per_task();
 // rmsnorm of one row (ops.cpp:7-17) and silu(g) * u in place (model.cpp:781-782)
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* out, int dim,
                           hipStream_t st);

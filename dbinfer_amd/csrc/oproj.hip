@@ -1,16 +1,15 @@
-// The matvecs of decode_layer (model.cpp:738-785) and forward's lm_head
-// (:915): tensor::matvec_quant ([out][in] row-major weights) of one
+// The unfused matvecs of decode_layer (model.cpp:738-785) and forward's
+// lm_head (:915): tensor::matvec_quant ([out][in] row-major weights) of one
 // activation row,
 //   y[o] = W[o] · x          (q, k, v, gate, up, lm_head)
 //   y[o] += W[o] · x         (o_proj and down, the residual adds)
 // for fp32 weights (tensor::matvec, matmul.cpp:36-43), f16 weights
 // (tensor::matvec_f16, matmul.cpp:45-54; every f16 weight converts exactly to
-// fp32 and is fused-multiply-added), Q8_0 blocks (matvec_q8_0_scalar,
-// matmul.cpp:56-75) and Q4_0 blocks (matvec_q4_0_scalar, :77-99), the
-// quantized types with the activation row quantized to Q8_0 first
-// (quantize_row_q8_0, dequant.cpp:80-97). The other GGUF block formats are
-// not served. The layer's rmsnorm (ops.cpp:7-17) and silu(gate) * up
-// (model.cpp:781-782, ops.cpp:54-56) are here too.
+// fp32 and is fused-multiply-added) and Q8_0 / Q4_0 rows of an odd block
+// count (matvec_q8_0_scalar / matvec_q4_0_scalar, matmul.cpp:56-99; the even
+// block counts run the fused kernels of matvec.hip). The layer's rmsnorm
+// (ops.cpp:7-17) and silu(gate) * up (model.cpp:781-782, ops.cpp:54-56) for
+// these unfused paths are here too.
 //
 // One wave per output row: each lane accumulates its share of the row with
 // fused multiply-adds, the wave sums the lanes, and lane 0 adds the result to
@@ -109,6 +108,15 @@ __global__ __launch_bounds__(kThreads) void oproj_kernel(OprojArgs a) {
   if (lane == 0) put_row(a, row, proj);
 }
 
+// global-address-space views (the block pointers are computed as integers)
+typedef __attribute__((address_space(1))) const uint32_t gu32;
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const f4v gf4;
+
+// Rows whose block count is odd (in % 64 == 32), which the pair-layout
+// kernels of matvec.hip do not take, run these per-block kernels (unfused:
+// the offload composes them with the rmsnorm and silu kernels below).
+//
 // Q8_0: a block is an f16 scale then 32 int8 codes (34 bytes). Each
 // workgroup first quantizes the activation row into LDS with
 // quantize_row_q8_0's arithmetic (amax over the block, d = amax / 127,
@@ -137,11 +145,11 @@ __device__ inline uint32_t pack4(int8_t a, int8_t b, int8_t c, int8_t d) {
 constexpr int kQStride4 = 10;
 __device__ inline void quantize_act(const float* x, int nbk, uint32_t* s_xq, int stride) {
   for (int b = threadIdx.x; b < nbk; b += kThreads) {
-    const float4* xb = reinterpret_cast<const float4*>(x + static_cast<size_t>(b) * 32);
+    gf4* xb = (gf4*)(x + static_cast<size_t>(b) * 32);
     float v[32];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float4 t = xb[i];
+      const f4v t = xb[i];
       v[4 * i] = t.x;
       v[4 * i + 1] = t.y;
       v[4 * i + 2] = t.z;
@@ -186,7 +194,7 @@ __global__ __launch_bounds__(kThreads) void oproj_q8_kernel(OprojArgs a) {
         const int b = min(b0 + 64 * q, nbk - 1);
         const uintptr_t p = wrow + static_cast<size_t>(b) * 34;
         off[q] = static_cast<uint32_t>(p & 2);
-        const uint32_t* base = reinterpret_cast<const uint32_t*>(p & ~static_cast<uintptr_t>(3));
+        gu32* base = (gu32*)(p & ~static_cast<uintptr_t>(3));
 #pragma unroll
         for (int i = 0; i < 9; ++i) wd[q][i] = base[i];
       }
@@ -243,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void oproj_q4_kernel(OprojArgs a) {
         const int b = min(b0 + 64 * q, nbk - 1);
         const uintptr_t p = wrow + static_cast<size_t>(b) * 18;
         off[q] = static_cast<uint32_t>(p & 2);
-        const uint32_t* base = reinterpret_cast<const uint32_t*>(p & ~static_cast<uintptr_t>(3));
+        gu32* base = (gu32*)(p & ~static_cast<uintptr_t>(3));
 #pragma unroll
         for (int i = 0; i < 5; ++i) wd[q][i] = base[i];
       }

@@ -11,9 +11,13 @@ the rounding of its sums: |a - b| <= 1e-5 + 1e-4 |b| on the residual stream
 and the logits. Q8_0 / Q4_0 weights quantize each activation row to Q8_0
 first (quantize_row_q8_0); an activation a rounding away from a code
 boundary can land on the other code (the reference's own result moves the
-same way with its compiler's contraction of rmsnorm's sum), which moves a
-matvec output by up to d_w * 127 * d_x, here ~2e-3; those layers are checked
-to 3e-3 (absolute and relative). The synthetic weights have the float ones'
+same way with its compiler's contraction of rmsnorm's sum). One such flip
+moves every output of that matvec by up to d_w * 127 * d_x (d_w <= 1e-3 for
+the synthetic Q8_0 weights, d_x ~ 0.02 for a normalized row: ~2.5e-3), and
+flips in the four quantized activations of a block compound over the two
+blocks, so quantized weights are checked to QTOL = 1e-2 (absolute and
+relative). A wiring error (a wrong segment, norm weight or gate/up order)
+moves the stream by O(0.1) and still fails. The synthetic weights have the float ones'
 spread (std ~0.05: every matvec's gain is below 1), so a flip in one layer
 is not amplified by the next; with hotter random weights (gain ~1.5 per
 matvec, a residual stream of |x| ~ 20) one layer-0 flip of 0.0017 grew to
@@ -33,6 +37,7 @@ from test_oracle_layer import layer_weights
 pytestmark = pytest.mark.gpu
 
 DIM, FF, NH, NKV, HD, EPS, L, VOCAB = 256, 512, 4, 2, 64, 1e-5, 2, 300
+QTOL = 1e-2
 
 
 @pytest.fixture(scope="module")
@@ -47,7 +52,7 @@ def dev(torch, a):
     return torch.from_numpy(a.copy()).cuda()
 
 
-def bind(torch, kv, lws, head=None):
+def bind(torch, kv, lws, head=None, dims=(DIM, FF, NH)):
     keep, layers = [], []
     for lw in lws:
         d = {}
@@ -68,7 +73,7 @@ def bind(torch, kv, lws, head=None):
                 d[name] = t.data_ptr()
         layers.append(d)
     if head is None:
-        kv.offload_setup(DIM, FF, NH, EPS, layers)
+        kv.offload_setup(*dims, EPS, layers)
     else:
         on, lm, wt = dev(torch, head[0]), dev(torch, head[1]), head[2]
         keep += [on, lm]
@@ -92,7 +97,7 @@ def test_decode_token_matches_decode_layer(torch, layout, wt, bias):
     o = pyoracle.OracleKV(L, cap, NKV, HD, rope_theta=1e4, **LAYOUTS[layout])
     keep = bind(torch, g, lws)
     g.set_stream(torch.cuda.current_stream().cuda_stream)
-    tol = 3e-3 if wt in (W_Q8_0, W_Q4_0) else None
+    tol = QTOL if wt in (W_Q8_0, W_Q4_0) else None
     for pos in range(9):  # the ring's window of 4 wraps twice
         x = normal(300 + pos, DIM)
         xt = dev(torch, x)
@@ -113,6 +118,42 @@ def test_decode_token_matches_decode_layer(torch, layout, wt, bias):
     g.close()
 
 
+# dim 160 and ff 224 are odd block counts (5 and 7 blocks of 32): those
+# matvecs run the unfused per-block kernels with a separate rmsnorm; mixed
+# types split the fused q/k/v and gate/up launches
+@pytest.mark.parametrize("wts", [
+    [W_Q8_0] * 7,
+    [W_Q4_0] * 7,
+    [W_Q8_0, W_Q4_0, W_Q8_0, W_Q4_0, W_Q8_0, W_Q4_0, W_Q8_0],
+    [W_F16, W_Q8_0, W_Q8_0, W_Q8_0, W_Q4_0, W_F32, W_Q8_0],
+])
+@pytest.mark.parametrize("dim,ff", [(160, 224), (256, 224), (192, 512)])
+def test_decode_token_odd_blocks_mixed_types(torch, wts, dim, ff):
+    nh, nkv, hd = 2, 1, 64
+    rng = np.random.default_rng(dim + ff + sum(wts))
+    lws = [layer_weights(rng, dim, ff, nh, nkv, hd, wts, True) for _ in range(L)]
+    g = HipKV(L, 8, nkv, hd, rope_theta=1e4)
+    o = pyoracle.OracleKV(L, 8, nkv, hd, rope_theta=1e4)
+    keep = bind(torch, g, lws, dims=(dim, ff, nh))
+    g.set_stream(torch.cuda.current_stream().cuda_stream)
+    for pos in range(3):
+        x = normal(700 + pos, dim)
+        xt = dev(torch, x)
+        g.decode_token_async(xt.data_ptr(), pos)
+        torch.cuda.synchronize()
+        got = xt.cpu().numpy().astype(np.float64)
+        want = x.copy()
+        for layer in range(L):
+            want = o.decode_layer(layer, want, pos, lws[layer], dim, ff, nh, EPS)
+        o.mark_position(pos)
+        want = want.astype(np.float64)
+        err = np.abs(got - want)
+        bound = QTOL * (1 + np.abs(want))
+        assert np.all(err <= bound), f"{wts} {dim}x{ff} pos {pos}: worst {float((err - bound).max()):.3e}"
+    del keep
+    g.close()
+
+
 @pytest.mark.parametrize("wt", [W_F16, W_Q8_0])
 def test_decode_token_full_logits(torch, wt):
     rng = np.random.default_rng(7 + wt)
@@ -124,7 +165,7 @@ def test_decode_token_full_logits(torch, wt):
     keep = bind(torch, g, lws, (onorm, lm, wt))
     g.set_stream(torch.cuda.current_stream().cuda_stream)
     logits = torch.zeros(VOCAB, device="cuda")
-    tol = 3e-3 if wt == W_Q8_0 else None
+    tol = QTOL if wt == W_Q8_0 else None
     for pos in range(4):
         x = normal(500 + pos, DIM)
         xt = dev(torch, x)

@@ -117,7 +117,13 @@ def test_matvec_quantized_against_integer_restatement(wt, out, n_in):
 
 
 def layer_weights(rng, dim, ff, nh, nkv, hd, wt, bias):
+    """One block's weights; wt is one type for all seven matrices or a list of
+    seven (wq wk wv wo wgate wup wdown)."""
+    wts = list(wt) if isinstance(wt, (list, tuple)) else [wt] * 7
+    it = iter(wts)
+
     def mat(o, i):
+        wt = next(it)
         if wt in (W_F32, W_F16):
             m = (rng.standard_normal((o, i)) * 0.05).astype(np.float32)
             return m.astype(np.float16).view(np.uint16) if wt == W_F16 else m
@@ -136,7 +142,7 @@ def layer_weights(rng, dim, ff, nh, nkv, hd, wt, bias):
         "ffn_norm": (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32),
         "w": [mat(qn, dim), mat(kvn, dim), mat(kvn, dim), mat(dim, qn), mat(ff, dim),
               mat(ff, dim), mat(dim, ff)],
-        "wtype": [wt] * 7,
+        "wtype": wts,
         "bq": (0.1 * rng.standard_normal(qn)).astype(np.float32) if bias else None,
         "bk": (0.1 * rng.standard_normal(kvn)).astype(np.float32) if bias else None,
         "bv": (0.1 * rng.standard_normal(kvn)).astype(np.float32) if bias else None,
