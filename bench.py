@@ -429,19 +429,21 @@ OPROJ_SHAPES = [("C1 TinyLlama", 2048, 2048), ("C3 Llama-3.2-3B", 3072, 3072),
 
 def run_oproj(torch, HipKV, args):
     """decode_layer's step after attention (model.cpp:773-774): the output
-    projection of the attention row plus the residual add, fp32, f16 and
-    Q8_0 weights, one call per layer with the layer's own weights (graph replay),
-    and its GB/s against the HBM peak (the weights are read once)."""
-    from dbinfer_amd.kv import W_F16, W_F32, W_Q8_0
+    projection of the attention row plus the residual add, fp32, f16, Q8_0
+    and Q4_0 weights, one call per layer with the layer's own weights (graph
+    replay), and its GB/s against the HBM peak (the weights are read once)."""
+    from dbinfer_amd.kv import W_F16, W_F32, W_Q4_0, W_Q8_0
 
     kv = HipKV(1, 64, 1, 64)
     for name, dim, n_in in OPROJ_SHAPES:
         L_ = 16  # distinct weight matrices, so no call reads another's from cache
         for wname, wtype, dt, esz in (("f32", W_F32, torch.float32, 4),
                                       ("f16", W_F16, torch.float16, 2),
-                                      ("q8_0", W_Q8_0, torch.uint8, 34 / 32)):
-            if wtype == W_Q8_0:  # random codes, every block scale 2^-8
-                w = torch.randint(0, 256, (L_, dim, n_in // 32, 34), dtype=torch.uint8,
+                                      ("q8_0", W_Q8_0, torch.uint8, 34 / 32),
+                                      ("q4_0", W_Q4_0, torch.uint8, 18 / 32)):
+            if wtype in (W_Q8_0, W_Q4_0):  # random codes, every block scale 2^-8
+                bb = 34 if wtype == W_Q8_0 else 18
+                w = torch.randint(0, 256, (L_, dim, n_in // 32, bb), dtype=torch.uint8,
                                   device="cuda")
                 w[..., 0] = 0x00
                 w[..., 1] = 0x1C
