@@ -275,17 +275,24 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   const rsrc_t rvs = make_rsrc(P.vs + head * NB, P.capg * NB * 4);
 
   using Buf = MBuf<HD, NQ>;
-  // one chunk buffer: fewer registers, and measured no slower than two (the
-  // next chunk's loads wait for the current chunk's math either way)
+  // one chunk buffer, refilled half by half (issue_k, issue_v) as the
+  // chunk's math frees it
   constexpr int NBUF = 1;
 
   // Every chunk issues the same loads, so the load waits are exact; a chunk
   // past c_end reads from p0 = capg, past the end of every array (reads
   // return 0). The group a fused step requantizes is read as well and
   // replaced from LDS.
-  auto issue = [&](Buf& b, int ch) {
-    const bool live = ch < c_end;
-    const int p0 = __builtin_amdgcn_readfirstlane(live ? ch * CHUNK : P.capg);
+  // A chunk's K half (codes, the group's channel scales) and V half (codes,
+  // block scales) are issued separately: the next chunk's K goes out as soon
+  // as this chunk's QK^T has read its K registers, its V as soon as PV has
+  // read V, so a wave always has loads in flight instead of waiting for its
+  // whole chunk before requesting the next.
+  auto chunk_p0 = [&](int ch) {
+    return __builtin_amdgcn_readfirstlane(ch < c_end ? ch * CHUNK : P.capg);
+  };
+  auto issue_k = [&](Buf& b, int ch) {
+    const int p0 = chunk_p0(ch);
     const int base = p0 * HD;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -295,12 +302,20 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     const int so = (p0 / kKGroup) * HD * 4;
     b.ks[0] = load_b128(rks, 32 * c8, so);
     b.ks[1] = load_b128(rks, 32 * c8 + 16, so);
+  };
+  auto issue_v = [&](Buf& b, int ch) {
+    const int p0 = chunk_p0(ch);
+    const int base = p0 * HD;
 #pragma unroll
     for (int tp = 0; tp < VL; ++tp)
       b.v[tp] = __builtin_bit_cast(uint4, stream_b128(rv, lane * 16, base + tp * 1024));
 #pragma unroll
     for (int s = 0; s < 8; ++s)
       b.vs[s] = load_b32(rvs, ((16 * (s / 4) + 4 * grp + s % 4) * NB + col % NBK) * 4, p0 * NB * 4);
+  };
+  auto issue = [&](Buf& b, int ch) {
+    issue_k(b, ch);
+    issue_v(b, ch);
   };
 
   // ---- q * scale * log2(e) of this lane's 8 channels of query T*QVT + qvl
@@ -345,10 +360,8 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   if (app_owner) App::load_row(A, kh, lane, app_in);
   __builtin_amdgcn_sched_barrier(0);
   const int ch0 = split * P.chunks_per_split + wave;  // chunk t of this wave: ch0 + t * 8
-  Buf RA, RB;
+  Buf RA;
   issue(RA, ch0);
-  __builtin_amdgcn_sched_barrier(0);
-  if constexpr (NBUF == 2 && CPW != 1) issue(RB, ch0 + kWaves);
   __builtin_amdgcn_sched_barrier(0);
   if (app_share) App::requant_share(A, wave, lane, app_knew, app_raw, s_kg);
 #pragma unroll
@@ -369,7 +382,8 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     for (int t = 0; t < NTV; ++t) o[T][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  auto compute = [&](Buf& b, const int ch, const bool first) {
+  // next >= 0: the chunk whose loads go into b as this chunk frees it
+  auto compute = [&](Buf& b, const int ch, const bool first, const int next) {
     // products feeding split3 are rounded to fp32 first (q * ks, as the
     // reference rounds it; p * vs): no contraction into the split's subtraction
 #pragma clang fp contract(off)
@@ -453,6 +467,12 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
         }
     }
 
+    if (next >= 0) {  // uniform: this chunk's K registers are read
+      __builtin_amdgcn_sched_barrier(0);
+      issue_k(b, next);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
     // ---- online softmax per column, then the PV A operand of the lane
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
@@ -510,36 +530,29 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
         for (int a = 0; a < 3; ++a) o[T][t] = mfma(aw[a], bv, o[T][t]);
       }
     }
+    if (next >= 0) {  // uniform: this chunk's V registers are read
+      __builtin_amdgcn_sched_barrier(0);
+      issue_v(b, next);
+    }
     __builtin_amdgcn_wave_barrier();
   };
 
+  static_assert(NBUF == 1, "the next chunk's loads reuse the one buffer");
   if constexpr (CPW > 0) {
 #pragma unroll
     for (int t = 0; t < CPW; ++t) {
-      Buf& X = (NBUF == 2 && (t & 1)) ? RB : RA;
       const int cht = ch0 + t * kWaves;
-      if (cht < c_end) compute(X, cht, t == 0);
-      __builtin_amdgcn_sched_barrier(0);
-      if (t + NBUF < CPW) issue(X, ch0 + (t + NBUF) * kWaves);
+      if (cht < c_end) compute(RA, cht, t == 0, t + 1 < CPW ? cht + kWaves : -1);
       __builtin_amdgcn_sched_barrier(0);
     }
   } else {
     int ch = ch0;
     bool first = true;
     while (ch < c_end) {
-      compute(RA, ch, first);
+      compute(RA, ch, first, ch + kWaves);
       first = false;
       __builtin_amdgcn_sched_barrier(0);
-      issue(RA, ch + NBUF * kWaves);
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (NBUF == 2) {
-        if (ch + kWaves >= c_end) break;
-        compute(RB, ch + kWaves, false);
-        __builtin_amdgcn_sched_barrier(0);
-        issue(RB, ch + 3 * kWaves);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      ch += NBUF * kWaves;
+      ch += kWaves;
     }
   }
 
