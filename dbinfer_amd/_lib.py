@@ -104,6 +104,10 @@ SIGNATURES = {
                                 _u32]),
     "dbi_decode_token_async": (_st, [_vp, _vp, _u32]),
     "dbi_decode_token_full_async": (_st, [_vp, _vp, _u32, _vp]),
+    "dbi_offload_setup_host": (_st, [_vp, ctypes.POINTER(OffloadConfig),
+                                     ctypes.POINTER(LayerWeights), _u32]),
+    "dbi_decode_token": (_st, [_vp, _vp, _u32]),
+    "dbi_decode_token_full": (_st, [_vp, _vp, _u32, _vp]),
     "dbi_kv_prefix_save": (_st, [_vp, ctypes.c_char_p, _vp, _u32]),
     "dbi_kv_prefix_load": (_st, [_vp, ctypes.c_char_p, _vp, _u32, ctypes.POINTER(_u32)]),
     "dbi_kv_export_bytes": (ctypes.c_size_t, [_vp, _u32]),

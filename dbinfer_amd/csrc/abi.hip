@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -17,6 +18,8 @@ struct OffloadState {
   float* buf = nullptr;  // one allocation: the rows below
   float *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
   float *gate = nullptr, *up = nullptr;
+  float *xrow = nullptr, *logits = nullptr;  // the host-row calls' device rows
+  void* owned = nullptr;  // device copies of host weights (dbi_offload_setup_host)
 };
 
 struct dbi_kv {
@@ -784,6 +787,7 @@ void dbi_kv_destroy(dbi_kv* kv) {
   free_store(kv->store);
   free_ws(kv->ws);
   if (kv->off.buf) (void)hipFree(kv->off.buf);
+  if (kv->off.owned) (void)hipFree(kv->off.owned);
   if (kv->own_stream) (void)hipStreamDestroy(kv->own_stream);
   delete kv;
 }
@@ -1533,8 +1537,10 @@ dbi_status dbi_oproj_residual_async(dbi_kv* kv, uint32_t wtype, const void* w_de
 // ---------------------------------------------------------------------------
 // full-layer offload (backend.hpp:133-157; model.cpp:730-787, 896-917)
 
-dbi_status dbi_offload_setup(dbi_kv* kv, const dbi_offload_config* cfg,
-                             const dbi_layer_weights* layers, uint32_t n_layers) {
+// owned: device copies the handle takes over on success (the host-row
+// setup's), or null; either way the previous setup's copies are released.
+static dbi_status offload_setup_impl(dbi_kv* kv, const dbi_offload_config* cfg,
+                              const dbi_layer_weights* layers, uint32_t n_layers, void* owned) {
   if (kv == nullptr || cfg == nullptr || layers == nullptr)
     return fail(DBI_ERR_INVALID, "null offload argument");
   const uint32_t nkv = kv->cfg.n_kv_heads, hd = kv->cfg.head_dim;
@@ -1584,7 +1590,9 @@ dbi_status dbi_offload_setup(dbi_kv* kv, const dbi_offload_config* cfg,
   o.buf = nullptr;
   // rows rounded up to 64 floats: every row stays 256-byte aligned
   auto r64 = [](size_t n) { return (n + 63) / 64 * 64; };
-  const size_t total = r64(cfg->dim) + 2 * r64(qn) + 2 * r64(kvn) + 2 * r64(cfg->ff);
+  const size_t nlog = cfg->lm_head.data != nullptr ? cfg->vocab : 0;
+  const size_t total =
+      2 * r64(cfg->dim) + 2 * r64(qn) + 2 * r64(kvn) + 2 * r64(cfg->ff) + r64(nlog);
   if (hipMalloc(reinterpret_cast<void**>(&o.buf), total * sizeof(float)) != hipSuccess) {
     o.layers.clear();
     return fail(DBI_ERR_NOMEM, "offload scratch allocation failed");
@@ -1596,10 +1604,19 @@ dbi_status dbi_offload_setup(dbi_kv* kv, const dbi_offload_config* cfg,
   o.k = p; p += r64(kvn);
   o.v = p; p += r64(kvn);
   o.gate = p; p += r64(cfg->ff);
-  o.up = p;
+  o.up = p; p += r64(cfg->ff);
+  o.xrow = p; p += r64(cfg->dim);
+  o.logits = nlog ? p : nullptr;
   o.cfg = *cfg;
   o.layers.assign(layers, layers + n_layers);
+  if (o.owned) (void)hipFree(o.owned);
+  o.owned = owned;
   return DBI_OK;
+}
+
+dbi_status dbi_offload_setup(dbi_kv* kv, const dbi_offload_config* cfg,
+                             const dbi_layer_weights* layers, uint32_t n_layers) {
+  return offload_setup_impl(kv, cfg, layers, n_layers, nullptr);
 }
 
 dbi_status dbi_decode_token_async(dbi_kv* kv, float* x_dev, uint32_t pos) {
@@ -1619,6 +1636,143 @@ dbi_status dbi_decode_token_full_async(dbi_kv* kv, float* x_dev, uint32_t pos,
   HIP_TRY(run_matvec(kv, o.cfg.lm_head, x_dev, logits_dev, o.cfg.vocab, o.cfg.dim, false,
                      o.cfg.output_norm, &normed),
           "lm_head launch");
+  return DBI_OK;
+}
+
+// ---- host-row forms (the reference's own Backend contract: setup_offload
+// copies the weights to the device once, decode_token / decode_token_full
+// take host rows)
+
+dbi_status dbi_offload_setup_host(dbi_kv* kv, const dbi_offload_config* cfg,
+                                  const dbi_layer_weights* layers, uint32_t n_layers) {
+  if (kv == nullptr || cfg == nullptr || layers == nullptr)
+    return fail(DBI_ERR_INVALID, "null offload argument");
+  if (n_layers == 0 || n_layers > kv->cfg.n_layers)
+    return fail(DBI_ERR_INVALID, "offload needs 1 to n_layers blocks");
+  if (cfg->dim == 0 || cfg->ff == 0 || cfg->n_heads == 0 || cfg->dim > (uint32_t(1) << 20) ||
+      cfg->ff > (uint32_t(1) << 20) || cfg->n_heads > 4096 ||
+      (cfg->lm_head.data != nullptr && (cfg->vocab == 0 || cfg->vocab > (uint32_t(1) << 30))))
+    return fail(DBI_ERR_INVALID, "offload needs dim, ff in [1, 2^20], n_heads in [1, 4096] "
+                                 "and, with lm_head, vocab in [1, 2^30]");
+  const size_t dim = cfg->dim, ff = cfg->ff;
+  const size_t qn = size_t(cfg->n_heads) * kv->cfg.head_dim;
+  const size_t kvn = size_t(kv->cfg.n_kv_heads) * kv->cfg.head_dim;
+  // bytes of a [out][in] matrix of a served type (0: not served or a row
+  // that is not a whole number of blocks; the device setup then reports it)
+  auto wbytes = [](uint32_t type, size_t out, size_t in) -> size_t {
+    switch (type) {
+      case DBI_W_F32: return out * in * 4;
+      case DBI_W_F16: return out * in * 2;
+      case DBI_W_Q8_0: return in % 32 == 0 ? out * (in / 32) * 34 : 0;
+      case DBI_W_Q4_0: return in % 32 == 0 ? out * (in / 32) * 18 : 0;
+      default: return 0;
+    }
+  };
+  struct Piece {
+    const void* src;
+    size_t bytes;
+    std::function<void(const void*)> bind;  // stores the device address
+  };
+  std::vector<dbi_layer_weights> dev(layers, layers + n_layers);
+  dbi_offload_config dcfg = *cfg;
+  std::vector<Piece> pieces;
+  auto add = [&](const void* src, size_t bytes, std::function<void(const void*)> bind,
+                 const char* what, uint32_t l) -> dbi_status {
+    if (src == nullptr) return DBI_OK;  // (the device setup checks what must be there)
+    if (bytes == 0)
+      return fail(DBI_ERR_UNSUPPORTED,
+                  "offload block " + std::to_string(l) + " " + what +
+                      ": the matvecs serve fp32, f16, Q8_0 and Q4_0 weights only (Q8_0 and "
+                      "Q4_0 rows a multiple of 32)");
+    pieces.push_back({src, bytes, std::move(bind)});
+    return DBI_OK;
+  };
+  auto fset = [](const float** f) {
+    return [f](const void* d) { *f = static_cast<const float*>(d); };
+  };
+  for (uint32_t l = 0; l < n_layers; ++l) {
+    dbi_layer_weights& L = dev[l];
+    const struct {
+      dbi_weight* w;
+      size_t out, in;
+      const char* name;
+    } ws[] = {{&L.wq, qn, dim, "wq"},      {&L.wk, kvn, dim, "wk"},   {&L.wv, kvn, dim, "wv"},
+              {&L.wo, dim, qn, "wo"},      {&L.wgate, ff, dim, "wgate"},
+              {&L.wup, ff, dim, "wup"},    {&L.wdown, dim, ff, "wdown"}};
+    for (const auto& w : ws) {
+      dbi_weight* wp = w.w;
+      if (dbi_status st = add(wp->data, wbytes(wp->type, w.out, w.in),
+                              [wp](const void* d) { wp->data = d; }, w.name, l))
+        return st;
+    }
+    (void)add(L.attn_norm, dim * 4, fset(&L.attn_norm), "attn_norm", l);
+    (void)add(L.ffn_norm, dim * 4, fset(&L.ffn_norm), "ffn_norm", l);
+    (void)add(L.bq, qn * 4, fset(&L.bq), "bq", l);
+    (void)add(L.bk, kvn * 4, fset(&L.bk), "bk", l);
+    (void)add(L.bv, kvn * 4, fset(&L.bv), "bv", l);
+  }
+  if (cfg->lm_head.data != nullptr) {
+    if (dbi_status st = add(cfg->lm_head.data, wbytes(cfg->lm_head.type, cfg->vocab, dim),
+                            [&dcfg](const void* d) { dcfg.lm_head.data = d; }, "lm_head", 0))
+      return st;
+    (void)add(cfg->output_norm, dim * 4, fset(&dcfg.output_norm), "output_norm", 0);
+  }
+  if (dbi_status st = refuse_capture(kv, "the offload weights")) return st;
+  // one device allocation, every piece 256-byte aligned
+  size_t total = 0;
+  for (const Piece& pc : pieces) total += (pc.bytes + 255) / 256 * 256;
+  uint8_t* base = nullptr;
+  if (total > 0 && hipMalloc(reinterpret_cast<void**>(&base), total) != hipSuccess)
+    return fail(DBI_ERR_NOMEM, "offload weight allocation failed (" + std::to_string(total) +
+                                   " bytes)");
+  size_t at = 0;
+  for (const Piece& pc : pieces) {
+    const hipError_t e = hipMemcpy(base + at, pc.src, pc.bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(base);
+      return hip_fail(e, "offload weight upload");
+    }
+    pc.bind(base + at);
+    at += (pc.bytes + 255) / 256 * 256;
+  }
+  const dbi_status st = offload_setup_impl(kv, &dcfg, dev.data(), n_layers, base);
+  if (st != DBI_OK) (void)hipFree(base);
+  return st;
+}
+
+dbi_status dbi_decode_token(dbi_kv* kv, float* x, uint32_t pos) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  const OffloadState& o = kv->off;
+  if (o.layers.empty()) return fail(DBI_ERR_INVALID, "decode_token needs dbi_offload_setup first");
+  if (x == nullptr) return fail(DBI_ERR_INVALID, "null residual row");
+  const size_t bytes = size_t(o.cfg.dim) * sizeof(float);
+  HIP_TRY(hipMemcpyAsync(o.xrow, x, bytes, hipMemcpyHostToDevice, kv->stream), "x upload");
+  if (dbi_status st = decode_token_impl(kv, o.xrow, pos)) {
+    (void)hipStreamSynchronize(kv->stream);  // the upload reads the caller's row
+    return st;
+  }
+  HIP_TRY(hipMemcpyAsync(x, o.xrow, bytes, hipMemcpyDeviceToHost, kv->stream), "x readback");
+  HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+  return DBI_OK;
+}
+
+dbi_status dbi_decode_token_full(dbi_kv* kv, const float* x, uint32_t pos, float* logits) {
+  if (kv == nullptr) return fail(DBI_ERR_INVALID, "null handle");
+  const OffloadState& o = kv->off;
+  if (o.cfg.lm_head.data == nullptr || o.logits == nullptr)
+    return fail(DBI_ERR_INVALID, "decode_token_full needs an offload tail (lm_head)");
+  if (x == nullptr || logits == nullptr) return fail(DBI_ERR_INVALID, "null row");
+  HIP_TRY(hipMemcpyAsync(o.xrow, x, size_t(o.cfg.dim) * sizeof(float), hipMemcpyHostToDevice,
+                         kv->stream),
+          "x upload");
+  if (dbi_status st = dbi_decode_token_full_async(kv, o.xrow, pos, o.logits)) {
+    (void)hipStreamSynchronize(kv->stream);
+    return st;
+  }
+  HIP_TRY(hipMemcpyAsync(logits, o.logits, size_t(o.cfg.vocab) * sizeof(float),
+                         hipMemcpyDeviceToHost, kv->stream),
+          "logits readback");
+  HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
   return DBI_OK;
 }
 

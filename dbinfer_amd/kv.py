@@ -278,10 +278,12 @@ class HipKV:
     # ---- full-layer offload (backend.hpp:133-157)
     def offload_setup(self, dim: int, ff: int, n_heads: int, rms_eps: float, layers: list,
                       output_norm: int | None = None, lm_head: tuple | None = None,
-                      vocab: int = 0) -> None:
-        """layers: per block a dict of device pointers attn_norm, ffn_norm,
-        bq/bk/bv (or None) and (data_ptr, wtype) tuples wq wk wv wo wgate wup
-        wdown; lm_head: (data_ptr, wtype) or None."""
+                      vocab: int = 0, host: bool = False) -> None:
+        """layers: per block a dict of pointers attn_norm, ffn_norm, bq/bk/bv
+        (or None) and (pointer, wtype) tuples wq wk wv wo wgate wup wdown;
+        lm_head: (pointer, wtype) or None. Device pointers, or with host=True
+        host pointers that the library copies to the device
+        (dbi_offload_setup_host)."""
         arr = (_lib.LayerWeights * len(layers))()
         for i, L in enumerate(layers):
             a = arr[i]
@@ -292,13 +294,26 @@ class HipKV:
             a.bq, a.bk, a.bv = L.get("bq"), L.get("bk"), L.get("bv")
         cfg = _lib.OffloadConfig(dim, ff, n_heads, rms_eps, output_norm,
                                  _lib.Weight(*(lm_head if lm_head else (None, 0))), vocab)
-        _check(self._lib, self._lib.dbi_offload_setup(self._h, ctypes.byref(cfg), arr, len(layers)))
+        fn = self._lib.dbi_offload_setup_host if host else self._lib.dbi_offload_setup
+        _check(self._lib, fn(self._h, ctypes.byref(cfg), arr, len(layers)))
 
     def decode_token_async(self, x_dev: int, pos: int) -> None:
         _check(self._lib, self._lib.dbi_decode_token_async(self._h, x_dev, pos))
 
     def decode_token_full_async(self, x_dev: int, pos: int, logits_dev: int) -> None:
         _check(self._lib, self._lib.dbi_decode_token_full_async(self._h, x_dev, pos, logits_dev))
+
+    def decode_token(self, x, pos: int) -> np.ndarray:
+        """Host residual row in, the row after every bound block out."""
+        xa = _f32(x).copy()
+        _check(self._lib, self._lib.dbi_decode_token(self._h, _ptr(xa), pos))
+        return xa
+
+    def decode_token_full(self, x, pos: int, vocab: int) -> np.ndarray:
+        xa = _f32(x)
+        logits = np.empty(vocab, np.float32)
+        _check(self._lib, self._lib.dbi_decode_token_full(self._h, _ptr(xa), pos, _ptr(logits)))
+        return logits
 
     # ---- prefix cache
     def save_prefix(self, path: str, tokens) -> None:

@@ -335,6 +335,26 @@ dbi_status dbi_decode_token_async(dbi_kv* kv, float* x_dev, uint32_t pos);
 dbi_status dbi_decode_token_full_async(dbi_kv* kv, float* x_dev, uint32_t pos,
                                        float* logits_dev);
 
+/* The same three calls on host memory, the reference Backend's own contract
+ * (backend.hpp:133-157: setup_offload "copies each offloaded block's weights
+ * to the device once"; decode_token and decode_token_full take host rows).
+ *
+ * dbi_offload_setup_host: dbi_offload_setup with every pointer of cfg and
+ * layers in host memory; the library copies the norms, weights, biases,
+ * output_norm and lm_head into one device allocation of its own (released
+ * by the next setup or by destroy) and binds the copies. Synchronous; not
+ * under graph capture. */
+dbi_status dbi_offload_setup_host(dbi_kv* kv, const dbi_offload_config* cfg,
+                                  const dbi_layer_weights* layers, uint32_t n_layers);
+
+/* Backend::decode_token (backend.hpp:145-149) on a host residual row x [dim],
+ * updated in place: upload, every bound block, read back. Synchronous. */
+dbi_status dbi_decode_token(dbi_kv* kv, float* x, uint32_t pos);
+
+/* Backend::decode_token_full (backend.hpp:151-157) on a host input row x
+ * [dim] (not modified) into host logits [vocab]. Synchronous. */
+dbi_status dbi_decode_token_full(dbi_kv* kv, const float* x, uint32_t pos, float* logits);
+
 /* Model::save_kv_prefix (model.hpp:292-293, model.cpp:1072-1107): writes the
  * DBKVCACH v1 file of positions [0, len) with the token ids from a dense
  * fp32 cache. A dense int8 cache writes version 2, which has no counterpart

@@ -5,6 +5,8 @@
 //   kv_prefix_cache_test.cpp:79-130  save -> load -> identical next attention
 //   chunked_prefill_test.cpp:19-70   chunk == per-token (here within tolerance)
 //   speculative_test.cpp:104-150     merge vectors, rollback state
+// the Backend offload seam (backend.hpp:133-157) through backend.hpp, token
+// by token against the oracle's decode_layer and logits,
 // plus decode/chunk parity against the CPU oracle (oracle/kv_oracle.h), which
 // is the checker only. `host_test --cpu-only` runs the parts that need no GPU.
 #include <algorithm>
@@ -18,6 +20,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include "backend.hpp"
 #include "kv_cache.hpp"
 #include "kv_oracle.h"
 #include "layer.hpp"
@@ -511,6 +514,146 @@ void test_output_projection() {
 
 }  // namespace
 
+// The offload seam (Backend::setup_offload / decode_token /
+// decode_token_full, backend.hpp:133-157) through the C++ mirror, token by
+// token against the oracle's Model::decode_layer (okv_decode_layer) and
+// forward's tail (ok_logits). Host weights, copied once by setup_offload.
+// Q8_0 blocks: random codes and f16 scales written as bit patterns
+// 2^(e-15) (1 + m/1024), e in {3, 4} (scales ~2.4e-4 .. 9.8e-4); f16
+// weights: random signs and mantissas at e in {9, 10} (|w| in [0.016, 0.06]).
+// Tolerance: fp32 sums in trees (1e-5 + 1e-4 |b|); for Q8_0 an activation
+// code can flip at a rounding boundary (1e-2 (1 + |b|), as test_gpu_layer.py
+// derives).
+void test_offload(bool q8) {
+  namespace be = dbinfer_amd::backend;
+  constexpr std::size_t D = 256, FF = 512, NH = 4, NKV = 2, HD = 64, NL = 2, V = 300, CAP = 8;
+  constexpr float EPS = 1e-5f, THETA = 1e4f;
+  Lcg rng{q8 ? 0x51u : 0x52u};
+  auto u32 = [&]() {
+    return static_cast<std::uint32_t>((rng.next() + 1.0f) * 1048576.0f);
+  };
+  auto mat = [&](std::size_t out, std::size_t in) {
+    std::vector<std::uint8_t> m;
+    if (q8) {
+      m.resize(out * (in / 32) * 34);
+      for (std::size_t b = 0; b < out * (in / 32); ++b) {
+        const std::uint16_t h = static_cast<std::uint16_t>(((3 + (u32() & 1)) << 10) | (u32() & 1023));
+        std::memcpy(&m[b * 34], &h, 2);
+        for (int i = 0; i < 32; ++i)
+          m[b * 34 + 2 + i] = static_cast<std::uint8_t>(static_cast<std::int8_t>(
+              static_cast<int>(u32() % 255) - 127));
+      }
+    } else {
+      m.resize(out * in * 2);
+      for (std::size_t i = 0; i < out * in; ++i) {
+        const std::uint16_t h = static_cast<std::uint16_t>(
+            ((u32() & 1) << 15) | ((9 + (u32() & 1)) << 10) | (u32() & 1023));
+        std::memcpy(&m[i * 2], &h, 2);
+      }
+    }
+    return m;
+  };
+  auto vec = [&](std::size_t n, float base, float amp) {
+    std::vector<float> v(n);
+    for (auto& x : v) x = base + amp * rng.next();
+    return v;
+  };
+  const std::size_t qn = NH * HD, kvn = NKV * HD;
+  struct Block {
+    std::vector<float> an, fn, bq, bk, bv;
+    std::vector<std::uint8_t> w[7];
+  };
+  std::vector<Block> blk(NL);
+  const std::size_t shapes[7][2] = {{qn, D}, {kvn, D}, {kvn, D}, {D, qn}, {FF, D}, {FF, D}, {D, FF}};
+  const be::WeightType wt = q8 ? be::WeightType::Q8_0 : be::WeightType::F16;
+  const int owt = q8 ? 8 : 1;  // GGUF type ids (oracle)
+  std::vector<be::LayerQ> lq(NL);
+  std::vector<ok_layer> ol(NL);
+  for (std::size_t l = 0; l < NL; ++l) {
+    Block& b = blk[l];
+    b.an = vec(D, 1.0f, 0.1f);
+    b.fn = vec(D, 1.0f, 0.1f);
+    b.bq = vec(qn, 0.0f, 0.1f);
+    b.bk = vec(kvn, 0.0f, 0.1f);
+    b.bv = vec(kvn, 0.0f, 0.1f);
+    for (int i = 0; i < 7; ++i) b.w[i] = mat(shapes[i][0], shapes[i][1]);
+    auto qw = [&](int i) { return be::QWeight{reinterpret_cast<const std::byte*>(b.w[i].data()), wt}; };
+    lq[l] = be::LayerQ{b.an.data(), b.fn.data(), qw(0), qw(1), qw(2), qw(3), qw(4), qw(5), qw(6),
+                       b.bq.data(), b.bk.data(), b.bv.data(), D, FF, NH, NKV, HD, EPS, THETA};
+    ol[l].attn_norm = b.an.data();
+    ol[l].ffn_norm = b.fn.data();
+    for (int i = 0; i < 7; ++i) {
+      ol[l].w[i] = b.w[i].data();
+      ol[l].wtype[i] = owt;
+    }
+    ol[l].bq = b.bq.data();
+    ol[l].bk = b.bk.data();
+    ol[l].bv = b.bv.data();
+  }
+  const std::vector<float> onorm = vec(D, 1.0f, 0.1f);
+  const std::vector<std::uint8_t> lm = mat(V, D);
+  const char* name = q8 ? "Q8_0" : "f16";
+  auto within = [&](const float* got, const std::vector<float>& want, double* worst) {
+    bool ok = true;
+    for (std::size_t i = 0; i < want.size(); ++i) {
+      const double b = std::fabs(static_cast<double>(want[i]));
+      const double bound = q8 ? 1e-2 * (1.0 + b) : 1e-5 + 1e-4 * b;
+      const double err = std::fabs(static_cast<double>(got[i]) - want[i]);
+      *worst = std::max(*worst, err / bound);
+      ok = ok && err <= bound;
+    }
+    return ok;
+  };
+  // decode_token on one cache, decode_token_full on another (each token
+  // appends at pos)
+  KVCache kv(NL, CAP, NKV, HD, {}, THETA), kv2(NL, CAP, NKV, HD, {}, THETA);
+  be::HipBackend b1(kv), b2(kv2);
+  auto s1 = b1.setup_offload(lq, nullptr, nullptr, 0, 0, nullptr, be::QWeight{}, 0);
+  auto s2 = b2.setup_offload(lq, nullptr, nullptr, CAP, NKV * HD, onorm.data(),
+                             be::QWeight{reinterpret_cast<const std::byte*>(lm.data()), wt}, V);
+  check(static_cast<bool>(s1) && static_cast<bool>(s2),
+        std::string("setup_offload copies the weights once: ") + name +
+            (s1 ? "" : " (" + s1.error().message + ")") + (s2 ? "" : " (" + s2.error().message + ")"));
+  if (!s1 || !s2) return;
+  okv* o = okv_create(NL, CAP, NKV, HD, 0, 0, OKV_F32);
+  okv* o2 = okv_create(NL, CAP, NKV, HD, 0, 0, OKV_F32);
+  bool ok = true, ok_full = true;
+  double worst = 0, worst_full = 0;
+  for (std::int32_t pos = 0; pos < 5; ++pos) {
+    const std::vector<float> x = vec(D, 0.0f, 1.0f);
+    std::vector<float> got = x, want = x, want2 = x;
+    auto r = b1.decode_token(got.data(), pos);
+    ok = ok && static_cast<bool>(r);
+    for (std::size_t l = 0; l < NL; ++l) {
+      okv_decode_layer(o, l, want.data(), pos, &ol[l], D, FF, NH, EPS, THETA, 1);
+      okv_decode_layer(o2, l, want2.data(), pos, &ol[l], D, FF, NH, EPS, THETA, 1);
+    }
+    okv_truncate(o, pos + 1);
+    okv_truncate(o2, pos + 1);
+    ok = ok && within(got.data(), want, &worst);
+    auto lg = b2.decode_token_full(x.data(), pos);
+    ok_full = ok_full && static_cast<bool>(lg);
+    if (lg) {
+      std::vector<float> wl(V);
+      ok_logits(want2.data(), onorm.data(), lm.data(), owt, EPS, wl.data(), D, V);
+      ok_full = ok_full && within(*lg, wl, &worst_full);
+    }
+  }
+  std::printf("  offload %s worst err/bound %.3f (residual), %.3f (logits)\n", name, worst,
+              worst_full);
+  check(ok, std::string("Backend::decode_token == decode_layer over every block: ") + name);
+  check(ok_full, std::string("Backend::decode_token_full == blocks + rmsnorm + lm_head: ") + name);
+  // errors come back as the reference's Error, not as aborts
+  float xx[D] = {};
+  check(!b1.decode_token_full(xx, 5), "decode_token_full without an lm_head is an error");
+  std::vector<be::LayerQ> bad = lq;
+  bad[1].dim = D + 64;
+  check(!b1.setup_offload(bad, nullptr, nullptr, 0, 0, nullptr, be::QWeight{}, 0),
+        "setup_offload rejects blocks of different shapes");
+  okv_destroy(o);
+  okv_destroy(o2);
+}
+
 int main(int argc, char** argv) {
   const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu-only") == 0;
   test_speculative_merge();
@@ -534,6 +677,8 @@ int main(int argc, char** argv) {
     test_speculative_rollback();
     test_speculative_verify();
     test_output_projection();
+    test_offload(true);
+    test_offload(false);
   }
   std::printf("---\n%d checks failed\n", g_failures);
   return g_failures == 0 ? 0 : 1;

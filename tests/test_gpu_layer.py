@@ -208,3 +208,62 @@ def test_offload_errors(torch):
     assert g.n_seen == 0
     del keep
     g.close()
+
+
+def host_layers(lws):
+    """The same blocks as host pointers (numpy arrays kept alive by lws)."""
+    out = []
+    for lw in lws:
+        d = {"attn_norm": lw["attn_norm"].ctypes.data, "ffn_norm": lw["ffn_norm"].ctypes.data}
+        for i, name in enumerate(("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")):
+            d[name] = (lw["w"][i].ctypes.data, lw["wtype"][i])
+        for name in ("bq", "bk", "bv"):
+            d[name] = None if lw[name] is None else lw[name].ctypes.data
+        out.append(d)
+    return out
+
+
+@pytest.mark.parametrize("wt", [W_Q8_0, W_F16])
+def test_host_rows_equal_device_rows(torch, wt):
+    """dbi_offload_setup_host / dbi_decode_token / dbi_decode_token_full (the
+    reference Backend's host-row contract) run the same kernels on copies of
+    the host weights: bit-identical to the device-pointer calls."""
+    rng = np.random.default_rng(90 + wt)
+    lws = [layer_weights(rng, DIM, FF, NH, NKV, HD, wt, True) for _ in range(L)]
+    onorm = (1.0 + 0.1 * rng.standard_normal(DIM)).astype(np.float32)
+    lm = np.ascontiguousarray(layer_weights(rng, DIM, VOCAB, NH, NKV, HD, wt, False)["w"][4])
+    gd = HipKV(L, 8, NKV, HD, rope_theta=1e4)
+    gh = HipKV(L, 8, NKV, HD, rope_theta=1e4)
+    keep = bind(torch, gd, lws, (onorm, lm, wt))
+    gd.set_stream(torch.cuda.current_stream().cuda_stream)
+    gh.offload_setup(DIM, FF, NH, EPS, host_layers(lws), onorm.ctypes.data, (lm.ctypes.data, wt),
+                     VOCAB, host=True)
+    logits = torch.zeros(VOCAB, device="cuda")
+    for pos in range(4):
+        x = normal(900 + pos, DIM)
+        xt = dev(torch, x)
+        gd.decode_token_full_async(xt.data_ptr(), pos, logits.data_ptr())
+        torch.cuda.synchronize()
+        want = logits.cpu().numpy()
+        got = gh.decode_token_full(x, pos, VOCAB)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"pos {pos}"
+    # decode_token on the host row: the residual after every block
+    gd2 = HipKV(L, 8, NKV, HD, rope_theta=1e4)
+    keep2 = bind(torch, gd2, lws)
+    gd2.set_stream(torch.cuda.current_stream().cuda_stream)
+    gh.truncate(0)
+    for pos in range(3):
+        x = normal(950 + pos, DIM)
+        xt = dev(torch, x)
+        gd2.decode_token_async(xt.data_ptr(), pos)
+        torch.cuda.synchronize()
+        got = gh.decode_token(x, pos)
+        assert np.array_equal(got.view(np.uint32), xt.cpu().numpy().view(np.uint32)), f"pos {pos}"
+    # host setup errors come back before anything is copied
+    with pytest.raises(DbiError) as e:
+        bad = host_layers(lws)
+        bad[0]["wq"] = (bad[0]["wq"][0], 6)  # Q5_0 is not served
+        gh.offload_setup(DIM, FF, NH, EPS, bad, host=True)
+    assert "Q4_0 weights only" in e.value.message
+    del keep, keep2
+    gd.close(), gd2.close(), gh.close()
