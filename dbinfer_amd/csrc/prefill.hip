@@ -31,6 +31,7 @@
 //    so the copy is a straight contiguous one and the operand offsets are
 //    the layout's offsets relative to the stage.
 #include <cmath>
+#include <type_traits>
 
 #include "kv_internal.hpp"
 
@@ -193,72 +194,99 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
   for (int tt = 0; tt < NT; ++tt) acc[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = kMinitP, l_run = 0.0f;
 
-  auto compute_stage = [&](int st, const float* sk, const float* sv) {
+  // S^T of tile t (keys st*SK + 16t ..) in four independent chains
+  auto qk = [&](int t, const float* sk, f4 (&sc)[4]) {
 #pragma unroll
-    for (int t = 0; t < SK / 16; ++t) {
-      const int kb = st * SK + 16 * t;  // first key of the tile (wave-uniform)
-      if (!wave_live || kb > wave_last) continue;  // tile past every row of the wave
-      // S^T tile in four independent chains
-      f4 sc[4];
+    for (int c = 0; c < 4; ++c) sc[c] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int c = 0; c < 4; ++c) sc[c] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int h = 0; h < NH; ++h) {
+      const int ko = static_cast<int>(k_off_tiled(HD, false, 16 * t + vec, 16 * gq + 64 * h));
 #pragma unroll
-      for (int h = 0; h < NH; ++h) {
-        const int ko = static_cast<int>(k_off_tiled(HD, false, 16 * t + vec, 16 * gq + 64 * h));
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-          const float4 x = lds4(sk + swz(ko + 4 * s4));
-          const int i = 16 * h + 4 * s4;
-          sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, qv[i + 0], sc[0], 0, 0, 0);
-          sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, qv[i + 1], sc[1], 0, 0, 0);
-          sc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, qv[i + 2], sc[2], 0, 0, 0);
-          sc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, qv[i + 3], sc[3], 0, 0, 0);
-        }
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const float4 x = lds4(sk + swz(ko + 4 * s4));
+        const int i = 16 * h + 4 * s4;
+        sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, qv[i + 0], sc[0], 0, 0, 0);
+        sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, qv[i + 1], sc[1], 0, 0, 0);
+        sc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, qv[i + 2], sc[2], 0, 0, 0);
+        sc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, qv[i + 3], sc[3], 0, 0, 0);
       }
-      const f4 s = (sc[0] + sc[1]) + (sc[2] + sc[3]);
+    }
+  };
 
-      // online softmax per vector
-      float sv4[4];
-      float mx = kMinitP;
+  // online softmax of tile t's scores, then O^T += V^T P^T. MASK: the tile
+  // reaches past some row's last key or past the workgroup's last key
+  // (causal diagonal, chunk tail); other tiles skip the masks.
+  auto soft_pv = [&](int st, int t, const float* sv, const f4 (&sc)[4], auto mask_c) {
+    constexpr bool MASK = decltype(mask_c)::value;
+    const int kb = st * SK + 16 * t;  // first key of the tile (wave-uniform)
+    const f4 s = (sc[0] + sc[1]) + (sc[2] + sc[3]);
+    float sv4[4];
+    float mx = kMinitP;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int key = kb + 4 * gq + v;
-        sv4[v] = key <= limit ? s[v] : -INFINITY;
-        mx = fmaxf(mx, sv4[v]);
-      }
-      mx = xmax32(xmax16(mx));
-      const float mn = fmaxf(m_run, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
-      float pv[4], ls = 0.0f;
+    for (int v = 0; v < 4; ++v) {
+      const int key = kb + 4 * gq + v;
+      sv4[v] = !MASK || key <= limit ? s[v] : -INFINITY;
+      mx = fmaxf(mx, sv4[v]);
+    }
+    mx = xmax32(xmax16(mx));
+    const float mn = fmaxf(m_run, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+    float pv[4], ls = 0.0f;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        pv[v] = __builtin_amdgcn_exp2f(sv4[v] - mn);
-        ls += pv[v];
-      }
-      ls = xsum32(xsum16(ls));
-      l_run = l_run * alpha + ls;
-      m_run = mn;
+    for (int v = 0; v < 4; ++v) {
+      pv[v] = __builtin_amdgcn_exp2f(sv4[v] - mn);
+      ls += pv[v];
+    }
+    ls = xsum32(xsum16(ls));
+    l_run = l_run * alpha + ls;
+    m_run = mn;
+    // once the running maxima settle, alpha is exactly 1 in every lane and
+    // the rescale (a multiply by 1) is skipped
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt) acc[tt] *= alpha;
+    }
 
-      // O^T += V^T P^T: output tile tt row i is dim VD i + tt. Keys past the
-      // workgroup's last row are never weighted and read as 0.
+    // O^T += V^T P^T: output tile tt row i is dim VD i + tt. Keys past the
+    // workgroup's last row are never weighted and read as 0.
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = kb + 4 * gq + j;
-        const int vo = static_cast<int>(v_off_tiled(HD, false, 16 * t + 4 * gq + j, VD * vec));
-        float vd[VD];
+    for (int j = 0; j < 4; ++j) {
+      const int key = kb + 4 * gq + j;
+      const int vo = static_cast<int>(v_off_tiled(HD, false, 16 * t + 4 * gq + j, VD * vec));
+      float vd[VD];
 #pragma unroll
-        for (int u = 0; u < VD / 4; ++u) {
-          const float4 x = lds4(sv + swz(vo + 256 * u));
-          vd[4 * u + 0] = key <= last_key ? x.x : 0.0f;
-          vd[4 * u + 1] = key <= last_key ? x.y : 0.0f;
-          vd[4 * u + 2] = key <= last_key ? x.z : 0.0f;
-          vd[4 * u + 3] = key <= last_key ? x.w : 0.0f;
-        }
+      for (int u = 0; u < VD / 4; ++u) {
+        const float4 x = lds4(sv + swz(vo + 256 * u));
+        vd[4 * u + 0] = !MASK || key <= last_key ? x.x : 0.0f;
+        vd[4 * u + 1] = !MASK || key <= last_key ? x.y : 0.0f;
+        vd[4 * u + 2] = !MASK || key <= last_key ? x.z : 0.0f;
+        vd[4 * u + 3] = !MASK || key <= last_key ? x.w : 0.0f;
+      }
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt)
-          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[tt], pv[j], acc[tt], 0, 0, 0);
+      for (int tt = 0; tt < NT; ++tt)
+        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[tt], pv[j], acc[tt], 0, 0, 0);
+    }
+  };
+
+  // A stage's tiles, software-pipelined: tile t + 1's QK^T products are
+  // issued before tile t's softmax, so the matrix core works through them
+  // while the wave's VALU runs the softmax. Tiles past every row of the wave
+  // (the causal tail) are skipped.
+  constexpr int NTS = SK / 16;  // tiles per stage
+  // keys every row of the wave attends, and that the workgroup holds
+  const int wave_full = min(P.pos0 + row0, last_key);
+  auto compute_stage = [&](int st, const float* sk, const float* sv) {
+    const int nt = !wave_live ? 0 : min(NTS, max(0, (wave_last - st * SK) / 16 + 1));  // uniform
+    f4 sc[2][4];
+    if (nt > 0) qk(0, sk, sc[0]);
+#pragma unroll
+    for (int t = 0; t < NTS; ++t) {
+      if (t < nt) {
+        if (t + 1 < nt) qk(t + 1, sk, sc[(t + 1) & 1]);
+        if (st * SK + 16 * t + 15 <= wave_full)  // uniform
+          soft_pv(st, t, sv, sc[t & 1], std::false_type{});
+        else
+          soft_pv(st, t, sv, sc[t & 1], std::true_type{});
       }
     }
   };
