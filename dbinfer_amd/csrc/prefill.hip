@@ -55,11 +55,28 @@ struct PrefillParams {
   float qscale;     // scale * log2(e)
 };
 
-// one 16-byte LDS-direct copy per lane (dst is the wave's base; lane l lands
-// at dst + 4 l). Kept out of line of the kernel body: used on a __shared__
-// array there, the builtin stops the host pass from emitting the kernel.
-__device__ __forceinline__ void lds_copy16(const float* src, float* dst) {
-  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+// One 16-byte LDS-direct copy per lane: lane l reads src + 16 voff bytes
+// (src wave-uniform) and lands at LDS byte address dst + 16 l (dst
+// wave-uniform, through m0). Issued as asm, so the compiler does not track
+// the copy: it would otherwise wait for every copy in flight (vmcnt 0)
+// before each LDS read, the next stage's included, since it cannot tell the
+// copy's destination from the buffer being read. Stage arrival is waited for
+// explicitly (s_waitcnt vmcnt, then the barrier).
+// m0 is saved and restored around the copy (the register is reserved to
+// the compiler).
+__device__ __forceinline__ void lds_copy16(const float* src, uint32_t voff, uint32_t dst) {
+  uint32_t keep;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, %1\n\ts_mov_b32 m0, %0"
+      : "=&s"(keep)
+      : "s"(src), "v"(voff), "s"(dst)
+      : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const float* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const float*)p));
 }
 
 // Workgroup barrier that waits for this wave's LDS accesses only. The
@@ -82,34 +99,48 @@ __device__ __forceinline__ float4 lds4(const float* p) {
 // used.
 __device__ __forceinline__ float xmax16(float x) {
   float a = x, b = x;
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
   return fmaxf(a, b);
 }
 __device__ __forceinline__ float xmax32(float x) {
   float a = x, b = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
   return fmaxf(a, b);
 }
 __device__ __forceinline__ float xsum16(float x) {
   float a = x, b = x;
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
   return a + b;
 }
 __device__ __forceinline__ float xsum32(float x) {
   float a = x, b = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
   return a + b;
 }
 
 // Stage buffers hold the cache's granule layout with its 16-byte units
-// swizzled inside every aligned run of 64 units: unit u sits at
-// u ^ ((u >> 3) & 7). A K operand read has lanes of eight position rows
-// (units 8 apart, one bank group in the plain layout) in one LDS pass; the
-// swizzle spreads them over eight bank groups. The map is its own inverse.
-__device__ __forceinline__ int swz(int o) {  // float offset in a stage array
-  const int u = o >> 2;
-  return ((u ^ ((u >> 3) & 7)) << 2) | (o & 3);
+// permuted inside every aligned run of 16 units: unit u sits at swz_u(u) =
+// u ^ m(u), m's bits 0-2 the parities of u >> 3 under the masks 62, 53, 15
+// and its bit 3 the parity of u >> 4 under 54. The masks were picked by
+// exhaustive check of every K and V operand read of both head dims: each
+// read (64 lanes x 16 bytes) then hits distinct banks in every group of 8
+// lanes (32 banks) and of 16 lanes (64 banks). The map is linear over GF(2),
+// so an offset that is a lane part XOR a constant permutes as the XOR of the
+// two permuted parts (the constant one folds at compile time).
+__host__ __device__ constexpr int parity(int x) { return __builtin_popcount(x) & 1; }
+__host__ __device__ constexpr int swz_u(int u) {
+  return u ^ (parity(62 & (u >> 3)) | (parity(53 & (u >> 3)) << 1) |
+              (parity(15 & (u >> 3)) << 2) | (parity(54 & (u >> 4)) << 3));
 }
+// the unit that swz_u places at s
+__host__ __device__ constexpr int swz_u_inv(int s) {
+  const int b3 = ((s >> 3) & 1) ^ parity(54 & (s >> 4));
+  const int u3 = (s & ~15) | (b3 << 3) | (s & 7);  // bits 3.. of the unit
+  return u3 ^ (parity(62 & (u3 >> 3)) | (parity(53 & (u3 >> 3)) << 1) |
+               (parity(15 & (u3 >> 3)) << 2));
+}
+static_assert(swz_u_inv(swz_u(777)) == 777 && swz_u(swz_u_inv(1000)) == 1000, "bijection");
+static_assert((swz_u(300 ^ 517) ^ swz_u(300)) == swz_u(517), "linear");
 
 template <int HD>
 struct Stage {
@@ -121,7 +152,7 @@ struct Stage {
 // NBUF stage buffers: NBUF - 1 stage copies are in flight ahead of the one
 // being computed (2: two workgroups per CU share the CU's LDS).
 template <int HD, int G, int NBUF>
-__global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams P) {
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(const PrefillParams P) {
   using S = Stage<HD>;
   constexpr int SK = S::SK, FL = S::FL, NDMA = S::NDMA;
   constexpr int RPV = 16 / G;    // rows per wave
@@ -129,9 +160,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
   constexpr int NH = HD / 64;    // 16-dim runs per lane group
   constexpr int VD = HD / 16;    // V dims per lane per key = output tiles
   constexpr int NT = HD / 16;
-  // one array per stage buffer ([K, V][stage]): with the buffer known at
-  // compile time, the compiler's own waits tell the buffers' LDS-direct
-  // copies apart instead of draining them all before every LDS read
+  // one array per stage buffer ([K, V][stage]), picked at compile time
   __shared__ __align__(16) float s_b0[2 * FL];
   __shared__ __align__(16) float s_b1[2 * FL];
   __shared__ __align__(16) float s_b2[NBUF > 2 ? 2 * FL : 4];
@@ -160,17 +189,39 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
   const float* kbase = P.kf + head_el;
   const float* vbase = P.vf + head_el;
 
-  // stage copy: K then V, 16 bytes per lane per instruction; each lane
-  // fetches the unit that the swizzle puts at its LDS slot
-  const int src_lane = lane ^ ((lane >> 3) & 7);
+  // stage copy: K then V, 16 bytes per lane per instruction; copy m of this
+  // wave fills units [m * kPThreads + 64 * wave, + 64) of the buffer, and
+  // lane l's slot holds unit swz_u_inv(slot) of the stage, from the same
+  // 1 KiB (the permutation stays within 16-unit runs)
+  uint32_t src_off[NDMA];
+#pragma unroll
+  for (int m = 0; m < NDMA; ++m) {
+    const int u0 = m * kPThreads + 64 * wave;
+    src_off[m] = 16u * static_cast<uint32_t>(swz_u_inv(u0 + lane) - u0);
+  }
   auto copy_stage = [&](int st, float* dst) {
     const size_t off = static_cast<size_t>(st) * FL;
+    const uint32_t d = lds_addr(dst);
 #pragma unroll
     for (int m = 0; m < NDMA; ++m) {
       const int e = (m * kPThreads + wave * 64) * 4;  // this wave's KiB of the copy
-      lds_copy16(kbase + off + e + src_lane * 4, dst + e);
-      lds_copy16(vbase + off + e + src_lane * 4, dst + FL + e);
+      lds_copy16(kbase + off + e, src_off[m], d + 4 * e);
+      lds_copy16(vbase + off + e, src_off[m], d + 4 * (FL + e));
     }
+  };
+  // permuted operand units: a tile's K read (tile t, dims run h, step s4) is
+  // unit kb[h] ^ (t * 4 HD) ^ s4 and a V read (tile t, key j of the lane
+  // group, half u) is vb ^ (t * 4 HD) ^ unit(j, 0) ^ 64 u, the lane parts
+  // kb, vb those of tile 0 (no carries between the parts)
+  int skb[NH];
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
+    skb[h] = swz_u(static_cast<int>(k_off_tiled(HD, false, vec, 16 * gq + 64 * h)) >> 2);
+  const int svb = swz_u(static_cast<int>(v_off_tiled(HD, false, 4 * gq, VD * vec)) >> 2);
+  auto k_at = [&](int t, int h, int s4) { return 4 * (skb[h] ^ swz_u(t * 4 * HD ^ s4)); };
+  auto v_at = [&](int t, int j, int u) {
+    return 4 * (svb ^ swz_u(t * 4 * HD ^ (static_cast<int>(v_off_tiled(HD, false, j, 0)) >> 2) ^
+                            (64 * u)));
   };
 
   // Q^T operands: dims 16 gq + 64 h + s, pre-scaled into the log2 domain
@@ -200,10 +251,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
     for (int c = 0; c < 4; ++c) sc[c] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
-      const int ko = static_cast<int>(k_off_tiled(HD, false, 16 * t + vec, 16 * gq + 64 * h));
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
-        const float4 x = lds4(sk + swz(ko + 4 * s4));
+        const float4 x = lds4(sk + k_at(t, h, s4));
         const int i = 16 * h + 4 * s4;
         sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, qv[i + 0], sc[0], 0, 0, 0);
         sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, qv[i + 1], sc[1], 0, 0, 0);
@@ -252,11 +302,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int key = kb + 4 * gq + j;
-      const int vo = static_cast<int>(v_off_tiled(HD, false, 16 * t + 4 * gq + j, VD * vec));
       float vd[VD];
 #pragma unroll
       for (int u = 0; u < VD / 4; ++u) {
-        const float4 x = lds4(sv + swz(vo + 256 * u));
+        const float4 x = lds4(sv + v_at(t, j, u));
         vd[4 * u + 0] = !MASK || key <= last_key ? x.x : 0.0f;
         vd[4 * u + 1] = !MASK || key <= last_key ? x.y : 0.0f;
         vd[4 * u + 2] = !MASK || key <= last_key ? x.z : 0.0f;
@@ -275,8 +324,98 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
   constexpr int NTS = SK / 16;  // tiles per stage
   // keys every row of the wave attends, and that the workgroup holds
   const int wave_full = min(P.pos0 + row0, last_key);
+  // A stage whose tiles are all full and unmasked runs as one straight-line
+  // block: the LDS operands of tile t + 1 (V) and t + 2 (K) are read while
+  // tile t's products run, and tile t + 1's QK^T products are issued before
+  // tile t's softmax, so the scheduler can place the softmax's VALU and the
+  // reads between matrix instructions. Same operations in the same order as
+  // the general path (the rescale is unconditional: a multiply by exactly 1
+  // when the maxima hold), so the results are identical.
+  auto stage_full = [&](const float* sk, const float* sv) {
+    constexpr int NK = NQ / 4;  // 16-byte K reads per tile
+    auto ld_k = [&](int t, float4 (&x)[NK]) {
+#pragma unroll
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) x[4 * h + s4] = lds4(sk + k_at(t, h, s4));
+    };
+    auto ld_v = [&](int t, float4 (&x)[4][VD / 4]) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int u = 0; u < VD / 4; ++u) x[j][u] = lds4(sv + v_at(t, j, u));
+    };
+    auto mm_qk = [&](const float4 (&x)[NK], f4 (&sc)[4]) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sc[c] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i4 = 0; i4 < NK; ++i4) {
+        const int i = 4 * i4;
+        sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[i4].x, qv[i + 0], sc[0], 0, 0, 0);
+        sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[i4].y, qv[i + 1], sc[1], 0, 0, 0);
+        sc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[i4].z, qv[i + 2], sc[2], 0, 0, 0);
+        sc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[i4].w, qv[i + 3], sc[3], 0, 0, 0);
+      }
+    };
+    auto softmax = [&](const f4 (&sc)[4], float (&pv)[4]) {
+      const f4 s = (sc[0] + sc[1]) + (sc[2] + sc[3]);
+      float mx = kMinitP;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s[v]);
+      mx = xmax32(xmax16(mx));
+      const float mn = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+      float ls = 0.0f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        pv[v] = __builtin_amdgcn_exp2f(s[v] - mn);
+        ls += pv[v];
+      }
+      ls = xsum32(xsum16(ls));
+      l_run = l_run * alpha + ls;
+      m_run = mn;
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) acc[tt] *= alpha;
+    };
+    auto mm_pv = [&](const float4 (&x)[4][VD / 4], const float (&pv)[4]) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float vd[VD];
+#pragma unroll
+        for (int u = 0; u < VD / 4; ++u) {
+          vd[4 * u + 0] = x[j][u].x;
+          vd[4 * u + 1] = x[j][u].y;
+          vd[4 * u + 2] = x[j][u].z;
+          vd[4 * u + 3] = x[j][u].w;
+        }
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[tt], pv[j], acc[tt], 0, 0, 0);
+      }
+    };
+    float4 kx[2][NK], vx[2][4][VD / 4];
+    f4 sc[2][4];
+    ld_k(0, kx[0]);
+    ld_v(0, vx[0]);
+    if (NTS > 1) ld_k(1, kx[1]);
+    mm_qk(kx[0], sc[0]);
+#pragma unroll
+    for (int t = 0; t < NTS; ++t) {
+      if (t + 1 < NTS) mm_qk(kx[(t + 1) & 1], sc[(t + 1) & 1]);
+      if (t + 2 < NTS) ld_k(t + 2, kx[t & 1]);
+      if (t + 1 < NTS) ld_v(t + 1, vx[(t + 1) & 1]);
+      float pv[4];
+      softmax(sc[t & 1], pv);
+      mm_pv(vx[t & 1], pv);
+    }
+  };
+
   auto compute_stage = [&](int st, const float* sk, const float* sv) {
     const int nt = !wave_live ? 0 : min(NTS, max(0, (wave_last - st * SK) / 16 + 1));  // uniform
+    if (wave_live && st * SK + SK - 1 <= wave_full) {  // uniform: every tile full
+      stage_full(sk, sv);
+      return;
+    }
     f4 sc[2][4];
     if (nt > 0) qk(0, sk, sc[0]);
 #pragma unroll
@@ -347,22 +486,48 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
   }
 }
 
-// Combines the KS key splits of every (row, query head): one thread per dim.
-template <int HD>
-__global__ __launch_bounds__(HD) void prefill_merge(const float* __restrict__ part,
-                                                    float* __restrict__ out, int n_vec, int ks) {
-  const int rh = blockIdx.x;
-  const int d = threadIdx.x;
-  float M = kMinitP;
-  for (int z = 0; z < ks; ++z) M = fmaxf(M, part[(static_cast<size_t>(z) * n_vec + rh) * (HD + 2) + HD]);
-  float L = 0.0f, O = 0.0f;
-  for (int z = 0; z < ks; ++z) {
+// Combines the KS key splits of every (row, query head): one thread per dim,
+// 256 / HD (row, head) pairs per workgroup. Every record load of a thread is
+// issued before any of them is used (one round trip, not one per split).
+constexpr int kMergeThreads = 256;
+template <int HD, int KS>
+__global__ __launch_bounds__(kMergeThreads) void prefill_merge(const float* __restrict__ part,
+                                                               float* __restrict__ out,
+                                                               int n_vec) {
+  const int rh = blockIdx.x * (kMergeThreads / HD) + static_cast<int>(threadIdx.x) / HD;
+  const int d = threadIdx.x % HD;
+  if (rh >= n_vec) return;
+  float o[KS], m[KS], l[KS];
+#pragma unroll
+  for (int z = 0; z < KS; ++z) {
     const float* r = part + (static_cast<size_t>(z) * n_vec + rh) * (HD + 2);
-    const float w = __builtin_amdgcn_exp2f(r[HD] - M);
-    L += r[HD + 1] * w;
-    O += r[d] * w;
+    o[z] = r[d];
+    m[z] = r[HD];
+    l[z] = r[HD + 1];
+  }
+  float M = kMinitP;
+#pragma unroll
+  for (int z = 0; z < KS; ++z) M = fmaxf(M, m[z]);
+  float L = 0.0f, O = 0.0f;
+#pragma unroll
+  for (int z = 0; z < KS; ++z) {
+    const float w = __builtin_amdgcn_exp2f(m[z] - M);
+    L += l[z] * w;
+    O += o[z] * w;
   }
   out[static_cast<size_t>(rh) * HD + d] = O / L;
+}
+
+template <int HD>
+void launch_merge(const float* part, float* out, int n_vec, int ks, hipStream_t st) {
+  const dim3 grid((n_vec + kMergeThreads / HD - 1) / (kMergeThreads / HD));
+  static_assert(kPrefillMaxSplits == 8, "merge instances for 2, 4 and 8 splits");
+  if (ks == 2)
+    hipLaunchKernelGGL((prefill_merge<HD, 2>), grid, dim3(kMergeThreads), 0, st, part, out, n_vec);
+  else if (ks == 4)
+    hipLaunchKernelGGL((prefill_merge<HD, 4>), grid, dim3(kMergeThreads), 0, st, part, out, n_vec);
+  else
+    hipLaunchKernelGGL((prefill_merge<HD, 8>), grid, dim3(kMergeThreads), 0, st, part, out, n_vec);
 }
 
 template <int HD, int NBUF>
@@ -434,11 +599,9 @@ hipError_t launch_prefill(const KvGeom& g, const KvStore& s, Workspace& ws, cons
                                  dim3(kPThreads), args, 0, st);
   if (e != hipSuccess || ks == 1) return e;
   if (g.hd == 64)
-    hipLaunchKernelGGL(prefill_merge<64>, dim3(c.rows * c.n_heads), dim3(64), 0, st, ws.part,
-                       c.out, c.rows * c.n_heads, ks);
+    launch_merge<64>(ws.part, c.out, c.rows * c.n_heads, ks, st);
   else
-    hipLaunchKernelGGL(prefill_merge<128>, dim3(c.rows * c.n_heads), dim3(128), 0, st, ws.part,
-                       c.out, c.rows * c.n_heads, ks);
+    launch_merge<128>(ws.part, c.out, c.rows * c.n_heads, ks, st);
   return hipGetLastError();
 }
 
