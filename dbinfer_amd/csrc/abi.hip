@@ -1594,7 +1594,13 @@ static dbi_status offload_setup_impl(dbi_kv* kv, const dbi_offload_config* cfg,
   const size_t total =
       2 * r64(cfg->dim) + 2 * r64(qn) + 2 * r64(kvn) + 2 * r64(cfg->ff) + r64(nlog);
   if (hipMalloc(reinterpret_cast<void**>(&o.buf), total * sizeof(float)) != hipSuccess) {
+    // the previous setup is gone with its scratch: leave no pointer into it
+    o.buf = nullptr;
     o.layers.clear();
+    o.logits = nullptr;
+    o.cfg = dbi_offload_config{};
+    if (o.owned) (void)hipFree(o.owned);
+    o.owned = nullptr;
     return fail(DBI_ERR_NOMEM, "offload scratch allocation failed");
   }
   float* p = o.buf;
