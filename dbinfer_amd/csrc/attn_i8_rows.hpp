@@ -57,7 +57,10 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
   constexpr int NTV = C::NTV, VL = C::VL, OP = C::OP;
   constexpr int CHUNK = kKGroup;
 
-  __shared__ __align__(16) float s_q[NQ][HD];  // q * scale * log2 e (0 past the queries)
+  // q * scale * log2 e (0 past the queries); rows padded by 16 bytes: a q~
+  // read takes one 16-byte piece of 16 consecutive rows, which a 512-byte
+  // pitch would put in the same banks
+  __shared__ __align__(16) float s_q[NQ][HD + 4];
   __shared__ __align__(16) float s_o[kWaves][16][OP];
   __shared__ float s_ml[kWaves][16][2];
 
