@@ -772,9 +772,14 @@ struct FusedAppend {
   // The stages to global memory in whole contiguous pieces, by one wave per
   // kv head, after its last load.
   // (kg: the dense int8 group stage; null for the other layouts)
+  // vblock (dense int8, optional): the new row's whole V chunk block as the
+  // owner holds it, 16 bytes per lane per 1 KiB piece (the chunk's V loads
+  // with the row's codes patched in); written back in whole lines instead of
+  // the row's bytes scattered one per 16-byte unit
   __device__ __forceinline__ static void flush(const AppendArgs& A, int kh, int lane,
                                                const AppStage& st, const KGroupStage* kg,
-                                               const float* row) {
+                                               const float* row,
+                                               const uint4* vblock = nullptr) {
     const bool on = 2 * lane < HD;
     const int d = 2 * lane;
     const size_t hel = static_cast<size_t>(kh) * A.capg * HD;
@@ -805,7 +810,12 @@ struct FusedAppend {
         }
       }
       if (pos >= A.n_sink) {
-        if (on) {  // V row: one byte per channel (channels d, d + 1 of this lane)
+        if (vblock != nullptr) {  // the chunk's V block, HD / 32 pieces of 1 KiB
+          uint8_t* vb = A.v8 + hel + static_cast<size_t>(pos / kKGroup) * kKGroup * HD;
+#pragma unroll
+          for (int tp = 0; tp < HD / 32; ++tp)
+            *reinterpret_cast<uint4*>(vb + tp * 1024 + lane * 16) = vblock[tp];
+        } else if (on) {  // V row: one byte per channel (channels d, d + 1 of this lane)
           const uint8_t* v8s = reinterpret_cast<const uint8_t*>(st.v8row);
           A.v8[hel + v_off_i8d(HD, pos, d)] = v8s[d];
           A.v8[hel + v_off_i8d(HD, pos, d + 1)] = v8s[d + 1];
