@@ -382,8 +382,11 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     for (int t = 0; t < NTV; ++t) o[T][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  // the owner's V chunk block with the new row patched in, kept for the flush
-  uint4 app_v[VL];
+  // the owner's V chunk block with the new row patched in, kept for the
+  // flush (plain inputs only: the producer instance has no registers to spare
+  // and writes the row's bytes)
+  constexpr bool kKeepV = !PROD;
+  uint4 app_v[kKeepV ? VL : 1];
   // next >= 0: the chunk whose loads go into b as this chunk frees it
   auto compute = [&](Buf& b, const int ch, const bool first, const int next) {
     // products feeding split3 are rounded to fp32 first (q * ks, as the
@@ -424,8 +427,10 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
         for (int s = 0; s < 8; ++s) b.vs[s] = s == ss ? s_stage.vs[col % NBK] : b.vs[s];
       }
       // every lane's part of the patched V block, for the flush
+      if constexpr (kKeepV) {
 #pragma unroll
-      for (int tp = 0; tp < VL; ++tp) app_v[tp] = b.v[tp];
+        for (int tp = 0; tp < VL; ++tp) app_v[tp] = b.v[tp];
+      }
     }
 
     // ---- q~ of this chunk's K group, three bf16 parts, into LDS
@@ -682,7 +687,8 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     for (int pr = wave; pr < nqv; pr += kWaves)
       if (s_last[pr / G]) merge_head<HD, G>(P, kh, row0 + pr / G, pr % G, lane);
   }
-  if (kFuse && app_owner) App::flush(A, kh, lane, s_stage, &s_kg, s_row, app_v);
+  if (kFuse && app_owner)
+    App::flush(A, kh, lane, s_stage, &s_kg, s_row, kKeepV ? app_v : nullptr);
 }
 
 // The largest rows-per-workgroup a (hd, G) instance serves: its query
