@@ -159,10 +159,10 @@ dbi_status ensure_part(dbi_kv* kv, size_t part) {
   return DBI_OK;
 }
 
-dbi_status ensure_workspace(dbi_kv* kv, const dbi::AttnCall& c) {
-  if (dbi_status st = ensure_part(kv, dbi::attention_workspace_need(kv->geom, c))) return st;
+// records of `part` floats and `cnt` split counters, grown only
+dbi_status ensure_ws_sizes(dbi_kv* kv, size_t part, size_t cnt) {
+  if (dbi_status st = ensure_part(kv, part)) return st;
   // the kernels leave the counters at zero; a fresh array starts there
-  const size_t cnt = dbi::attention_counters_need(kv->geom, c);
   if (cnt > kv->ws.counters_n) {
     if (dbi_status st = refuse_capture(kv, "the split counters")) return st;
     HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
@@ -178,6 +178,11 @@ dbi_status ensure_workspace(dbi_kv* kv, const dbi::AttnCall& c) {
     kv->ws.counters_n = cnt;
   }
   return DBI_OK;
+}
+
+dbi_status ensure_workspace(dbi_kv* kv, const dbi::AttnCall& c) {
+  return ensure_ws_sizes(kv, dbi::attention_workspace_need(kv->geom, c),
+                         dbi::attention_counters_need(kv->geom, c));
 }
 
 dbi_status check_attend(const dbi_kv* kv, uint32_t layer, uint32_t n_heads, const void* q,
@@ -1585,6 +1590,13 @@ static dbi_status offload_setup_impl(dbi_kv* kv, const dbi_offload_config* cfg,
   }
   if (dbi_status st = refuse_capture(kv, "the offload scratch")) return st;
   HIP_TRY(hipStreamSynchronize(kv->stream), "stream sync");
+  // the token calls allocate nothing: the rope table and the split workspace
+  // of the largest decode plan at any position are in place from here on
+  if (dbi_status st = ensure_rope_table(kv)) return st;
+  if (dbi_status st = ensure_ws_sizes(
+          kv, dbi::attention_workspace_bound(kv->geom, static_cast<int>(cfg->n_heads)),
+          dbi::attention_counters_bound(kv->geom)))
+    return st;
   OffloadState& o = kv->off;
   if (o.buf) (void)hipFree(o.buf);
   o.buf = nullptr;

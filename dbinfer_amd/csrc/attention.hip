@@ -102,6 +102,14 @@ size_t attention_workspace_need(const KvGeom& g, const AttnCall& c) {
   return p.merge ? static_cast<size_t>(c.rows) * g.nkv * record_region(p.nsplit, G, g.hd) : 0;
 }
 
+size_t attention_workspace_bound(const KvGeom& g, int n_heads) {
+  return static_cast<size_t>(g.nkv) * record_region(kMaxSplits, n_heads / g.nkv, g.hd);
+}
+
+size_t attention_counters_bound(const KvGeom& g) {
+  return static_cast<size_t>(g.nkv) * kCounterStride;
+}
+
 hipError_t launch_attention(const KvGeom& g, const KvStore& s, Workspace& ws, const AttnCall& c,
                             hipStream_t st) {
   const int G = c.n_heads / g.nkv;

@@ -207,6 +207,10 @@ size_t prefill_workspace_need(const KvGeom& g, const AttnCall& c);
 hipError_t launch_prefill(const KvGeom& g, const KvStore& s, Workspace& ws, const AttnCall& c,
                           hipStream_t st);
 size_t attention_counters_need(const KvGeom& g, const AttnCall& c);
+// The largest record floats / counters a one-row decode call of n_heads can
+// need at any position (the planner's split cap bounds both).
+size_t attention_workspace_bound(const KvGeom& g, int n_heads);
+size_t attention_counters_bound(const KvGeom& g);
 bool attention_supported(const KvGeom& g, int n_heads);
 // Key splits (partial records per query row and kv head) of a call.
 int attention_split_count(const KvGeom& g, const AttnCall& c);

@@ -60,6 +60,7 @@ class HipKV:
         self.n_sink, self.window, self.dtype, self.rope_theta = n_sink, window, dtype, rope_theta
         self.pos_stride = n_kv_heads * head_dim
         self.n_blocks = (head_dim + 31) // 32
+        self._vocab = 0  # logits length bound by offload_setup (0: no tail)
 
     # ---- lifetime
     def close(self) -> None:
@@ -296,6 +297,7 @@ class HipKV:
                                  _lib.Weight(*(lm_head if lm_head else (None, 0))), vocab)
         fn = self._lib.dbi_offload_setup_host if host else self._lib.dbi_offload_setup
         _check(self._lib, fn(self._h, ctypes.byref(cfg), arr, len(layers)))
+        self._vocab = vocab if lm_head else 0
 
     def decode_token_async(self, x_dev: int, pos: int) -> None:
         _check(self._lib, self._lib.dbi_decode_token_async(self._h, x_dev, pos))
@@ -310,6 +312,10 @@ class HipKV:
         return xa
 
     def decode_token_full(self, x, pos: int, vocab: int) -> np.ndarray:
+        # the library writes the vocabulary bound at setup: a buffer of any
+        # other size would be overrun or left short
+        if vocab != self._vocab:
+            raise ValueError(f"vocab {vocab} differs from the {self._vocab} bound at setup")
         xa = _f32(x)
         logits = np.empty(vocab, np.float32)
         _check(self._lib, self._lib.dbi_decode_token_full(self._h, _ptr(xa), pos, _ptr(logits)))

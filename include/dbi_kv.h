@@ -307,7 +307,9 @@ typedef struct dbi_offload_config {
 /* Backend::setup_offload (backend.hpp:133-143): binds n_layers blocks (the
  * first n_layers of the cache's layers) and the tail; the weights are the
  * caller's device memory, used in place until the next setup or destroy.
- * Allocates the layer's scratch rows; not under graph capture. The cache may
+ * Allocates the layer's scratch rows, the dense cache's rope table and the
+ * attention split workspace of the largest decode plan at any position;
+ * not under graph capture. The cache may
  * be any layout (the reference offloads dense fp32 only, main.cpp:241-244):
  * dense fp32 and int8 attend after rope + append at pos, a ring through its
  * own attention (model.cpp:757-771). dim, ff and n_heads*head_dim must be
@@ -320,8 +322,10 @@ dbi_status dbi_offload_setup(dbi_kv* kv, const dbi_offload_config* cfg,
  * decode_layer's sequence: rmsnorm, q/k/v matvecs, biases, rope, append,
  * attention (the fused decode step), o_proj + residual, rmsnorm, gate/up,
  * silu(gate) * up, down + residual. x_dev: device [dim] (16-byte aligned),
- * the residual stream, updated in place. Allocates nothing; capturable
- * after the handle's first producer call (which builds its rope table).
+ * the residual stream, updated in place. Allocates nothing and never syncs:
+ * dbi_offload_setup builds the rope table and sizes the split workspace for
+ * the largest decode plan at any position, so a call is capturable into a
+ * HIP graph right after setup.
  * Each matvec sums in a tree and rmsnorm's sum of squares too, so results
  * agree with the reference to the rounding of those sums; with Q8_0 / Q4_0
  * weights a rounding difference can move an activation code across a

@@ -267,3 +267,45 @@ def test_host_rows_equal_device_rows(torch, wt):
     assert "Q4_0 weights only" in e.value.message
     del keep, keep2
     gd.close(), gd2.close(), gh.close()
+
+
+@pytest.mark.parametrize("layout", ["f32", "int8"])
+def test_decode_token_captured_after_setup(torch, layout):
+    """dbi_offload_setup sizes the rope table and the split workspace of the
+    largest decode plan, so the token call allocates nothing: after one eager
+    call at position 0, a call at position 5000 (a wider split plan than any
+    earlier call) is captured into a HIP graph without an eager warm-up, and
+    every replay equals the eager call bit for bit. A call that grew the
+    workspace would fail under capture (refuse_capture)."""
+    rng = np.random.default_rng(77)
+    lws = [layer_weights(rng, DIM, FF, NH, NKV, HD, W_F16, True) for _ in range(L)]
+    cap, pos = 5008, 5000
+    g = HipKV(L, cap, NKV, HD, rope_theta=1e4, **LAYOUTS[layout])
+    keep = bind(torch, g, lws)
+    g.set_stream(torch.cuda.current_stream().cuda_stream)
+    g.decode_token_async(dev(torch, normal(600, DIM)).data_ptr(), 0)
+    torch.cuda.synchronize()
+    assert g.splits(pos, 1, NH) > g.splits(0, 1, NH)
+    x0 = dev(torch, normal(601, DIM))
+    xt = x0.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    g.set_stream(s.cuda_stream)
+    with torch.cuda.graph(graph, stream=s):
+        g.decode_token_async(xt.data_ptr(), pos)
+    torch.cuda.synchronize()
+    g.set_stream(torch.cuda.current_stream().cuda_stream)
+    xe = x0.clone()
+    g.decode_token_async(xe.data_ptr(), pos)  # the same row appended again
+    torch.cuda.synchronize()
+    want = xe.cpu().numpy().view(np.uint32)
+    for rep in range(3):
+        xt.copy_(x0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = xt.cpu().numpy().view(np.uint32)
+        assert np.array_equal(got, want), f"{layout} replay {rep}"
+    del graph, keep
+    g.close()

@@ -195,3 +195,24 @@ def test_decode_layer_wiring(layout, wt, bias):
         assert np.array_equal(xa.view(np.uint32), xb.view(np.uint32)), f"pos {pos}"
         for kv in (a, b):
             kv.mark_position(pos)
+
+
+@pytest.mark.parametrize("wt", [W_F32, W_F16, W_Q8_0, W_Q4_0])
+def test_logits_tail_wiring(wt):
+    """ok_logits (Model::forward's tail, model.cpp:914-915) is rmsnorm with
+    output_norm, then the lm_head matvec: bit for bit the composition of the
+    two pinned functions (rmsnorm against the reference build, the matvec
+    against its integer restatement). A tail that skipped the norm, or
+    normed with unit weights, gives other bits (the check can fail)."""
+    dim, vocab, eps = 256, 300, 1e-5
+    rng = np.random.default_rng(23 + wt)
+    lm = layer_weights(rng, dim, vocab, 4, 2, 32, wt, False)["w"][4]  # [vocab][dim]
+    onorm = (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    for seed in range(3):
+        x = normal(700 + seed, dim) * 2.0
+        got = pyoracle.logits(x, onorm, lm, wt, eps, vocab)
+        want = pyoracle.matvec(lm, wt, pyoracle.rmsnorm(x, onorm, eps), vocab)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"seed {seed}"
+        unnormed = pyoracle.matvec(lm, wt, x, vocab)
+        unit = pyoracle.matvec(lm, wt, pyoracle.rmsnorm(x, np.ones(dim, np.float32), eps), vocab)
+        assert not np.array_equal(got, unnormed) and not np.array_equal(got, unit)

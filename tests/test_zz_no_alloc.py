@@ -111,3 +111,52 @@ def test_noalloc_largest_plan():
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     for kv in (ref, new):
         kv.close()
+
+
+def test_noalloc_captured_on_fresh_handle():
+    """The allocation-free step needs no eager warm-up: on a handle that has
+    never attended, a call at config 3's 32-split plan is captured into a HIP
+    graph (a workspace growth would be refused under capture), and every
+    replay equals dbi_kv_decode_async on a twin handle bit for bit."""
+    torch = pytest.importorskip("torch")
+    nh, nkv, hd, n_sink, ctx = 24, 8, 128, 4, 8192
+    P, Q = nkv * hd, nh * hd
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    rng = np.random.default_rng(1700)
+    K = rng.standard_normal((ctx, P), dtype=np.float32)
+    V = rng.standard_normal((ctx, P), dtype=np.float32)
+    q = rng.standard_normal(Q, dtype=np.float32)
+    ref = HipKV(1, ctx, nkv, hd, n_sink, 0, INT8, 1e6)
+    new = HipKV(1, ctx, nkv, hd, n_sink, 0, INT8, 1e6)
+    for kv in (ref, new):
+        kv.append_n(0, 0, K[:-1], V[:-1])
+    assert new.splits(ctx - 1, 1, nh) == 32
+    Kd, Vd, qd = (torch.from_numpy(a).cuda() for a in (K, V, q))
+    out_ref = torch.full((Q,), float("nan"), device="cuda")
+    out_new = torch.full((Q,), float("nan"), device="cuda")
+    pos = ctx - 1
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    new.set_stream(s.cuda_stream)
+    with torch.cuda.graph(graph, stream=s):
+        new.decode_noalloc_async(0, pos, Kd[pos].data_ptr(), Vd[pos].data_ptr(), nh, scale,
+                                 qd.data_ptr(), out_new.data_ptr())
+    torch.cuda.synchronize()
+    ref.set_stream(torch.cuda.current_stream().cuda_stream)
+    ref.decode_async(0, pos, Kd[pos].data_ptr(), Vd[pos].data_ptr(), nh, scale, qd.data_ptr(),
+                     out_ref.data_ptr())
+    torch.cuda.synchronize()
+    want = out_ref.cpu().numpy().view(np.uint32)
+    for rep in range(3):
+        out_new.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out_new.cpu().numpy().view(np.uint32), want), f"replay {rep}"
+    for n in stores(INT8, 0, n_sink):
+        assert np.array_equal(new.export(n, 0).view(np.uint8), ref.export(n, 0).view(np.uint8)), n
+    del graph
+    for kv in (ref, new):
+        kv.close()
