@@ -368,12 +368,18 @@ __device__ __forceinline__ void finish(const AttnParams& P, float (&s_o)[kWaves]
 // SINKS: the dense int8 fp32 sinks (positions < n_sink, model.cpp:612-626)
 // of this row are attended here too (the rows kernels leave them to the
 // merge): their scores join the split maxima, their V rows the sum.
-template <int HD, int G, bool SINKS = false>
+// MAXS (32 or 64) bounds nsplit: the loads and sums are straight-line over
+// MAXS splits (splits past nsplit reload the last record and weigh 0), and
+// each lane fetches the weight of its split from the split's lane with an
+// independent ds_bpermute; a per-split branch and readlane chain, with its
+// SGPR hazards, cost ~1.2 us per merge at 32 splits.
+template <int HD, int G, bool SINKS = false, int MAXS = kMaxSplits>
 __device__ __forceinline__ void merge_head(const AttnParams& P, int kh, int qrow, int g, int lane) {
   constexpr int kSC1 = 16;  // cache policy: agent-coherent load
   constexpr int LPH = HD / 4;       // lanes per record of one head
   constexpr int SPI = 64 / LPH;     // splits per load instruction
-  constexpr int NI = kMaxSplits / SPI;
+  constexpr int NI = MAXS / SPI;
+  static_assert(MAXS <= kMaxSplits, "split bound");
   const size_t head_base = static_cast<size_t>(qrow) * P.nkv + kh;
   constexpr int RF = record_floats(G, HD);
   const float* region = P.part + head_base * record_region(P.nsplit, G, HD);
@@ -383,16 +389,13 @@ __device__ __forceinline__ void merge_head(const AttnParams& P, int kh, int qrow
       float2, __builtin_amdgcn_raw_buffer_load_b64(ro, (min(lane, P.nsplit - 1) * RF + G * HD + 2 * g) * 4,
                                                    0, kSC1));
   const int sub = lane / LPH, dl = lane % LPH;  // split within an instruction, dims 4dl..
-  const int ni = (P.nsplit + SPI - 1) / SPI;    // uniform
   float4 ov[NI];
 #pragma unroll
   for (int k = 0; k < NI; ++k) {
-    if (k < ni) {
-      const int sp = min(k * SPI + sub, P.nsplit - 1);
-      ov[k] = __builtin_bit_cast(
-          float4, __builtin_amdgcn_raw_buffer_load_b128(ro, (sp * RF + g * HD + 4 * dl) * 4, 0,
-                                                        kSC1));
-    }
+    const int sp = min(k * SPI + sub, P.nsplit - 1);
+    ov[k] = __builtin_bit_cast(
+        float4, __builtin_amdgcn_raw_buffer_load_b128(ro, (sp * RF + g * HD + 4 * dl) * 4, 0,
+                                                      kSC1));
   }
   // the sinks' scores (uniform): q * scale * log2 e (as the kernels scale it)
   // against each sink's K row, dims lane and lane + 64 of each lane
@@ -439,21 +442,20 @@ __device__ __forceinline__ void merge_head(const AttnParams& P, int kh, int qrow
   const float w = on ? fast_exp2(ml.x - M) : 0.0f;  // splits past nsplit weigh 0
   float L = wave_sum(on ? ml.y * w : 0.0f);
   float4 acc[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
-  auto lane_w = [&](int sp) {  // weight of split sp (scalar: readlane)
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), sp));
-  };
+  // weight of this lane's split of instruction k, from lane k * SPI + sub
+  // (0 past nsplit); the fetches are independent of each other
+  float ws[NI];
+#pragma unroll
+  for (int k = 0; k < NI; ++k)
+    ws[k] = __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_bpermute(4 * (k * SPI + sub), __builtin_bit_cast(int, w)));
 #pragma unroll
   for (int k = 0; k < NI; ++k) {
-    if (k < ni) {
-      float ws = lane_w(k * SPI);
-#pragma unroll
-      for (int j = 1; j < SPI; ++j) ws = sub == j ? lane_w(k * SPI + j) : ws;
-      float4& a = acc[k & 1];
-      a.x = fmaf(ws, ov[k].x, a.x);
-      a.y = fmaf(ws, ov[k].y, a.y);
-      a.z = fmaf(ws, ov[k].z, a.z);
-      a.w = fmaf(ws, ov[k].w, a.w);
-    }
+    float4& a = acc[k & 1];
+    a.x = fmaf(ws[k], ov[k].x, a.x);
+    a.y = fmaf(ws[k], ov[k].y, a.y);
+    a.z = fmaf(ws[k], ov[k].z, a.z);
+    a.w = fmaf(ws[k], ov[k].w, a.w);
   }
   float o4[4] = {acc[0].x + acc[1].x, acc[0].y + acc[1].y, acc[0].z + acc[1].z,
                  acc[0].w + acc[1].w};
@@ -491,10 +493,20 @@ __device__ __forceinline__ void merge_head(const AttnParams& P, int kh, int qrow
         make_float4(o4[0] * inv, o4[1] * inv, o4[2] * inv, o4[3] * inv);
   }
 }
+// merge_head with the split bound of the plan (uniform choice)
+template <int HD, int G, bool SINKS = false>
+__device__ __forceinline__ void merge_split(const AttnParams& P, int kh, int qrow, int g,
+                                            int lane) {
+  if (P.nsplit <= 32)
+    merge_head<HD, G, SINKS, 32>(P, kh, qrow, g, lane);
+  else
+    merge_head<HD, G, SINKS, kMaxSplits>(P, kh, qrow, g, lane);
+}
+
 template <int HD, int G>
 __device__ __forceinline__ void merge_last(const AttnParams& P, int kh, int qrow, int wave,
                                            int lane) {
-  if (wave < G) merge_head<HD, G>(P, kh, qrow, wave, lane);
+  if (wave < G) merge_split<HD, G>(P, kh, qrow, wave, lane);
 }
 
 

@@ -685,7 +685,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     __syncthreads();
     // the (row, head) merges this workgroup owns, one wave each
     for (int pr = wave; pr < nqv; pr += kWaves)
-      if (s_last[pr / G]) merge_head<HD, G>(P, kh, row0 + pr / G, pr % G, lane);
+      if (s_last[pr / G]) merge_split<HD, G>(P, kh, row0 + pr / G, pr % G, lane);
   }
   if (kFuse && app_owner)
     App::flush(A, kh, lane, s_stage, &s_kg, s_row, kKeepV ? app_v : nullptr);

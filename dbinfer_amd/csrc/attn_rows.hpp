@@ -323,9 +323,9 @@ __global__ __launch_bounds__(64) void attn_rows_merge(const AttnParams P) {
   const int pr = blockIdx.x;  // (row, kv head, head) pair
   const int g = pr % G, kh = (pr / G) % P.nkv, qrow = pr / (G * P.nkv);
   if (P.n_sink > 0)
-    merge_head<HD, G, true>(P, kh, qrow, g, threadIdx.x);
+    merge_split<HD, G, true>(P, kh, qrow, g, threadIdx.x);
   else
-    merge_head<HD, G, false>(P, kh, qrow, g, threadIdx.x);
+    merge_split<HD, G, false>(P, kh, qrow, g, threadIdx.x);
 }
 
 template <int HD, int NVT>
