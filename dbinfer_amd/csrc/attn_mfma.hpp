@@ -86,6 +86,38 @@ __device__ __forceinline__ f32x4 mfma(const bf16x8& a, const uint4& b, const f32
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+using i32x4 = int __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 mfma_i8(const i32x4& a, const uint4& b, const i32x4& c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+}
+
+// planes[i] = byte i of d0, d1, d2, d3 (in that byte order): a 4 x 4 byte
+// transpose in eight v_perm_b32
+__device__ __forceinline__ void byte_planes(const uint32_t (&d)[4], uint32_t (&planes)[4]) {
+  const uint32_t ab_lo = __builtin_amdgcn_perm(d[1], d[0], 0x05010400u);  // a0 b0 a1 b1
+  const uint32_t ab_hi = __builtin_amdgcn_perm(d[1], d[0], 0x07030602u);  // a2 b2 a3 b3
+  const uint32_t cd_lo = __builtin_amdgcn_perm(d[3], d[2], 0x05010400u);
+  const uint32_t cd_hi = __builtin_amdgcn_perm(d[3], d[2], 0x07030602u);
+  planes[0] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u);
+  planes[1] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u);
+  planes[2] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u);
+  planes[3] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u);
+}
+
+// max / sum of a lane's value over the 16 lanes of its row (DPP butterfly)
+__device__ __forceinline__ float row16_max(float a) {
+  a = fmaxf(a, dpp<kX1>(a));
+  a = fmaxf(a, dpp<kX2>(a));
+  a = fmaxf(a, dpp<kX7>(a));
+  return fmaxf(a, dpp<kX8>(a));
+}
+__device__ __forceinline__ float row16_sum(float a) {
+  a += dpp<kX1>(a);
+  a += dpp<kX2>(a);
+  a += dpp<kX7>(a);
+  return a + dpp<kX8>(a);
+}
+
 // max / sum of a lane's value over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four
 // 16-lane rows of one matrix column)
 __device__ __forceinline__ float col_max(float a) {
@@ -151,6 +183,11 @@ struct MCfg {
   static constexpr int VL = HD / 32;           // V loads per chunk (two tiles each)
   static constexpr int QROW = HD / 8 + 4;      // uint4 per q~ row in LDS (64-byte pad: no
                                                // bank conflicts between the 4 x 4 lane groups)
+  static constexpr int NT2 = (NQ + 3) / 4;     // int8 QK^T row tiles: 4 queries x 4 digits
+  static constexpr int KS = HD / 64;           // int8 QK^T k-steps (64 channels)
+  // queries a weight / rescale row of LDS holds (the PV tiles may cover more
+  // than the QK^T tiles: hd 64 puts 8 queries in a PV tile)
+  static constexpr int NQS = (NT2 * 4 > NT * QVT) ? NT2 * 4 : NT * QVT;
   static_assert(HD == 64 || HD == 128, "head dim");
   static_assert(QVT * LPQ == 64, "one q~ tile per wave pass");
 };
@@ -233,8 +270,9 @@ template <int HD, int G, bool PROD, int CPW, int NR>
 __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, const AppendArgs A) {
   constexpr int NQ = NR * G;
   using C = MCfg<HD, NQ>;
-  constexpr int NBK = C::NBK, QVT = C::QVT, NT = C::NT, LPQ = C::LPQ, NJ = C::NJ;
-  constexpr int KL = C::KL, NTV = C::NTV, VL = C::VL, QROW = C::QROW;
+  constexpr int NBK = C::NBK, QVT = C::QVT, NT = C::NT, LPQ = C::LPQ;
+  constexpr int KL = C::KL, NTV = C::NTV, VL = C::VL;
+  constexpr int NT2 = C::NT2, KS = C::KS, NQS = C::NQS;
   constexpr int CHUNK = kKGroup;
   constexpr int NB = NBK;
 
@@ -243,7 +281,13 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   __shared__ float s_o[kWaves][NQ][HD];
   __shared__ float s_ml[kWaves][NQ][2];
   __shared__ int s_last[NR];
-  __shared__ __align__(16) uint4 s_qt[kWaves][NT][3][QVT][QROW];
+  // q~ digits: the int8 QK^T A operand of row tile T2, k-step jp, lane
+  // group g, row m (lane m + 16 g reads [T2][jp][g][m]: 16 consecutive
+  // bytes per lane, no bank conflicts)
+  __shared__ __align__(16) uint4 s_qd[kWaves][NT2][KS][4][16];
+  __shared__ float s_qsc[kWaves][NT2 * 4];       // 2^-S of each query's digits
+  __shared__ __align__(16) float s_p[kWaves][NQS][32];  // chunk weights (masked: -1)
+  __shared__ float s_al[kWaves][NQS];            // rescale factor of each query
   // fused step stages (the single head group's)
   __shared__ __align__(16) AppStage s_stage;
   __shared__ __align__(16) float s_row[PROD ? 768 : 256];
@@ -369,18 +413,20 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
 #pragma unroll
     for (int e = 0; e < 8; ++e) qs[T][e] = T * QVT + qvl < nqv ? qs[T][e] * P.qscale : 0.0f;
 
-  // running state: per column tile, the max and the lane's partial sum of its
-  // column's query (QK^T layout), and the PV accumulators (row (query,
-  // block), column = channel of tile t)
-  float M[NT], l[NT];
+  // running state: per QK^T row tile, the max and the lane's partial sum of
+  // the query of its lane group (query 4 T2 + grp), and the PV accumulators
+  // (row (query, block), column = channel of tile t)
+  float M[NT2], l[NT2];
   f32x4 o[NT][NTV];
 #pragma unroll
-  for (int T = 0; T < NT; ++T) {
-    M[T] = kMinit;
-    l[T] = 0.0f;
+  for (int T2 = 0; T2 < NT2; ++T2) {
+    M[T2] = kMinit;
+    l[T2] = 0.0f;
+  }
+#pragma unroll
+  for (int T = 0; T < NT; ++T)
 #pragma unroll
     for (int t = 0; t < NTV; ++t) o[T][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
 
   // the owner's V chunk block with the new row patched in, kept for the
   // flush (plain inputs only: the producer instance has no registers to spare
@@ -433,48 +479,93 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
       }
     }
 
-    // ---- q~ of this chunk's K group, three bf16 parts, into LDS
+    // ---- q~ of this chunk's K group as exact base-256 digits, into LDS.
+    // Per query, X = trunc(q~ * 2^S) with S fitting |X| < 2^30, and
+    // X = sum_i 256^i D_i with balanced digits D_i in [-128, 127] (the
+    // bytes of (X + 0x80808080) ^ 0x80808080). Digit i of query q is row
+    // 4 (q % 4) + i of row tile q / 4; the lane's 8 channels are 8 bytes of
+    // one A operand (channel 64 jp + 32 j2 + 8 g + e at byte 8 j2 + e, the
+    // order of the K codes in the B operand).
     {
       const float ks8[8] = {b.ks[0].x, b.ks[0].y, b.ks[0].z, b.ks[0].w,
                             b.ks[1].x, b.ks[1].y, b.ks[1].z, b.ks[1].w};
+      const int jp = c8 / 8, j2 = (c8 / 4) % 2, gq = c8 % 4;
 #pragma unroll
       for (int T = 0; T < NT; ++T) {
-        float x[8];
+        const int qv = T * QVT + qvl;
+        float x[8], mx = 0.0f, nf = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = qs[T][e] * ks8[e];
-        uint4 pt[3];
-        split3(x, pt);
+        for (int e = 0; e < 8; ++e) {
+          x[e] = qs[T][e] * ks8[e];
+          mx = fmaxf(mx, fabsf(x[e]));
+          nf += x[e];
+        }
+        // the query's max over its LPQ lanes; nf becomes NaN when any of its
+        // q~ is not finite (the digits cannot carry it: the scale below does)
+        nf *= 0.0f;
+        mx = fmaxf(mx, dpp<kX1>(mx));
+        nf += dpp<kX1>(nf);
+        mx = fmaxf(mx, dpp<kX2>(mx));
+        nf += dpp<kX2>(nf);
+        mx = fmaxf(mx, dpp<kX7>(mx));
+        nf += dpp<kX7>(nf);
+        if constexpr (LPQ == 16) {
+          mx = fmaxf(mx, dpp<kX8>(mx));
+          nf += dpp<kX8>(nf);
+        }
+        const int ex = __builtin_amdgcn_frexp_expf(mx);  // mx < 2^ex
+        const float up = __builtin_amdgcn_ldexpf(1.0f, 30 - ex);
+        uint32_t d[8];
 #pragma unroll
-        for (int a = 0; a < 3; ++a) s_qt[wave][T][a][qvl][c8] = pt[a];
+        for (int e = 0; e < 8; ++e)
+          d[e] = (static_cast<uint32_t>(static_cast<int>(x[e] * up)) + 0x80808080u) ^ 0x80808080u;
+        uint32_t lo[4], hi[4];
+        byte_planes({d[0], d[1], d[2], d[3]}, lo);
+        byte_planes({d[4], d[5], d[6], d[7]}, hi);
+        if (qv < NT2 * 4) {
+          uint8_t* rowb = reinterpret_cast<uint8_t*>(&s_qd[wave][qv / 4][jp][gq][0]) + 8 * j2;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<uint2*>(rowb + 16 * (4 * (qv % 4) + i)) = make_uint2(lo[i], hi[i]);
+          if (c8 == 0) s_qsc[wave][qv] = __builtin_amdgcn_ldexpf(1.0f, ex - 30) + nf;
+        }
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- QK^T: scores of column col (query T*QVT + col / NBK) at positions
-    // 16h + 4*grp + i, i < 4
-    f32x4 sc[2][NT];
+    // ---- QK^T on the int8 matrix cores: row 4 g + i of tile T2 = digit i
+    // of query 4 T2 + g, column = position 16 h + col; every product and
+    // sum is exact in int32. The score combines the digits in fp32.
+    float sc[2][NT2];
+    {
+      i32x4 acc[2][NT2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int T = 0; T < NT; ++T) sc[h][T] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int T2 = 0; T2 < NT2; ++T2) acc[h][T2] = i32x4{0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      bf16x8 ak[2];
+      for (int jp = 0; jp < KS; ++jp)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint4 w = b.k[h][j / 2];
-        ak[h] = (j & 1) ? codes_bf16(w.z, w.w) : codes_bf16(w.x, w.y);
-      }
+        for (int T2 = 0; T2 < NT2; ++T2) {
+          const i32x4 a = __builtin_bit_cast(i32x4, s_qd[wave][T2][jp][grp][col]);
 #pragma unroll
-      for (int T = 0; T < NT; ++T)
-#pragma unroll
-        for (int a = 0; a < 3; ++a) {
-          const uint4 bq = s_qt[wave][T][a][col / NBK][4 * j + grp];
-#pragma unroll
-          for (int h = 0; h < 2; ++h) sc[h][T] = mfma(ak[h], bq, sc[h][T]);
+          for (int h = 0; h < 2; ++h) acc[h][T2] = mfma_i8(a, b.k[h][jp], acc[h][T2]);
         }
+#pragma unroll
+      for (int T2 = 0; T2 < NT2; ++T2) {
+        const float down = s_qsc[wave][4 * T2 + grp];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const i32x4 a = acc[h][T2];
+          float t = static_cast<float>(a[3]);
+          t = fmaf(t, 256.0f, static_cast<float>(a[2]));
+          t = fmaf(t, 256.0f, static_cast<float>(a[1]));
+          t = fmaf(t, 256.0f, static_cast<float>(a[0]));
+          sc[h][T2] = t * down;
+        }
+      }
     }
 
     if (next >= 0) {  // uniform: this chunk's K registers are read
@@ -483,47 +574,55 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
       __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- online softmax per column, then the PV A operand of the lane
+    // ---- online softmax per query (its 16 lanes hold the chunk's 32
+    // positions, two each); the weights go to LDS for the PV A operand
+#pragma unroll
+    for (int T2 = 0; T2 < NT2; ++T2) {
+      const int qv = 4 * T2 + grp;
+      // keys of this query's row (causal: row r attends [0, pos0 + r])
+      const int nk = qv < nqv ? P.pos0 + row0 + qv / G + 1 : 0;
+      float sv[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int p = p0 + 16 * h + col;
+        sv[h] = p < nk && p >= P.n_sink ? sc[h][T2] : -INFINITY;
+      }
+      const float mn = fmaxf(M[T2], row16_max(fmaxf(sv[0], sv[1])));
+      const float alpha = first ? 0.0f : fast_exp2(M[T2] - mn);
+      M[T2] = mn;
+      const float p0w = fast_exp2(sv[0] - mn), p1w = fast_exp2(sv[1] - mn);
+      l[T2] = first ? p0w + p1w : fmaf(l[T2], alpha, p0w + p1w);
+      // masked slots: -1, weighed exactly 0 (their stale V scales may be anything)
+      s_p[wave][qv][col] = sv[0] != -INFINITY ? p0w : -1.0f;
+      s_p[wave][qv][16 + col] = sv[1] != -INFINITY ? p1w : -1.0f;
+      if (col == 0) s_al[wave][qv] = alpha;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- PV: A = weight x V block scale in three bf16 parts, row (query,
+    // block) = col, k = the lane's 8 positions 16 (s / 4) + 4 grp + s % 4
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
-      // keys of this column's row (causal: row r attends [0, pos0 + r])
-      const int nk = P.pos0 + row0 + (T * QVT + col / NBK) / G + 1;
-      float s[8];
+      const int qv = T * QVT + col / NBK;
+      const float4 pa = *reinterpret_cast<const float4*>(&s_p[wave][qv][4 * grp]);
+      const float4 pb = *reinterpret_cast<const float4*>(&s_p[wave][qv][16 + 4 * grp]);
+      const float pk[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+      float w[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int p = p0 + 16 * (k / 4) + 4 * grp + k % 4;
-        const bool valid = p < nk && p >= P.n_sink;
-        s[k] = valid ? sc[k / 4][T][k % 4] : -INFINITY;
-      }
-      float mx = s[0];
-#pragma unroll
-      for (int k = 1; k < 8; ++k) mx = fmaxf(mx, s[k]);
-      const float mn = fmaxf(M[T], col_max(mx));
-      const float alpha = first ? 0.0f : fast_exp2(M[T] - mn);
-      M[T] = mn;
-      float w[8], ls = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float pk = fast_exp2(s[k] - mn);
-        ls += pk;
-        // masked slots weigh exactly 0 (their stale V scales may be anything)
-        w[k] = s[k] != -INFINITY ? pk * b.vs[k] : 0.0f;
-      }
-      l[T] = first ? ls : fmaf(l[T], alpha, ls);
+      for (int k = 0; k < 8; ++k) w[k] = pk[k] >= 0.0f ? pk[k] * b.vs[k] : 0.0f;
       uint4 aw[3];
       split3(w, aw);
-      // the row's (query's) rescale factor, from the QK^T lane of that column
+      // the rescale of output rows 4 grp + i: query T QVT + (4 grp + i) / NBK
       if (!first) {
         if constexpr (NBK == 4) {
-          const float ar = __builtin_bit_cast(
-              float, __builtin_amdgcn_ds_bpermute(4 * (4 * grp), __builtin_bit_cast(int, alpha)));
+          const float ar = s_al[wave][T * QVT + grp];
 #pragma unroll
           for (int t = 0; t < NTV; ++t) o[T][t][t / 2] *= ar;
         } else {
-          const float a0 = __builtin_bit_cast(
-              float, __builtin_amdgcn_ds_bpermute(4 * (4 * grp), __builtin_bit_cast(int, alpha)));
-          const float a1 = __builtin_bit_cast(
-              float, __builtin_amdgcn_ds_bpermute(4 * (4 * grp + 2), __builtin_bit_cast(int, alpha)));
+          const float a0 = s_al[wave][T * QVT + 2 * grp];
+          const float a1 = s_al[wave][T * QVT + 2 * grp + 1];
 #pragma unroll
           for (int t = 0; t < NTV; ++t) {
             o[T][t][t / 2] *= a0;
@@ -531,7 +630,6 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
           }
         }
       }
-      // ---- PV: the chunk's V tiles against the three weight parts
 #pragma unroll
       for (int t = 0; t < NTV; ++t) {
         const uint4 vw = b.v[t / 2];
@@ -571,13 +669,16 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   // is query (4*grp + i) / NBK at block (4*grp + i) % NBK; kept when that is
   // the tile's block t / 2). A wave without a chunk writes (kMinit, 0, 0).
 #pragma unroll
-  for (int T = 0; T < NT; ++T) {
-    const float lt = col_sum(l[T]);
-    const int qv = T * QVT + col / NBK;
-    if (grp == 0 && col % NBK == 0 && qv < NQ) {
-      s_ml[wave][qv][0] = M[T];
+  for (int T2 = 0; T2 < NT2; ++T2) {
+    const float lt = row16_sum(l[T2]);
+    const int qv = 4 * T2 + grp;
+    if (col == 0 && qv < NQ) {
+      s_ml[wave][qv][0] = M[T2];
       s_ml[wave][qv][1] = lt;
     }
+  }
+#pragma unroll
+  for (int T = 0; T < NT; ++T) {
 #pragma unroll
     for (int t = 0; t < NTV; ++t)
 #pragma unroll
