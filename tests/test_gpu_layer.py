@@ -309,3 +309,103 @@ def test_decode_token_captured_after_setup(torch, layout):
         assert np.array_equal(got, want), f"{layout} replay {rep}"
     del graph, keep
     g.close()
+
+
+def real_block(rng, dim, ff, nh, nkv, hd, wt):
+    """One block at a real model's dims, every matvec's gain about 0.5 (weight
+    std 0.5 / sqrt(n_in)); Q8_0 codes uniform in [-127, 127] with block
+    scales of that spread."""
+    from test_oracle_layer import q8_blocks
+
+    def mat(o, i):
+        std = 0.5 / np.sqrt(i)
+        if wt == W_F16:
+            return (rng.standard_normal((o, i), dtype=np.float32) * std).astype(np.float16).view(
+                np.uint16)
+        nb = i // 32
+        vals = rng.integers(-127, 128, (o, nb, 32), dtype=np.int8)
+        sc = rng.uniform(0.5, 1.5, (o, nb)).astype(np.float32) * np.float32(std / 73.0)
+        return q8_blocks(vals, sc)
+    qn, kvn = nh * hd, nkv * hd
+    return {"attn_norm": (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32),
+            "ffn_norm": (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32),
+            "w": [mat(qn, dim), mat(kvn, dim), mat(kvn, dim), mat(dim, qn), mat(ff, dim),
+                  mat(ff, dim), mat(dim, ff)],
+            "wtype": [wt] * 7, "bq": None, "bk": None, "bv": None}
+
+
+@pytest.mark.parametrize("wt", [W_F16, W_Q8_0])
+def test_decode_token_llama32_3b_blocks(torch, wt):
+    """Two Llama-3.2-3B blocks (dim 3072, ff 8192, 24 q / 8 kv heads, hd 128),
+    four tokens through dbi_decode_token_async against the oracle's
+    decode_layer. At these dims the Q8_0 blocks run the fused launches: the
+    3-segment q/k/v matvec (3072 + 1024 + 1024 rows) and the gate/up pair
+    with silu * up over multi-chunk rows (8192 inputs of the down projection,
+    3072 of gate/up).
+
+    f16: |a - b| <= 1e-5 + 1e-4 |b|, the float bar (no activation is
+    quantized; only the order of the sums differs).
+    Q8_0: every activation row is quantized to Q8_0 before its matvec, and a
+    value within a rounding of a code boundary can take the other code on
+    the device. The bar is the measured size of such a flip at this shape:
+    the test moves one element of the layer-0 input by two codes' width in
+    the oracle and takes the largest output change that causes as the size
+    of a flip, and requires the device within 4x that plus the float bar.
+    Measured on MI355X: worst |device - oracle| 5.5e-3 over the four tokens
+    (f16: 0 beyond the float bar), one such perturbation 1.2e-2. A wiring
+    error (wrong segment, norm or gate/up order) moves the outputs by O(|x|)
+    and fails by orders of magnitude."""
+    dim, ff, nh, nkv, hd, L_, eps = 3072, 8192, 24, 8, 128, 2, 1e-5
+    rng = np.random.default_rng(3000 + wt)
+    lws = [real_block(rng, dim, ff, nh, nkv, hd, wt) for _ in range(L_)]
+    cap = 8
+    g = HipKV(L_, cap, nkv, hd, rope_theta=5e5)
+    o = pyoracle.OracleKV(L_, cap, nkv, hd, rope_theta=5e5)
+    keep = bind(torch, g, lws, dims=(dim, ff, nh))
+    g.set_stream(torch.cuda.current_stream().cuda_stream)
+    worst = 0.0
+    flip = None
+    for pos in range(4):
+        x = normal(3100 + pos, dim)
+        xt = dev(torch, x)
+        g.decode_token_async(xt.data_ptr(), pos)
+        torch.cuda.synchronize()
+        got = xt.cpu().numpy().astype(np.float64)
+        want = x.copy()
+        for layer in range(L_):
+            want = o.decode_layer(layer, want, pos, lws[layer], dim, ff, nh, eps, n_threads=8)
+        o.mark_position(pos)
+        want = want.astype(np.float64)
+        fbar = 1e-5 + 1e-4 * np.abs(want)
+        err = np.abs(got - want)
+        if wt == W_F16:
+            assert np.all(err <= fbar), f"f16 pos {pos}: worst {float((err - fbar).max()):.3e}"
+            worst = max(worst, float(err.max()))
+            continue
+        if flip is None:
+            # the output change of one activation code flip at this shape: the
+            # same token on a twin cache, with one element of the residual row
+            # moved so that its code in the layer-0 q/k/v input changes
+            t = pyoracle.OracleKV(L_, cap, nkv, hd, rope_theta=5e5)
+            xf = x.copy()
+            xf[7] += np.float32(2.0) * np.abs(x).max() / 127.0
+            yf = xf.copy()
+            for layer in range(L_):
+                yf = t.decode_layer(layer, yf, pos, lws[layer], dim, ff, nh, eps, n_threads=8)
+            t.close()
+            yb = x.copy()
+            t2 = pyoracle.OracleKV(L_, cap, nkv, hd, rope_theta=5e5)
+            for layer in range(L_):
+                yb = t2.decode_layer(layer, yb, pos, lws[layer], dim, ff, nh, eps, n_threads=8)
+            t2.close()
+            flip = float(np.abs(yf.astype(np.float64) - yb - (xf - x)).max())
+            assert flip > 0.0
+        bound = fbar + 4.0 * flip
+        assert np.all(err <= bound), (f"Q8_0 pos {pos}: worst {float(err.max()):.3e}, "
+                                      f"flip scale {flip:.3e}")
+        worst = max(worst, float(err.max()))
+    print(f"wt {wt}: worst |device - oracle| {worst:.3e}, one-code flip moves the output by "
+          f"{flip if flip is not None else 0.0:.3e}")
+    del keep
+    g.close()
+    o.close()
