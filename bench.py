@@ -129,6 +129,19 @@ def eager_kernel_us(torch, kv, q, out, scale, reps: int) -> float:
     return 1000.0 * statistics.median(a.elapsed_time(b) for a, b in pairs)
 
 
+def kernel_name(name: str, splits: int) -> str:
+    """The decode kernel instance a call at POS runs (attention.hip's plan:
+    chunks of 32 positions for int8, 16 for fp32, split over 8 waves)."""
+    G = NH // NKV
+    chunk = 32 if name == "int8" else 16
+    per_split = -(-(-(-CTX // chunk)) // splits)
+    per_wave = -(-per_split // 8)
+    cpw = 1 if per_wave <= 1 else 2 if per_wave <= 2 else 4 if per_wave <= 4 else 0
+    if name == "int8":
+        return f"attn_i8_kernel<{HD},{G},false,{cpw},1>"
+    return f"attn_kernel<{HD},{G},0,false,{cpw}>"
+
+
 def measure(torch, HipKV, code, name, K, V, q, args, scale):
     kv = build_cache(torch, HipKV, code, K, V)
     out = torch.empty(L, NH * HD, device="cuda")
@@ -156,6 +169,7 @@ def measure(torch, HipKV, code, name, K, V, q, args, scale):
     kv.set_stream(torch.cuda.current_stream().cuda_stream)
     res["attn_us_events"] = eager_kernel_us(torch, kv, q, out, scale, max(2, args.steps // 20))
     res["attn_bytes"] = attn_bytes(name)
+    res["kernel"] = kernel_name(name, kv.splits(POS, 1, NH))
     kv.close()
     del g_full, g_attn
     torch.cuda.synchronize()
@@ -784,6 +798,10 @@ def main():
 
     dom_us = i8["attn_us_graph"]
     achieved = i8["attn_bytes"] / (dom_us * 1e-6) / 1e9
+    # the same kernel in the fused step that `value` times (append inside the
+    # launch): its fraction with the attention's algorithmic bytes
+    fused_us = i8["us_per_token_layer"]
+    achieved_fused = i8["attn_bytes"] / (fused_us * 1e-6) / 1e9
     line = {
         "metric": METRIC,
         "value": round(i8["step_gbs"], 2),
@@ -818,12 +836,16 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_kernel<hd 128, gqa 3, int8 dense> "
-                      "(one decode-attention call)",
+            "kernel": i8["kernel"] + " (one decode-attention call, attention only)",
             "achieved": round(achieved, 2),
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_GBS, 4),
+            "fused_step": {"kernel": i8["kernel"] + " with the append inside (what `value` "
+                                                   "times)",
+                           "us_per_launch": round(fused_us, 3),
+                           "achieved": round(achieved_fused, 2),
+                           "frac": round(achieved_fused / PEAK_GBS, 4)},
             "traffic": _profiled_traffic(),
             "traffic_source": PROFILE,
             "bytes_per_launch": i8["attn_bytes"],

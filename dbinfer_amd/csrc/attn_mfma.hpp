@@ -357,10 +357,6 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     for (int s = 0; s < 8; ++s)
       b.vs[s] = load_b32(rvs, ((16 * (s / 4) + 4 * grp + s % 4) * NB + col % NBK) * 4, p0 * NB * 4);
   };
-  auto issue = [&](Buf& b, int ch) {
-    issue_k(b, ch);
-    issue_v(b, ch);
-  };
 
   // ---- q * scale * log2(e) of this lane's 8 channels of query T*QVT + qvl
   // (raw projections: bias, then the fp64 rope, as the producer computes
@@ -405,7 +401,16 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   __builtin_amdgcn_sched_barrier(0);
   const int ch0 = split * P.chunks_per_split + wave;  // chunk t of this wave: ch0 + t * 8
   Buf RA;
-  issue(RA, ch0);
+  // every wave's K half of its first chunk goes out before any V half: a
+  // CU's loads are served roughly in issue order, so the waves that issue
+  // last would otherwise get their whole chunk last and do all of its math
+  // after the stream; this way all K arrives in the first part of the
+  // stream, QK^T and the softmax overlap the V half, and only PV follows it
+  issue_k(RA, ch0);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  issue_v(RA, ch0);
   __builtin_amdgcn_sched_barrier(0);
   if (app_share) App::requant_share(A, wave, lane, app_knew, app_raw, s_kg);
 #pragma unroll
