@@ -24,7 +24,8 @@
 //    V layout stores each lane's 8 positions in that order. No LDS transpose.
 //  - PV: A = weight * V block scale in three bf16 parts, B = the V codes of a
 //    16-channel tile; row (query, block) is kept for the tiles of its block.
-//  - Records, merge, fused append and the fp32 sinks as attn_kernel.
+//  - Records, merge and fused append as attn_kernel; the fp32 sinks by wave 0
+//    of split 0, their loads issued at entry with q.
 #pragma once
 
 #include "attn_kernel.hpp"
@@ -335,27 +336,30 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   auto chunk_p0 = [&](int ch) {
     return __builtin_amdgcn_readfirstlane(ch < c_end ? ch * CHUNK : P.capg);
   };
+  // Scales go out before codes: loads return in issue order, so the q~
+  // digits (q * the group's channel scales) and the PV weights (p * the V
+  // block scales) are built while the chunk's codes are still arriving.
   auto issue_k = [&](Buf& b, int ch) {
     const int p0 = chunk_p0(ch);
     const int base = p0 * HD;
+    const int so = (p0 / kKGroup) * HD * 4;
+    b.ks[0] = load_b128(rks, 32 * c8, so);
+    b.ks[1] = load_b128(rks, 32 * c8 + 16, so);
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int jp = 0; jp < KL; ++jp)
         b.k[h][jp] = __builtin_bit_cast(uint4, stream_b128(rk, lane * 16, base + (h * KL + jp) * 1024));
-    const int so = (p0 / kKGroup) * HD * 4;
-    b.ks[0] = load_b128(rks, 32 * c8, so);
-    b.ks[1] = load_b128(rks, 32 * c8 + 16, so);
   };
   auto issue_v = [&](Buf& b, int ch) {
     const int p0 = chunk_p0(ch);
     const int base = p0 * HD;
 #pragma unroll
-    for (int tp = 0; tp < VL; ++tp)
-      b.v[tp] = __builtin_bit_cast(uint4, stream_b128(rv, lane * 16, base + tp * 1024));
-#pragma unroll
     for (int s = 0; s < 8; ++s)
       b.vs[s] = load_b32(rvs, ((16 * (s / 4) + 4 * grp + s % 4) * NB + col % NBK) * 4, p0 * NB * 4);
+#pragma unroll
+    for (int tp = 0; tp < VL; ++tp)
+      b.v[tp] = __builtin_bit_cast(uint4, stream_b128(rv, lane * 16, base + tp * 1024));
   };
 
   // ---- q * scale * log2(e) of this lane's 8 channels of query T*QVT + qvl
@@ -398,6 +402,57 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   typename App::RowIn app_in{};
   if (app_share) App::load_share(A, kh, wave, lane, app_knew);
   if (app_owner) App::load_row(A, kh, lane, app_in);
+  // the fp32 sinks' K and V rows (wave 0 of split 0): their loads go out
+  // with q, ahead of the stream, and their scores are taken before the
+  // wave's chunk, so attending them after the stream waits on no load. A
+  // fused step's own sink row comes from the step's inputs.
+  constexpr int SB = 4;  // sinks taken at entry (further ones after the stream)
+  const int ns = min(P.n_sink, nkeys);  // sinks of the last row (a row r sees pos0 + r + 1 keys)
+  const bool sink_wave = split == 0 && wave == 0 && ns > 0;  // wave-uniform
+  const bool fresh_sink = kFuse && A.slot >= 0 && A.pos < P.n_sink;
+  auto sink_rows = [&](int p, float (&kx)[8], float (&vx)[8]) {
+    const float* ksb = P.ksink + static_cast<size_t>(kh) * P.n_sink * HD;
+    const float* vsb = P.vsink + static_cast<size_t>(kh) * P.n_sink * HD;
+    const float4* ks4 = reinterpret_cast<const float4*>(ksb + p * HD + 8 * c8);
+    const float4* vs4 = reinterpret_cast<const float4*>(vsb + p * HD + 8 * c8);
+    const float4 k0 = ks4[0], k1 = ks4[1], v0 = vs4[0], v1 = vs4[1];
+    kx[0] = k0.x; kx[1] = k0.y; kx[2] = k0.z; kx[3] = k0.w;
+    kx[4] = k1.x; kx[5] = k1.y; kx[6] = k1.z; kx[7] = k1.w;
+    vx[0] = v0.x; vx[1] = v0.y; vx[2] = v0.z; vx[3] = v0.w;
+    vx[4] = v1.x; vx[5] = v1.y; vx[6] = v1.z; vx[7] = v1.w;
+    if (fresh_sink && p == A.pos) {  // uniform
+      const float* kin = A.k + kh * HD;
+      const float* vin = A.v + kh * HD;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = 8 * c8 + e;
+        if (PROD && A.prod) {
+          kx[e] = produced<HD>(kin, A.kb != nullptr ? A.kb + kh * HD : nullptr, A.kcs, d);
+          vx[e] = produced<HD>(vin, A.vb != nullptr ? A.vb + kh * HD : nullptr, nullptr, d);
+        } else {
+          kx[e] = kin[d];
+          vx[e] = vin[d];
+        }
+      }
+    }
+  };
+  // a sink's score for this lane's query: q (scaled) . k over the LPQ lanes
+  // of the query (hd 128: a 16-lane row); -inf past the row's sinks
+  auto sink_dot = [&](const float (&qv8)[8], const float (&kx)[8], bool seen) {
+    float sdot = qv8[0] * kx[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) sdot += qv8[e] * kx[e];
+    if constexpr (LPQ == 16) sdot += dpp<kX8>(sdot);
+    sdot += dpp<kX7>(sdot);
+    sdot += dpp<kX2>(sdot);
+    sdot += dpp<kX1>(sdot);
+    return seen ? sdot : -INFINITY;
+  };
+  float skx[SB][8], svx[SB][8];
+  if (sink_wave) {
+#pragma unroll
+    for (int u = 0; u < SB; ++u) sink_rows(min(u, ns - 1), skx[u], svx[u]);
+  }
   __builtin_amdgcn_sched_barrier(0);
   const int ch0 = split * P.chunks_per_split + wave;  // chunk t of this wave: ch0 + t * 8
   Buf RA;
@@ -417,6 +472,16 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   for (int T = 0; T < NT; ++T)
 #pragma unroll
     for (int e = 0; e < 8; ++e) qs[T][e] = T * QVT + qvl < nqv ? qs[T][e] * P.qscale : 0.0f;
+  float ssd[NT][SB];  // the first SB sinks' scores
+  if (sink_wave) {
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const int qv = T * QVT + qvl;
+      const int nsq = min(P.n_sink, P.pos0 + row0 + (qv < nqv ? qv / G : 0) + 1);
+#pragma unroll
+      for (int u = 0; u < SB; ++u) ssd[T][u] = sink_dot(qs[T], skx[u], u < nsq);
+    }
+  }
 
   // running state: per QK^T row tile, the max and the lane's partial sum of
   // the query of its lane group (query 4 T2 + grp), and the PV accumulators
@@ -695,17 +760,11 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
 
   // ---- the fp32 sinks (positions < n_sink, model.cpp:612-626), folded into
   // wave 0's record of split 0 (q~ layout: lane = query qvl, channels
-  // 8*c8..); a fused step's own sink row comes from the step's inputs
-  const int ns = min(P.n_sink, nkeys);  // sinks of the last row (a row r sees pos0 + r + 1 keys)
-  if (split == 0 && wave == 0 && ns > 0) {  // wave-uniform
+  // 8*c8..): the first SB from the scores and V rows taken at entry
+  if (sink_wave) {  // wave-uniform
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const float* ksb = P.ksink + static_cast<size_t>(kh) * P.n_sink * HD;
-    const float* vsb = P.vsink + static_cast<size_t>(kh) * P.n_sink * HD;
-    const bool fresh_sink = kFuse && A.slot >= 0 && A.pos < P.n_sink;
-    const float* kin = fresh_sink ? A.k + kh * HD : nullptr;
-    const float* vin = fresh_sink ? A.v + kh * HD : nullptr;
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
       const int qv = T * QVT + qvl;
@@ -714,54 +773,25 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
       float Ms = real ? s_ml[0][qv][0] : kMinit, Ls = real ? s_ml[0][qv][1] : 0.0f, os[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) os[e] = real ? s_o[0][qv][8 * c8 + e] : 0.0f;
-      // blocks of SB sinks, every load of a block in flight at once
-      constexpr int SB = 4;
-      for (int pb = 0; pb < ns; pb += SB) {
+      auto update = [&](float sdot, const float (&vx)[8]) {
+        const float mn = fmaxf(Ms, sdot);
+        const float al = fast_exp2(Ms - mn), pw = fast_exp2(sdot - mn);
+        Ms = mn;
+        Ls = fmaf(Ls, al, pw);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) os[e] = fmaf(os[e], al, pw * vx[e]);
+      };
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+        if (u < ns) update(ssd[T][u], svx[u]);  // uniform
+      // further blocks of SB sinks, every load of a block in flight at once
+      for (int pb = SB; pb < ns; pb += SB) {
         float kx[SB][8], vx[SB][8];
 #pragma unroll
-        for (int u = 0; u < SB; ++u) {
-          const int p = min(pb + u, ns - 1);
-          const float4* ks4 = reinterpret_cast<const float4*>(ksb + p * HD + 8 * c8);
-          const float4* vs4 = reinterpret_cast<const float4*>(vsb + p * HD + 8 * c8);
-          const float4 k0 = ks4[0], k1 = ks4[1], v0 = vs4[0], v1 = vs4[1];
-          kx[u][0] = k0.x; kx[u][1] = k0.y; kx[u][2] = k0.z; kx[u][3] = k0.w;
-          kx[u][4] = k1.x; kx[u][5] = k1.y; kx[u][6] = k1.z; kx[u][7] = k1.w;
-          vx[u][0] = v0.x; vx[u][1] = v0.y; vx[u][2] = v0.z; vx[u][3] = v0.w;
-          vx[u][4] = v1.x; vx[u][5] = v1.y; vx[u][6] = v1.z; vx[u][7] = v1.w;
-          if (fresh_sink && p == A.pos) {  // uniform
+        for (int u = 0; u < SB; ++u) sink_rows(min(pb + u, ns - 1), kx[u], vx[u]);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const int d = 8 * c8 + e;
-              if (PROD && A.prod) {
-                kx[u][e] = produced<HD>(kin, A.kb != nullptr ? A.kb + kh * HD : nullptr, A.kcs, d);
-                vx[u][e] = produced<HD>(vin, A.vb != nullptr ? A.vb + kh * HD : nullptr, nullptr, d);
-              } else {
-                kx[u][e] = kin[d];
-                vx[u][e] = vin[d];
-              }
-            }
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < SB; ++u) {
-          if (pb + u < ns) {  // uniform
-            float sdot = qs[T][0] * kx[u][0];
-#pragma unroll
-            for (int e = 1; e < 8; ++e) sdot += qs[T][e] * kx[u][e];
-            // sum over the LPQ lanes of the query (hd 128: a 16-lane row)
-            if constexpr (LPQ == 16) sdot += dpp<kX8>(sdot);
-            sdot += dpp<kX7>(sdot);
-            sdot += dpp<kX2>(sdot);
-            sdot += dpp<kX1>(sdot);
-            sdot = pb + u < nsq ? sdot : -INFINITY;
-            const float mn = fmaxf(Ms, sdot);
-            const float al = fast_exp2(Ms - mn), pw = fast_exp2(sdot - mn);
-            Ms = mn;
-            Ls = fmaf(Ls, al, pw);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) os[e] = fmaf(os[e], al, pw * vx[u][e]);
-          }
-        }
+        for (int u = 0; u < SB; ++u)
+          if (pb + u < ns) update(sink_dot(qs[T], kx[u], pb + u < nsq), vx[u]);  // uniform
       }
       if (real) {
 #pragma unroll
