@@ -61,11 +61,15 @@ Plan plan(const KvGeom& g, const AttnCall& c) {
   const int wpg = kWaves;
   // at least one chunk per wave; a short context may go down to one chunk
   // per two waves (more CUs share the stream, some waves idle) while that
-  // keeps the merge within 32 records (measured: 64 records cost the C4
-  // ring more than the wider spread gains)
+  // keeps one merging workgroup within 32 records, or within 64 where the
+  // merge is spread over several workgroups anyway (records beyond
+  // kOneMergerBytes at 64 splits; measured: 64 records read by one
+  // workgroup cost the C4 ring more than the wider spread gains)
+  const int rec_cap = 64 * G * g.hd * 4 > kOneMergerBytes && !rowsk ? 64 : 32;
   const int strict = (nchunks + wpg - 1) / wpg;
   const int relaxed = (nchunks + wpg / 2 - 1) / (wpg / 2);
-  const int max_by_chunks = strict > (relaxed < 32 ? relaxed : 32) ? strict : (relaxed < 32 ? relaxed : 32);
+  const int relaxed_c = relaxed < rec_cap ? relaxed : rec_cap;
+  const int max_by_chunks = strict > relaxed_c ? strict : relaxed_c;
   if (want > max_by_chunks) want = max_by_chunks;
   if (want > kMaxSplits) want = kMaxSplits;
   if (want < 1) want = 1;

@@ -503,10 +503,58 @@ __device__ __forceinline__ void merge_split(const AttnParams& P, int kh, int qro
     merge_head<HD, G, SINKS, kMaxSplits>(P, kh, qrow, g, lane);
 }
 
-template <int HD, int G>
-__device__ __forceinline__ void merge_last(const AttnParams& P, int kh, int qrow, int wave,
-                                           int lane) {
-  if (wave < G) merge_split<HD, G>(P, kh, qrow, wave, lane);
+// Re-reads of a counter before a waiting merger gives up (a bound only: the
+// arrival it waits for belongs to a workgroup that is already running and
+// waits on nothing).
+constexpr int kSpinLimit = 1 << 22;
+
+// Records a single merging workgroup reads before the merge is spread over
+// several: its CU fetches them at ~64 bytes per clock plus a round trip
+// (~1 us for C3's 3 heads x 32 records), while handing slices to other
+// workgroups costs a round trip of its own (measured slower at C3).
+constexpr int kOneMergerBytes = 96 << 10;
+
+// Split arrival and merge of the decode kernels, after this workgroup's
+// records have reached the coherence point; thread r < nr counts row
+// row0 + r. A (row, kv head) counter holds (epoch << 8) | arrivals. The
+// last D arrivals each merge one slice of the query heads (slice m: heads
+// m, m + D, ..): D = 1 unless the records exceed kOneMergerBytes (a C4 ring
+// call: 7 heads x 33 records), then D = min(G, nsplit), so the records are
+// read by D workgroups on D CUs. The last arrival moves the counter to the
+// next epoch (arrivals back to 0, with no wait) and merges its slice; the
+// other mergers wait until the epoch moves, which the last arrival does
+// right after its own count: every record was acknowledged before its
+// split was counted, so all of them are at the coherence point by then.
+template <int HD, int G, int NR>
+__device__ __forceinline__ void arrive_and_merge(const AttnParams& P, int kh, int row0, int nr,
+                                                 int wave, int lane, int (&s_slice)[NR]) {
+  const int D = P.nsplit * G * HD * 4 > kOneMergerBytes ? min(G, P.nsplit) : 1;
+  if (static_cast<int>(threadIdx.x) < nr) {
+    unsigned* cnt =
+        P.cnt + (static_cast<size_t>(row0 + threadIdx.x) * P.nkv + kh) * kCounterStride;
+    const unsigned before =
+        __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int a = static_cast<int>(before & 0xFFu);
+    const int slice = a - (P.nsplit - D);
+    if (a == P.nsplit - 1) {
+      (void)__hip_atomic_fetch_add(cnt, 256u - static_cast<unsigned>(P.nsplit), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    } else if (slice >= 0) {
+      const unsigned epoch = before >> 8;
+      for (int it = 0; it < kSpinLimit &&
+                       (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 8) == epoch;
+           ++it)
+        __builtin_amdgcn_s_sleep(1);
+    }
+    s_slice[threadIdx.x] = slice;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int slice = r < nr ? s_slice[r] : -1;  // uniform
+    const int g = slice + wave * D;
+    if (slice >= 0 && g < G) merge_split<HD, G>(P, kh, row0 + r, g, lane);
+  }
 }
 
 
@@ -893,7 +941,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
 
   __shared__ float s_o[kWaves][GW][HD];
   __shared__ float s_ml[kWaves][GW][2];
-  __shared__ int s_last;
+  __shared__ int s_slice[1];
   __shared__ __align__(16) float s_w[kWaves][CHUNK][GP];
   __shared__ __align__(16) AppStage s_stage[C::NHG];
   // dense int8 fused step: each head group's copy of the group's raw K rows
@@ -1378,17 +1426,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnParams P, cons
     // this thread's record stores have reached the coherence point
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0) {
-      unsigned* cnt = P.cnt + (static_cast<size_t>(qrow) * P.nkv + kh) * kCounterStride;
-      const unsigned before =
-          __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = before == static_cast<unsigned>(P.nsplit - 1);
-      if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = last;
-    }
-    __syncthreads();
-    // (wave g merges head g)
-    if (s_last) merge_last<HD, G>(P, kh, qrow, wave, lane);
+    arrive_and_merge<HD, G, 1>(P, kh, qrow, 1, wave, lane, s_slice);
   }
   if (app_owner && g0 == 0) App::flush(A, kh, lane, s_app, nullptr, app_row);
 }

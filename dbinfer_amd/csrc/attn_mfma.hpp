@@ -281,7 +281,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   constexpr bool kFuse = NR == 1;  // the fused decode step (one row) only
   __shared__ float s_o[kWaves][NQ][HD];
   __shared__ float s_ml[kWaves][NQ][2];
-  __shared__ int s_last[NR];
+  __shared__ int s_slice[NR];
   // q~ digits: the int8 QK^T A operand of row tile T2, k-step jp, lane
   // group g, row m (lane m + 16 g reads [T2][jp][g][m]: 16 consecutive
   // bytes per lane, no bank conflicts)
@@ -809,19 +809,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     // this thread's record stores have reached the coherence point
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (static_cast<int>(threadIdx.x) < nr) {  // one arrival per row
-      const int qrow = row0 + threadIdx.x;
-      unsigned* cnt = P.cnt + (static_cast<size_t>(qrow) * P.nkv + kh) * kCounterStride;
-      const unsigned before =
-          __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = before == static_cast<unsigned>(P.nsplit - 1);
-      if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last[threadIdx.x] = last;
-    }
-    __syncthreads();
-    // the (row, head) merges this workgroup owns, one wave each
-    for (int pr = wave; pr < nqv; pr += kWaves)
-      if (s_last[pr / G]) merge_split<HD, G>(P, kh, row0 + pr / G, pr % G, lane);
+    arrive_and_merge<HD, G, NR>(P, kh, row0, nr, wave, lane, s_slice);
   }
   if (kFuse && app_owner)
     App::flush(A, kh, lane, s_stage, &s_kg, s_row, kKeepV ? app_v : nullptr);

@@ -1,7 +1,7 @@
 """Graph capture of the decode step (append + attention of every layer), as
 bench.py replays it: every replay, with eager work and synchronizations in
-between, must give the eager result bit for bit (the split-K counters reset
-themselves; no memset node is recorded)."""
+between, must give the eager result bit for bit (each launch leaves the
+split-K counters ready for the next; no memset node is recorded)."""
 import numpy as np
 import pytest
 

@@ -313,7 +313,7 @@ def test_chunk_rows(dtype, nh, nkv, hd, pos0, n, ns):
     got = g.attend_chunk(0, pos0, q, nh, scale_of(hd))
     want = o.attend_chunk(0, pos0, q, nh, scale_of(hd), n_threads=8)
     assert_close(got, want, what=f"rows dtype {dtype} pos0 {pos0} n {n} gqa {nh // nkv}")
-    # a second call on the same workspace (split counters back at zero)
+    # a second call on the same workspace (split counters at a new epoch)
     again = g.attend_chunk(0, pos0, q, nh, scale_of(hd))
     assert np.array_equal(again, got)
 
