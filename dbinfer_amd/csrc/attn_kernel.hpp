@@ -594,13 +594,14 @@ struct KGroupStage {
 // channels each, before their own chunk: their loads go out first, so the
 // shares are done by the time the owner (usually a later wave) reaches the
 // new row's chunk. They publish through an LDS counter that only the owners
-// wait on; no other wave waits.
+// wait on; no other wave waits. (Measured: all 8 waves sharing, or the 4
+// waves just before the owner, made the step slower.)
 //
-// Loads are LDS-direct (16 bytes per lane, no registers held): the new K
+// Loads are ordinary 16-byte vector loads into registers (the compiler's
+// load waits stay exact), written to LDS where they are consumed: the new K
 // and V rows into `row` ([0, HD) and [HD, 2 HD) of 256 floats; k_dev and
 // v_dev are 16-byte aligned) and a wave's channels of the group's 32 staged
-// raw rows into its `raw` share ([32][CPW]). The compiler does not track
-// these loads: the consumers wait for them explicitly.
+// raw rows into its `raw` share ([32][CPW]).
 template <int HD, int KIND, bool PROD>
 struct FusedAppend {
   static constexpr bool kInt8 = (KIND == kI8Dense || KIND == kI8Ring);
