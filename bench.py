@@ -251,16 +251,23 @@ CPU_LAYERS = 4
 PROFILE = "profiles/decode_c3_ctx8192_kernels.md"
 
 
-def _profiled_traffic():
-    """HBM bytes of one int8 decode-attention call from the committed rocprofv3
-    FETCH_SIZE/WRITE_SIZE passes (PMC counters cannot be read in-process)."""
+def _profiled(key):
+    """A figure of the committed rocprofv3 summary (PMC counters cannot be read
+    in-process): `key: value` lines of PROFILE."""
     try:
         for line in open(os.path.join(ROOT, PROFILE)):
-            if line.startswith("traffic_bytes_per_call_int8:"):
-                return int(line.split(":", 1)[1])
+            if line.startswith(key + ":"):
+                return float(line.split(":", 1)[1])
     except OSError:
         pass
     return None
+
+
+def _profiled_traffic():
+    """HBM bytes of one int8 decode-attention call from the FETCH_SIZE/WRITE_SIZE
+    passes of PROFILE."""
+    t = _profiled("traffic_bytes_per_call_int8")
+    return None if t is None else int(t)
 
 
 # The five benchmark configurations, one decode step (and, where the config has them, the
@@ -848,6 +855,13 @@ def main():
                            "frac": round(achieved_fused / PEAK_GBS, 4)},
             "traffic": _profiled_traffic(),
             "traffic_source": PROFILE,
+            # the traced duration of the profiled kernel beside the live one: a
+            # kernel changed since the profile shows as a disagreement
+            "traffic_profiled_us": _profiled("traced_attention_us_int8"),
+            "traffic_profile_agrees": (
+                None if _profiled("traced_attention_us_int8") is None else
+                abs(dom_us - _profiled("traced_attention_us_int8"))
+                <= 0.1 * _profiled("traced_attention_us_int8")),
             "bytes_per_launch": i8["attn_bytes"],
         },
         "cpu_baseline": None if args.no_cpu else cpu_baseline(args.cpu_seconds),
