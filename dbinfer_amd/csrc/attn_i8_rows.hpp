@@ -204,6 +204,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- online softmax per column, then the block weights (PV A operands)
+    float pk[NVT][8];
 #pragma unroll
     for (int T = 0; T < NVT; ++T) {
       // keys of this column's row (causal: row r attends [0, pos0 + r]); the
@@ -222,11 +223,11 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
       const float mn = fmaxf(M[T], col_max(mx));
       const float alpha = fast_exp2(M[T] - mn);
       M[T] = mn;
-      float pk[8], ls = 0.0f;
+      float ls = 0.0f;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        pk[k] = fast_exp2(s[k] - mn);
-        ls += pk[k];
+        pk[T][k] = fast_exp2(s[k] - mn);
+        ls += pk[T][k];
       }
       l[T] = fmaf(l[T], alpha, ls);
       // rescale of the output rows (queries 4 grp + i of this tile): the
@@ -238,24 +239,30 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
 #pragma unroll
         for (int t = 0; t < NTV; ++t) o[T][t][i] *= ar;
       }
-      // ---- PV per V block: w_b = p * vs[pos][b] (masked slots: p = 0, and
-      // outside the group's keys vs = 0), three parts, against the V codes of
-      // the block's two channel tiles
+    }
+    // ---- PV per V block: w_b = p * vs[pos][b] (masked slots: p = 0, and
+    // outside the group's keys vs = 0), three parts, against the V codes of
+    // the block's two channel tiles; each tile's codes are converted once
+    // and serve every vector tile
 #pragma unroll
-      for (int b = 0; b < NBK; ++b) {
+    for (int b = 0; b < NBK; ++b) {
+      uint4 aw[NVT][3];
+#pragma unroll
+      for (int T = 0; T < NVT; ++T) {
         float w[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) w[k] = pk[k] * vsc[k][b];
-        uint4 aw[3];
-        split3(w, aw);
+        for (int k = 0; k < 8; ++k) w[k] = pk[T][k] * vsc[k][b];
+        split3(w, aw[T]);
+      }
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const int t = 2 * b + tt;
-          const uint4 vw = vc[t / 2];
-          const bf16x8 bv = (t & 1) ? codes_bf16(vw.z, vw.w) : codes_bf16(vw.x, vw.y);
+      for (int tt = 0; tt < 2; ++tt) {
+        const int t = 2 * b + tt;
+        const uint4 vw = vc[t / 2];
+        const bf16x8 bv = (t & 1) ? codes_bf16(vw.z, vw.w) : codes_bf16(vw.x, vw.y);
 #pragma unroll
-          for (int a = 0; a < 3; ++a) o[T][t] = mfma(aw[a], bv, o[T][t]);
-        }
+        for (int T = 0; T < NVT; ++T)
+#pragma unroll
+          for (int a = 0; a < 3; ++a) o[T][t] = mfma(aw[T][a], bv, o[T][t]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
