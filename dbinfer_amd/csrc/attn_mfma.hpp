@@ -29,20 +29,10 @@
 #pragma once
 
 #include "attn_kernel.hpp"
+#include "bf16x3.hpp"
 
 namespace dbi {
 namespace {
-
-using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
-using f32x4 = float __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
-__device__ __forceinline__ float ffrom(uint32_t u) { return __builtin_bit_cast(float, u); }
-
-// the upper halves (bf16) of two fp32 bit patterns, a in the low half
-__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x07060302u);
-}
 
 // 8 signed int8 codes (bytes of lo, then hi) -> 8 bf16, exactly (|code| <=
 // 127 leaves the low 16 bits of its fp32 value zero)
@@ -58,26 +48,6 @@ __device__ __forceinline__ bf16x8 codes_bf16(uint32_t lo, uint32_t hi) {
   w.z = pack_hi(fbits(f[4]), fbits(f[5]));
   w.w = pack_hi(fbits(f[6]), fbits(f[7]));
   return __builtin_bit_cast(bf16x8, w);
-}
-
-// x = hi + mid + lo exactly, each part a bf16 (truncations: the residual of
-// an 8-bit truncation of a 24-bit significand keeps at most 16 bits, that of
-// the second at most 8); parts packed 8 per uint4
-__device__ __forceinline__ void split3(const float (&x)[8], uint4 (&part)[3]) {
-  uint32_t h[8], m[8], l[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    h[e] = fbits(x[e]) & 0xFFFF0000u;
-    const float r1 = x[e] - ffrom(h[e]);
-    m[e] = fbits(r1) & 0xFFFF0000u;
-    l[e] = fbits(r1 - ffrom(m[e]));
-  }
-  part[0] = make_uint4(pack_hi(h[0], h[1]), pack_hi(h[2], h[3]), pack_hi(h[4], h[5]),
-                       pack_hi(h[6], h[7]));
-  part[1] = make_uint4(pack_hi(m[0], m[1]), pack_hi(m[2], m[3]), pack_hi(m[4], m[5]),
-                       pack_hi(m[6], m[7]));
-  part[2] = make_uint4(pack_hi(l[0], l[1]), pack_hi(l[2], l[3]), pack_hi(l[4], l[5]),
-                       pack_hi(l[6], l[7]));
 }
 
 __device__ __forceinline__ f32x4 mfma(const uint4& a, const bf16x8& b, const f32x4& c) {

@@ -3,36 +3,35 @@
 // chunk at pos0 attending keys [0, pos0 + c], for chunks long enough to
 // make QK^T and PV real matrix products (the prefill chunks of config 2).
 //
-// Design (CDNA4 v_mfma_f32_16x16x4_f32, fp32 in and out, so the result stays
-// within the fp32 tolerance of the CPU path):
+// Design (CDNA4 v_mfma_f32_16x16x32_bf16 over exact three-part splits of the
+// fp32 operands, bf16x3.hpp, so the result stays within the fp32 tolerance
+// of the CPU path):
 //  - A workgroup of 4 waves owns 64 query vectors of one kv head: each wave
 //    16 vectors (16/G rows x the G query heads sharing the kv head). The
-//    workgroup walks its keys in stages of SK keys: the stage's K and V are
-//    copied into LDS once, by LDS-direct loads (no registers), and every
-//    wave reads its MFMA operands from there. Stages are double-buffered:
-//    the next stage's copy is in flight while the current one computes.
+//    workgroup walks its keys in stages of 32 (one pair of 16-key tiles).
+//  - Staging: the stage's fp32 K and V are loaded into registers while the
+//    previous stage computes, split once per workgroup into hi, mid and lo
+//    bf16 parts and written to LDS in the matrix cores' operand layout:
+//    every operand read of the waves is one 16-byte LDS load of 8 bf16, and
+//    no wave converts K or V itself. Waves 0-1 stage K, waves 2-3 V.
 //  - Keys can be split over KS workgroups (grid z) to fill the GPU on short
 //    chunks; a split writes its unnormalized (o, m, l) and prefill_merge
 //    combines them.
-//  - S^T = K Q^T: A = K (16 keys x 4 dims), B = Q^T (4 dims x 16 vectors),
-//    one instruction per 4 dims, in four independent accumulator chains.
-//    Dims are permuted per lane group so that every lane's operands are 16
-//    contiguous floats: in instruction (h, s), k-index kk stands for dim
-//    16 kk + 64 h + s. The result holds S[vector l % 16][key 4 (l / 16) + v]
-//    in lane l.
-//  - O^T += V^T P^T: A = V^T (16 dims x 4 keys), B = P^T straight from the S
-//    registers (instruction j uses key 4 kk + j, the score lane l already
-//    holds). Output tile tt row i stands for dim (hd/16) i + tt, so a lane's
-//    V operands are hd/16 contiguous floats per key and its output is hd/4
-//    contiguous floats of its vector.
+//  - S^T = K Q^T: A = K (16 keys x 32 dims), B = Q^T (32 dims x 16 vectors),
+//    six bf16 products per 32-dim step. In k-step ks = 2 h + hf, lane group
+//    gq's k-index 8 gq + e stands for dim 16 gq + 64 h + 8 hf + e. The
+//    result holds S[vector l % 16][key 4 (l / 16) + v] in lane l.
+//  - O^T += V^T P^T over the pair's 32 keys: B = P^T straight from the
+//    score registers (k-index 8 gq + e: key 4 gq + e of the first tile for
+//    e < 4, key 4 gq + e - 4 of the second otherwise), A = V^T in the same
+//    key order. Output tile tt row i stands for dim (hd/16) i + tt, so a
+//    lane's output is hd/4 contiguous floats of its vector.
 //  - Online softmax per vector (= per lane % 16); the four lane groups
-//    holding one vector combine through two xor shuffles.
-//  - LDS holds the stage in the cache's own granule layout (kv_internal.hpp),
-//    so the copy is a straight contiguous one and the operand offsets are
-//    the layout's offsets relative to the stage.
+//    holding one vector combine through two lane swaps.
 #include <cmath>
 #include <type_traits>
 
+#include "bf16x3.hpp"
 #include "kv_internal.hpp"
 
 namespace dbi {
@@ -55,40 +54,9 @@ struct PrefillParams {
   float qscale;     // scale * log2(e)
 };
 
-// One 16-byte LDS-direct copy per lane: lane l reads src + 16 voff bytes
-// (src wave-uniform) and lands at LDS byte address dst + 16 l (dst
-// wave-uniform, through m0). Issued as asm, so the compiler does not track
-// the copy: it would otherwise wait for every copy in flight (vmcnt 0)
-// before each LDS read, the next stage's included, since it cannot tell the
-// copy's destination from the buffer being read. Stage arrival is waited for
-// explicitly (s_waitcnt vmcnt, then the barrier).
-// m0 is saved and restored around the copy (the register is reserved to
-// the compiler).
-__device__ __forceinline__ void lds_copy16(const float* src, uint32_t voff, uint32_t dst) {
-  uint32_t keep;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, %1\n\ts_mov_b32 m0, %0"
-      : "=&s"(keep)
-      : "s"(src), "v"(voff), "s"(dst)
-      : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const float* p) {
-  return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const float*)p));
-}
-
-// Workgroup barrier that waits for this wave's LDS accesses only. The
-// compiler's __syncthreads also waits for every vector memory load (vmcnt 0)
-// when LDS-direct copies are in flight, which would drain the prefetched
-// stages at every stage; stage arrival is waited for explicitly instead.
+// Workgroup barrier after this wave's LDS accesses have completed.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-__device__ __forceinline__ float4 lds4(const float* p) {
-  return *reinterpret_cast<const float4*>(p);
 }
 
 // Lane-group exchanges of the softmax through the gfx950 permlane swaps
@@ -118,54 +86,40 @@ __device__ __forceinline__ float xsum32(float x) {
   return a + b;
 }
 
-// Stage buffers hold the cache's granule layout with its 16-byte units
-// permuted inside every aligned run of 16 units: unit u sits at swz_u(u) =
-// u ^ m(u), m's bits 0-2 the parities of u >> 3 under the masks 62, 53, 15
-// and its bit 3 the parity of u >> 4 under 54. The masks were picked by
-// exhaustive check of every K and V operand read of both head dims: each
-// read (64 lanes x 16 bytes) then hits distinct banks in every group of 8
-// lanes (32 banks) and of 16 lanes (64 banks). The map is linear over GF(2),
-// so an offset that is a lane part XOR a constant permutes as the XOR of the
-// two permuted parts (the constant one folds at compile time).
-__host__ __device__ constexpr int parity(int x) { return __builtin_popcount(x) & 1; }
-__host__ __device__ constexpr int swz_u(int u) {
-  return u ^ (parity(62 & (u >> 3)) | (parity(53 & (u >> 3)) << 1) |
-              (parity(15 & (u >> 3)) << 2) | (parity(54 & (u >> 4)) << 3));
-}
-// the unit that swz_u places at s
-__host__ __device__ constexpr int swz_u_inv(int s) {
-  const int b3 = ((s >> 3) & 1) ^ parity(54 & (s >> 4));
-  const int u3 = (s & ~15) | (b3 << 3) | (s & 7);  // bits 3.. of the unit
-  return u3 ^ (parity(62 & (u3 >> 3)) | (parity(53 & (u3 >> 3)) << 1) |
-               (parity(15 & (u3 >> 3)) << 2));
-}
-static_assert(swz_u_inv(swz_u(777)) == 777 && swz_u(swz_u_inv(1000)) == 1000, "bijection");
-static_assert((swz_u(300 ^ 517) ^ swz_u(300)) == swz_u(517), "linear");
-
+// One stage in LDS: parts p = 0, 1, 2 (hi, mid, lo) of K, then of V, each a
+// plane of SK x HD bf16.
+//  - K plane: key k's dims 8 u .. 8 u + 7 are the 16-byte unit
+//    k * HD/8 + (u ^ kswz(k)). The swizzle puts the 8 (16) keys of one
+//    operand read's 8-lane (16-lane) group on distinct banks of 128 (256)
+//    bytes.
+//  - V plane: unit (j, s) = j * HD + s holds keys kv(j, e), e < 8, of dim
+//    vdim(s): kv(j, e) = 4 j + e for e < 4 and 16 + 4 j + e - 4 otherwise
+//    (the PV k-order of lane group j), vdim(s) = (HD/16) (s % 16) + s / 16
+//    (lane i of output tile tt reads s = 16 tt + i: 16 contiguous units).
 template <int HD>
 struct Stage {
-  static constexpr int SK = HD == 64 ? 64 : 32;                // keys per stage
-  static constexpr int FL = SK * HD;                           // floats of K (or V)
-  static constexpr int NDMA = FL * 4 / (kPThreads * 16);       // 16-byte copies per thread
+  static constexpr int SK = 32;                   // keys per stage
+  static constexpr int NBUF = HD == 64 ? 2 : 1;   // stage buffers (two workgroups per CU)
+  static constexpr int UPR = HD / 8;              // 16-byte units per key of a K part
+  static constexpr int PLANE = SK * HD * 2;       // bytes of one part of K or V
+  static constexpr int BYTES = 6 * PLANE;
+  static constexpr int NU = SK * HD / 1024;       // staging lane: K units, or V dims
 };
 
-// NBUF stage buffers: NBUF - 1 stage copies are in flight ahead of the one
-// being computed (2: two workgroups per CU share the CU's LDS).
-template <int HD, int G, int NBUF>
+template <int HD>
+__host__ __device__ constexpr int kswz(int key) {
+  return HD == 64 ? ((key & 7) ^ ((key >> 3) & 1)) : (key & 15);
+}
+
+template <int HD, int G>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(const PrefillParams P) {
   using S = Stage<HD>;
-  constexpr int SK = S::SK, FL = S::FL, NDMA = S::NDMA;
+  constexpr int SK = S::SK, NBUF = S::NBUF, UPR = S::UPR, PLANE = S::PLANE, NU = S::NU;
   constexpr int RPV = 16 / G;    // rows per wave
-  constexpr int NQ = HD / 4;     // QK instructions per 16-key tile
-  constexpr int NH = HD / 64;    // 16-dim runs per lane group
-  constexpr int VD = HD / 16;    // V dims per lane per key = output tiles
-  constexpr int NT = HD / 16;
-  // one array per stage buffer ([K, V][stage]), picked at compile time
-  __shared__ __align__(16) float s_b0[2 * FL];
-  __shared__ __align__(16) float s_b1[2 * FL];
-  __shared__ __align__(16) float s_b2[NBUF > 2 ? 2 * FL : 4];
-  __shared__ __align__(16) float s_b3[NBUF > 3 ? 2 * FL : 4];
-  auto bufp = [&](int b) -> float* { return b == 0 ? s_b0 : b == 1 ? s_b1 : b == 2 ? s_b2 : s_b3; };
+  constexpr int NH = HD / 64;    // 64-dim runs of a K row
+  constexpr int VD = HD / 16;    // output tiles
+  constexpr int NT = VD;
+  __shared__ __align__(16) char s_stage[NBUF * S::BYTES];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -189,103 +143,198 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const float* kbase = P.kf + head_el;
   const float* vbase = P.vf + head_el;
 
-  // stage copy: K then V, 16 bytes per lane per instruction; copy m of this
-  // wave fills units [m * kPThreads + 64 * wave, + 64) of the buffer, and
-  // lane l's slot holds unit swz_u_inv(slot) of the stage, from the same
-  // 1 KiB (the permutation stays within 16-unit runs)
-  uint32_t src_off[NDMA];
+  // ---- staging. K lanes (waves 0-1, t < 128): units n = t + 128 m, key
+  // n / UPR, dims 8 (n % UPR) .. + 7 (two float4 of the granule layout).
+  // V lanes (waves 2-3, t = 128 + 32 j + c): keys kv(j, e) x dims NU c ..
+  // NU c + NU - 1. The source offsets of stage 0 (stage st adds st * SK * HD:
+  // a stage is two whole granules).
+  const bool k_stager = wave < 2;  // uniform
+  uint32_t src[8];
+  uint32_t dst[NU];  // K: the unit's byte offset in a part plane; V: [0] of dim NU c
+  int vkey[8];
+  if (k_stager) {
 #pragma unroll
-  for (int m = 0; m < NDMA; ++m) {
-    const int u0 = m * kPThreads + 64 * wave;
-    src_off[m] = 16u * static_cast<uint32_t>(swz_u_inv(u0 + lane) - u0);
+    for (int m = 0; m < NU; ++m) {
+      const int n = static_cast<int>(threadIdx.x) + 128 * m;
+      const int key = n / UPR, u = n % UPR;
+      src[2 * m] = static_cast<uint32_t>(k_off_tiled(HD, false, key, 8 * u));
+      src[2 * m + 1] = static_cast<uint32_t>(k_off_tiled(HD, false, key, 8 * u + 4));
+      dst[m] = static_cast<uint32_t>((key * UPR + (u ^ kswz<HD>(key))) * 16);
+    }
+#pragma unroll
+    for (int e = 2 * NU; e < 8; ++e) src[e] = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vkey[e] = 0;
+  } else {
+    const int t = static_cast<int>(threadIdx.x) - 128;
+    const int j = t >> 5, c = t & 31;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      vkey[e] = e < 4 ? 4 * j + e : 16 + 4 * j + e - 4;
+      src[e] = static_cast<uint32_t>(v_off_tiled(HD, false, vkey[e], NU * c));
+    }
+    const int d = NU * c;  // dims d .. d + NU - 1: units s, s + 16, ..
+    dst[0] = static_cast<uint32_t>((j * HD + (d % VD) * 16 + d / VD) * 16);
+#pragma unroll
+    for (int m = 1; m < NU; ++m) dst[m] = dst[0] + 256u * m;
   }
-  auto copy_stage = [&](int st, float* dst) {
-    const size_t off = static_cast<size_t>(st) * FL;
-    const uint32_t d = lds_addr(dst);
+  // the loaded stage: K lanes hold unit m in r[2 m], r[2 m + 1]; V lanes key
+  // e's NU dims in r[e] (NU = 4) or in half e % 2 of r[e / 2] (NU = 2)
+  float4 r[2 * NU];
+  auto load_stage = [&](int st) {
+    const size_t so = static_cast<size_t>(st) * SK * HD;
+    if (k_stager) {
 #pragma unroll
-    for (int m = 0; m < NDMA; ++m) {
-      const int e = (m * kPThreads + wave * 64) * 4;  // this wave's KiB of the copy
-      lds_copy16(kbase + off + e, src_off[m], d + 4 * e);
-      lds_copy16(vbase + off + e, src_off[m], d + 4 * (FL + e));
+      for (int i = 0; i < 2 * NU; ++i)
+        r[i] = *reinterpret_cast<const float4*>(kbase + so + src[i]);
+    } else if constexpr (NU == 4) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = *reinterpret_cast<const float4*>(vbase + so + src[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float2 a = *reinterpret_cast<const float2*>(vbase + so + src[e]);
+        const float2 b = *reinterpret_cast<const float2*>(vbase + so + src[e + 1]);
+        r[e / 2] = make_float4(a.x, a.y, b.x, b.y);
+      }
     }
   };
-  // permuted operand units: a tile's K read (tile t, dims run h, step s4) is
-  // unit kb[h] ^ (t * 4 HD) ^ s4 and a V read (tile t, key j of the lane
-  // group, half u) is vb ^ (t * 4 HD) ^ unit(j, 0) ^ 64 u, the lane parts
-  // kb, vb those of tile 0 (no carries between the parts)
-  int skb[NH];
+  auto vdim = [&](int e, int m) -> float {
+    if constexpr (NU == 4) {
+      const float4 x = r[e];
+      return m == 0 ? x.x : m == 1 ? x.y : m == 2 ? x.z : x.w;
+    } else {
+      const float4 x = r[e / 2];
+      return (e & 1) == 0 ? (m == 0 ? x.x : x.y) : (m == 0 ? x.z : x.w);
+    }
+  };
+  // split and store; V of keys past the workgroup's last key is stored as 0
+  // (its weight is 0, and the cache past the chunk may hold anything)
+  auto store_stage = [&](int st, char* sb) {
+    if (k_stager) {
 #pragma unroll
-  for (int h = 0; h < NH; ++h)
-    skb[h] = swz_u(static_cast<int>(k_off_tiled(HD, false, vec, 16 * gq + 64 * h)) >> 2);
-  const int svb = swz_u(static_cast<int>(v_off_tiled(HD, false, 4 * gq, VD * vec)) >> 2);
-  auto k_at = [&](int t, int h, int s4) { return 4 * (skb[h] ^ swz_u(t * 4 * HD ^ s4)); };
-  auto v_at = [&](int t, int j, int u) {
-    return 4 * (svb ^ swz_u(t * 4 * HD ^ (static_cast<int>(v_off_tiled(HD, false, j, 0)) >> 2) ^
-                            (64 * u)));
+      for (int m = 0; m < NU; ++m) {
+        const float4 a = r[2 * m], b = r[2 * m + 1];
+        const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint4 part[3];
+        split3(x, part);
+#pragma unroll
+        for (int p = 0; p < 3; ++p) *reinterpret_cast<uint4*>(sb + p * PLANE + dst[m]) = part[p];
+      }
+    } else {
+      const bool tail = st * SK + SK - 1 > last_key;  // uniform
+#pragma unroll
+      for (int m = 0; m < NU; ++m) {
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float v = vdim(e, m);
+          x[e] = !tail || st * SK + vkey[e] <= last_key ? v : 0.0f;
+        }
+        uint4 part[3];
+        split3(x, part);
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+          *reinterpret_cast<uint4*>(sb + (3 + p) * PLANE + dst[m]) = part[p];
+      }
+    }
   };
 
-  // Q^T operands: dims 16 gq + 64 h + s, pre-scaled into the log2 domain
-  float qv[NQ];
+  // ---- operands. Q^T: dims 16 gq + 64 h + 8 hf + e of k-step 2 h + hf,
+  // pre-scaled into the log2 domain, in three bf16 parts
+  constexpr int KS = HD / 32;
+  uint4 qp[KS][3];
   {
-    const float* qp = P.q + (static_cast<size_t>(row) * P.n_heads + head) * HD + 16 * gq;
+    const float* qp_src = P.q + (static_cast<size_t>(row) * P.n_heads + head) * HD + 16 * gq;
 #pragma unroll
-    for (int h = 0; h < NH; ++h)
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const float4 t = *reinterpret_cast<const float4*>(qp + 64 * h + 4 * s4);
-        qv[16 * h + 4 * s4 + 0] = t.x * P.qscale;
-        qv[16 * h + 4 * s4 + 1] = t.y * P.qscale;
-        qv[16 * h + 4 * s4 + 2] = t.z * P.qscale;
-        qv[16 * h + 4 * s4 + 3] = t.w * P.qscale;
-      }
+    for (int ks = 0; ks < KS; ++ks) {
+      const float4 a = *reinterpret_cast<const float4*>(qp_src + 64 * (ks / 2) + 8 * (ks % 2));
+      const float4 b = *reinterpret_cast<const float4*>(qp_src + 64 * (ks / 2) + 8 * (ks % 2) + 4);
+      const float x[8] = {a.x * P.qscale, a.y * P.qscale, a.z * P.qscale, a.w * P.qscale,
+                          b.x * P.qscale, b.y * P.qscale, b.z * P.qscale, b.w * P.qscale};
+      split3(x, qp[ks]);
+    }
   }
+  // lane byte offsets of the K reads (tile 0, k-step 2 h + hf) and V reads
+  // (output tile 0) within a part plane
+  int klo[NH][2];
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+      klo[h][hf] = (vec * UPR + ((2 * gq + 8 * h + hf) ^ kswz<HD>(vec))) * 16;
+  const int vlo = (gq * HD + vec) * 16;
 
   f4 acc[NT];
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) acc[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = kMinitP, l_run = 0.0f;
 
-  // S^T of tile t (keys st*SK + 16t ..) in four independent chains
-  auto qk = [&](int t, const float* sk, f4 (&sc)[4]) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) sc[c] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int h = 0; h < NH; ++h) {
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const float4 x = lds4(sk + k_at(t, h, s4));
-        const int i = 16 * h + 4 * s4;
-        sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, qv[i + 0], sc[0], 0, 0, 0);
-        sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, qv[i + 1], sc[1], 0, 0, 0);
-        sc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, qv[i + 2], sc[2], 0, 0, 0);
-        sc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, qv[i + 3], sc[3], 0, 0, 0);
-      }
-    }
+  // a b = sum of a_i b_j over the parts; the six terms with i + j <= 2 are
+  // kept (the dropped ones are below 2^-23 |a b|, the size of the fp32
+  // rounding the reference's own sums carry)
+  auto terms2 = [&](const uint4 (&a)[3], const uint4 (&b)[3], f4& c0, f4& c1) {
+    c0 = mfma_bf16(a[0], b[0], c0);
+    c1 = mfma_bf16(a[0], b[1], c1);
+    c0 = mfma_bf16(a[1], b[0], c0);
+    c1 = mfma_bf16(a[0], b[2], c1);
+    c0 = mfma_bf16(a[1], b[1], c0);
+    c1 = mfma_bf16(a[2], b[0], c1);
+  };
+  auto terms1 = [&](const uint4 (&a)[3], const uint4 (&b)[3], f4& c) {
+    c = mfma_bf16(a[2], b[0], c);
+    c = mfma_bf16(a[1], b[1], c);
+    c = mfma_bf16(a[0], b[2], c);
+    c = mfma_bf16(a[1], b[0], c);
+    c = mfma_bf16(a[0], b[1], c);
+    c = mfma_bf16(a[0], b[0], c);
   };
 
-  // online softmax of tile t's scores, then O^T += V^T P^T. MASK: the tile
-  // reaches past some row's last key or past the workgroup's last key
-  // (causal diagonal, chunk tail); other tiles skip the masks.
-  auto soft_pv = [&](int st, int t, const float* sv, const f4 (&sc)[4], auto mask_c) {
+  // keys every row of the wave attends, and that the workgroup holds
+  const int wave_full = min(P.pos0 + row0, last_key);
+
+  // One stage: S^T of its two tiles, online softmax of the 32 keys, then
+  // O^T += V^T P^T. MASK: the stage reaches past some row's last key
+  // (causal diagonal, chunk tail).
+  auto compute = [&](int st, const char* sb, auto mask_c) {
     constexpr bool MASK = decltype(mask_c)::value;
-    const int kb = st * SK + 16 * t;  // first key of the tile (wave-uniform)
-    const f4 s = (sc[0] + sc[1]) + (sc[2] + sc[3]);
-    float sv4[4];
+    f4 sc[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      sc[u][0] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      sc[u][1] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          uint4 kp[3];
+#pragma unroll
+          for (int p = 0; p < 3; ++p)
+            kp[p] = *reinterpret_cast<const uint4*>(sb + p * PLANE + u * 16 * UPR * 16 + klo[h][hf]);
+          terms2(kp, qp[2 * h + hf], sc[u][0], sc[u][1]);
+        }
+    }
+    const int kb = st * SK;  // first key of the stage (wave-uniform)
+    float s8[8];
     float mx = kMinitP;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int key = kb + 4 * gq + v;
-      sv4[v] = !MASK || key <= limit ? s[v] : -INFINITY;
-      mx = fmaxf(mx, sv4[v]);
+    for (int u = 0; u < 2; ++u) {
+      const f4 s = sc[u][0] + sc[u][1];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int key = kb + 16 * u + 4 * gq + v;
+        s8[4 * u + v] = !MASK || key <= limit ? s[v] : -INFINITY;
+        mx = fmaxf(mx, s8[4 * u + v]);
+      }
     }
     mx = xmax32(xmax16(mx));
     const float mn = fmaxf(m_run, mx);
     const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
-    float pv[4], ls = 0.0f;
+    float pv8[8], ls = 0.0f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      pv[v] = __builtin_amdgcn_exp2f(sv4[v] - mn);
-      ls += pv[v];
+    for (int e = 0; e < 8; ++e) {
+      pv8[e] = __builtin_amdgcn_exp2f(s8[e] - mn);
+      ls += pv8[e];
     }
     ls = xsum32(xsum16(ls));
     l_run = l_run * alpha + ls;
@@ -296,164 +345,55 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt) acc[tt] *= alpha;
     }
-
-    // O^T += V^T P^T: output tile tt row i is dim VD i + tt. Keys past the
-    // workgroup's last row are never weighted and read as 0.
+    uint4 pb[3];
+    split3(pv8, pb);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int key = kb + 4 * gq + j;
-      float vd[VD];
+    for (int tt = 0; tt < NT; ++tt) {
+      uint4 va[3];
 #pragma unroll
-      for (int u = 0; u < VD / 4; ++u) {
-        const float4 x = lds4(sv + v_at(t, j, u));
-        vd[4 * u + 0] = !MASK || key <= last_key ? x.x : 0.0f;
-        vd[4 * u + 1] = !MASK || key <= last_key ? x.y : 0.0f;
-        vd[4 * u + 2] = !MASK || key <= last_key ? x.z : 0.0f;
-        vd[4 * u + 3] = !MASK || key <= last_key ? x.w : 0.0f;
-      }
-#pragma unroll
-      for (int tt = 0; tt < NT; ++tt)
-        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[tt], pv[j], acc[tt], 0, 0, 0);
+      for (int p = 0; p < 3; ++p)
+        va[p] = *reinterpret_cast<const uint4*>(sb + (3 + p) * PLANE + tt * 256 + vlo);
+      terms1(va, pb, acc[tt]);
     }
   };
-
-  // A stage's tiles, software-pipelined: tile t + 1's QK^T products are
-  // issued before tile t's softmax, so the matrix core works through them
-  // while the wave's VALU runs the softmax. Tiles past every row of the wave
-  // (the causal tail) are skipped.
-  constexpr int NTS = SK / 16;  // tiles per stage
-  // keys every row of the wave attends, and that the workgroup holds
-  const int wave_full = min(P.pos0 + row0, last_key);
-  // A stage whose tiles are all full and unmasked runs as one straight-line
-  // block: the LDS operands of tile t + 1 (V) and t + 2 (K) are read while
-  // tile t's products run, and tile t + 1's QK^T products are issued before
-  // tile t's softmax, so the scheduler can place the softmax's VALU and the
-  // reads between matrix instructions. Same operations in the same order as
-  // the general path (the rescale is unconditional: a multiply by exactly 1
-  // when the maxima hold), so the results are identical.
-  auto stage_full = [&](const float* sk, const float* sv) {
-    constexpr int NK = NQ / 4;  // 16-byte K reads per tile
-    auto ld_k = [&](int t, float4 (&x)[NK]) {
-#pragma unroll
-      for (int h = 0; h < NH; ++h)
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) x[4 * h + s4] = lds4(sk + k_at(t, h, s4));
-    };
-    auto ld_v = [&](int t, float4 (&x)[4][VD / 4]) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int u = 0; u < VD / 4; ++u) x[j][u] = lds4(sv + v_at(t, j, u));
-    };
-    auto mm_qk = [&](const float4 (&x)[NK], f4 (&sc)[4]) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) sc[c] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int i4 = 0; i4 < NK; ++i4) {
-        const int i = 4 * i4;
-        sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[i4].x, qv[i + 0], sc[0], 0, 0, 0);
-        sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[i4].y, qv[i + 1], sc[1], 0, 0, 0);
-        sc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[i4].z, qv[i + 2], sc[2], 0, 0, 0);
-        sc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[i4].w, qv[i + 3], sc[3], 0, 0, 0);
-      }
-    };
-    auto softmax = [&](const f4 (&sc)[4], float (&pv)[4]) {
-      const f4 s = (sc[0] + sc[1]) + (sc[2] + sc[3]);
-      float mx = kMinitP;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s[v]);
-      mx = xmax32(xmax16(mx));
-      const float mn = fmaxf(m_run, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
-      float ls = 0.0f;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        pv[v] = __builtin_amdgcn_exp2f(s[v] - mn);
-        ls += pv[v];
-      }
-      ls = xsum32(xsum16(ls));
-      l_run = l_run * alpha + ls;
-      m_run = mn;
-#pragma unroll
-      for (int tt = 0; tt < NT; ++tt) acc[tt] *= alpha;
-    };
-    auto mm_pv = [&](const float4 (&x)[4][VD / 4], const float (&pv)[4]) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float vd[VD];
-#pragma unroll
-        for (int u = 0; u < VD / 4; ++u) {
-          vd[4 * u + 0] = x[j][u].x;
-          vd[4 * u + 1] = x[j][u].y;
-          vd[4 * u + 2] = x[j][u].z;
-          vd[4 * u + 3] = x[j][u].w;
-        }
-#pragma unroll
-        for (int tt = 0; tt < NT; ++tt)
-          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[tt], pv[j], acc[tt], 0, 0, 0);
-      }
-    };
-    float4 kx[2][NK], vx[2][4][VD / 4];
-    f4 sc[2][4];
-    ld_k(0, kx[0]);
-    ld_v(0, vx[0]);
-    if (NTS > 1) ld_k(1, kx[1]);
-    mm_qk(kx[0], sc[0]);
-#pragma unroll
-    for (int t = 0; t < NTS; ++t) {
-      if (t + 1 < NTS) mm_qk(kx[(t + 1) & 1], sc[(t + 1) & 1]);
-      if (t + 2 < NTS) ld_k(t + 2, kx[t & 1]);
-      if (t + 1 < NTS) ld_v(t + 1, vx[(t + 1) & 1]);
-      float pv[4];
-      softmax(sc[t & 1], pv);
-      mm_pv(vx[t & 1], pv);
-    }
+  // stages past every row of the wave (the causal tail) are skipped
+  auto compute_stage = [&](int st, const char* sb) {
+    if (!wave_live || st * SK > wave_last) return;  // uniform
+    if (st * SK + SK - 1 <= wave_full)
+      compute(st, sb, std::false_type{});
+    else
+      compute(st, sb, std::true_type{});
   };
 
-  auto compute_stage = [&](int st, const float* sk, const float* sv) {
-    const int nt = !wave_live ? 0 : min(NTS, max(0, (wave_last - st * SK) / 16 + 1));  // uniform
-    if (wave_live && st * SK + SK - 1 <= wave_full) {  // uniform: every tile full
-      stage_full(sk, sv);
-      return;
+  // The next stage's loads are in flight while a stage computes; the
+  // compiler waits for them where the split reads them. With two buffers
+  // one barrier per stage separates the writes of one buffer from the
+  // reads of the other; with one, a barrier before and after the writes.
+  if (st_begin < st_end) {
+    load_stage(st_begin);
+    store_stage(st_begin, s_stage);
+  }
+  lds_barrier();
+  if constexpr (NBUF == 2) {
+    for (int st = st_begin; st < st_end; st += 2) {
+      if (st + 1 < st_end) load_stage(st + 1);
+      compute_stage(st, s_stage);
+      if (st + 1 < st_end) store_stage(st + 1, s_stage + S::BYTES);
+      lds_barrier();
+      if (st + 1 >= st_end) break;  // uniform
+      if (st + 2 < st_end) load_stage(st + 2);
+      compute_stage(st + 1, s_stage + S::BYTES);
+      if (st + 2 < st_end) store_stage(st + 2, s_stage);
+      lds_barrier();
     }
-    f4 sc[2][4];
-    if (nt > 0) qk(0, sk, sc[0]);
-#pragma unroll
-    for (int t = 0; t < NTS; ++t) {
-      if (t < nt) {
-        if (t + 1 < nt) qk(t + 1, sk, sc[(t + 1) & 1]);
-        if (st * SK + 16 * t + 15 <= wave_full)  // uniform
-          soft_pv(st, t, sv, sc[t & 1], std::false_type{});
-        else
-          soft_pv(st, t, sv, sc[t & 1], std::true_type{});
-      }
-    }
-  };
-
-#pragma unroll
-  for (int i = 0; i < NBUF - 1; ++i)
-    if (st_begin + i < st_end) copy_stage(st_begin + i, bufp(i));
-  // unrolled by the buffer count, so every buffer index is a constant
-  for (int st0 = st_begin; st0 < st_end; st0 += NBUF) {
-#pragma unroll
-    for (int b = 0; b < NBUF; ++b) {
-      const int st = st0 + b;
-      if (st >= st_end) break;  // uniform
-      if (st + NBUF - 1 < st_end) copy_stage(st + NBUF - 1, bufp((b + NBUF - 1) % NBUF));
-      // stage st has landed once at most the copies of the stages after it
-      // are outstanding (loads complete in order)
-      const int after = min(st_end - 1 - st, NBUF - 1);  // uniform
-      if (after >= 3)
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * 2 * NDMA) : "memory");
-      else if (after == 2)
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * 2 * NDMA) : "memory");
-      else if (after == 1)
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      lds_barrier();  // every wave's part of stage st has landed
-      compute_stage(st, bufp(b), bufp(b) + FL);
-      lds_barrier();  // every wave is done with this buffer before it is refilled
+  } else {
+    for (int st = st_begin; st < st_end; ++st) {
+      if (st + 1 < st_end) load_stage(st + 1);
+      compute_stage(st, s_stage);
+      if (st + 1 >= st_end) break;  // uniform
+      lds_barrier();
+      store_stage(st + 1, s_stage);
+      lds_barrier();
     }
   }
 
@@ -530,19 +470,19 @@ void launch_merge(const float* part, float* out, int n_vec, int ks, hipStream_t 
     hipLaunchKernelGGL((prefill_merge<HD, 8>), grid, dim3(kMergeThreads), 0, st, part, out, n_vec);
 }
 
-template <int HD, int NBUF>
+template <int HD>
 void* prefill_for(int G) {
   switch (G) {
-    case 1: return reinterpret_cast<void*>(&prefill_kernel<HD, 1, NBUF>);
-    case 2: return reinterpret_cast<void*>(&prefill_kernel<HD, 2, NBUF>);
-    case 4: return reinterpret_cast<void*>(&prefill_kernel<HD, 4, NBUF>);
-    case 8: return reinterpret_cast<void*>(&prefill_kernel<HD, 8, NBUF>);
+    case 1: return reinterpret_cast<void*>(&prefill_kernel<HD, 1>);
+    case 2: return reinterpret_cast<void*>(&prefill_kernel<HD, 2>);
+    case 4: return reinterpret_cast<void*>(&prefill_kernel<HD, 4>);
+    case 8: return reinterpret_cast<void*>(&prefill_kernel<HD, 8>);
     default: return nullptr;
   }
 }
 
 void* pick_prefill(int hd, int G, int /*rows*/) {
-  return hd == 64 ? prefill_for<64, 2>(G) : prefill_for<128, 2>(G);
+  return hd == 64 ? prefill_for<64>(G) : prefill_for<128>(G);
 }
 
 // key splits: two workgroups per CU (one wave per SIMD cannot hide the LDS
