@@ -99,7 +99,7 @@ __device__ __forceinline__ float xsum32(float x) {
 template <int HD>
 struct Stage {
   static constexpr int SK = 32;                   // keys per stage
-  static constexpr int NBUF = HD == 64 ? 2 : 1;   // stage buffers (two workgroups per CU)
+  static constexpr int NBUF = HD == 64 ? 3 : 1;   // stage buffers (two workgroups per CU)
   static constexpr int UPR = HD / 8;              // 16-byte units per key of a K part
   static constexpr int PLANE = SK * HD * 2;       // bytes of one part of K or V
   static constexpr int BYTES = 6 * PLANE;
@@ -179,22 +179,31 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     for (int m = 1; m < NU; ++m) dst[m] = dst[0] + 256u * m;
   }
   // the loaded stage: K lanes hold unit m in r[2 m], r[2 m + 1]; V lanes key
-  // e's NU dims in r[e] (NU = 4) or in half e % 2 of r[e / 2] (NU = 2)
+  // e's NU dims in r[e] (NU = 4) or in half e % 2 of r[e / 2] (NU = 2).
+  // Buffer loads from a resource over the stage (src offsets in bytes).
+#pragma unroll
+  for (int e = 0; e < 8; ++e) src[e] *= 4u;
   float4 r[2 * NU];
   auto load_stage = [&](int st) {
     const size_t so = static_cast<size_t>(st) * SK * HD;
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>((k_stager ? kbase : vbase) + so), static_cast<short>(0), SK * HD * 4,
+        0x00020000);
     if (k_stager) {
 #pragma unroll
       for (int i = 0; i < 2 * NU; ++i)
-        r[i] = *reinterpret_cast<const float4*>(kbase + so + src[i]);
+        r[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, src[i], 0, 0));
     } else if constexpr (NU == 4) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) r[e] = *reinterpret_cast<const float4*>(vbase + so + src[e]);
+      for (int e = 0; e < 8; ++e)
+        r[e] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, src[e], 0, 0));
     } else {
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
-        const float2 a = *reinterpret_cast<const float2*>(vbase + so + src[e]);
-        const float2 b = *reinterpret_cast<const float2*>(vbase + so + src[e + 1]);
+        const float2 a =
+            __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rs, src[e], 0, 0));
+        const float2 b =
+            __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rs, src[e + 1], 0, 0));
         r[e / 2] = make_float4(a.x, a.y, b.x, b.y);
       }
     }
@@ -293,12 +302,9 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   // keys every row of the wave attends, and that the workgroup holds
   const int wave_full = min(P.pos0 + row0, last_key);
 
-  // One stage: S^T of its two tiles, online softmax of the 32 keys, then
-  // O^T += V^T P^T. MASK: the stage reaches past some row's last key
-  // (causal diagonal, chunk tail).
-  auto compute = [&](int st, const char* sb, auto mask_c) {
-    constexpr bool MASK = decltype(mask_c)::value;
-    f4 sc[2][2];
+  // S^T of a stage's two tiles: sc[u] holds tile u in two chains (lane l:
+  // S[vector l % 16][key 4 (l / 16) + v])
+  auto qk = [&](const char* sb, f4 (&sc)[2][2]) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       sc[u][0] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -314,6 +320,11 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
           terms2(kp, qp[2 * h + hf], sc[u][0], sc[u][1]);
         }
     }
+  };
+  // Online softmax of a stage's 32 keys, then O^T += V^T P^T. MASK: the
+  // stage reaches past some row's last key (causal diagonal, chunk tail).
+  auto soft_pv = [&](int st, const char* sb, const f4 (&sc)[2][2], auto mask_c) {
+    constexpr bool MASK = decltype(mask_c)::value;
     const int kb = st * SK;  // first key of the stage (wave-uniform)
     float s8[8];
     float mx = kMinitP;
@@ -357,39 +368,69 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     }
   };
   // stages past every row of the wave (the causal tail) are skipped
-  auto compute_stage = [&](int st, const char* sb) {
-    if (!wave_live || st * SK > wave_last) return;  // uniform
+  auto live = [&](int st) { return wave_live && st * SK <= wave_last; };  // uniform
+  auto soft_pv_stage = [&](int st, const char* sb, const f4 (&sc)[2][2]) {
     if (st * SK + SK - 1 <= wave_full)
-      compute(st, sb, std::false_type{});
+      soft_pv(st, sb, sc, std::false_type{});
     else
-      compute(st, sb, std::true_type{});
+      soft_pv(st, sb, sc, std::true_type{});
   };
 
-  // The next stage's loads are in flight while a stage computes; the
-  // compiler waits for them where the split reads them. With two buffers
-  // one barrier per stage separates the writes of one buffer from the
-  // reads of the other; with one, a barrier before and after the writes.
+  // The next stages' loads are in flight while a stage computes; the
+  // compiler waits for them where the split reads them.
   if (st_begin < st_end) {
     load_stage(st_begin);
     store_stage(st_begin, s_stage);
   }
-  lds_barrier();
-  if constexpr (NBUF == 2) {
-    for (int st = st_begin; st < st_end; st += 2) {
-      if (st + 1 < st_end) load_stage(st + 1);
-      compute_stage(st, s_stage);
-      if (st + 1 < st_end) store_stage(st + 1, s_stage + S::BYTES);
-      lds_barrier();
-      if (st + 1 >= st_end) break;  // uniform
+  if constexpr (NBUF == 3) {
+    // Three buffers hold stages s, s + 1 (both stored) and s + 2 (being
+    // stored); the S^T products of stage s + 1 are issued before the
+    // softmax of stage s, so the matrix cores work through them while the
+    // wave's VALU runs the softmax, the splits and the staging. One barrier
+    // per stage: stage s + 2 is stored into the buffer stage s - 1 was read
+    // from, and read after the next barrier.
+    if (st_begin + 1 < st_end) {
+      load_stage(st_begin + 1);
+      store_stage(st_begin + 1, s_stage + S::BYTES);
+    }
+    lds_barrier();
+    f4 sa[2][2], sb2[2][2];
+    if (st_begin < st_end && live(st_begin)) qk(s_stage, sa);
+    // stage st in buffer B; cur / nxt its and the next stage's scores
+    auto step = [&](int st, auto b_c, f4 (&cur)[2][2], f4 (&nxt)[2][2]) {
+      constexpr int B = decltype(b_c)::value;
       if (st + 2 < st_end) load_stage(st + 2);
-      compute_stage(st + 1, s_stage + S::BYTES);
-      if (st + 2 < st_end) store_stage(st + 2, s_stage);
+      if (st + 1 < st_end && live(st + 1)) qk(s_stage + ((B + 1) % 3) * S::BYTES, nxt);
+      if (live(st)) soft_pv_stage(st, s_stage + B * S::BYTES, cur);
+      if (st + 2 < st_end) store_stage(st + 2, s_stage + ((B + 2) % 3) * S::BYTES);
       lds_barrier();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    for (int st = st_begin; st < st_end; st += 6) {
+      step(st, I0{}, sa, sb2);
+      if (st + 1 >= st_end) break;  // uniform
+      step(st + 1, I1{}, sb2, sa);
+      if (st + 2 >= st_end) break;
+      step(st + 2, I2{}, sa, sb2);
+      if (st + 3 >= st_end) break;
+      step(st + 3, I0{}, sb2, sa);
+      if (st + 4 >= st_end) break;
+      step(st + 4, I1{}, sa, sb2);
+      if (st + 5 >= st_end) break;
+      step(st + 5, I2{}, sb2, sa);
     }
   } else {
+    // one buffer: a barrier before and after each stage's writes
+    lds_barrier();
     for (int st = st_begin; st < st_end; ++st) {
       if (st + 1 < st_end) load_stage(st + 1);
-      compute_stage(st, s_stage);
+      if (live(st)) {
+        f4 sc[2][2];
+        qk(s_stage, sc);
+        soft_pv_stage(st, s_stage, sc);
+      }
       if (st + 1 >= st_end) break;  // uniform
       lds_barrier();
       store_stage(st + 1, s_stage);

@@ -278,6 +278,7 @@ def test_fused_decode_rejects_bad_input():
     (32, 8, 64, 0, 64), (32, 8, 64, 256, 100),
     (32, 8, 64, 1792, 256),   # config 2's last prefill chunk (matrix-core path for fp32)
     (32, 8, 128, 300, 128),   # hd 128, gqa 4
+    (32, 8, 128, 1500, 64),   # hd 128, 8 key splits
     (8, 8, 64, 5, 70),        # gqa 1
     (16, 8, 128, 17, 77),     # gqa 2, ragged last wave
     (32, 4, 64, 1000, 65),    # gqa 8 (config 1 shape)
@@ -290,6 +291,9 @@ def test_chunk_attention(dtype, nh, nkv, hd, pos0, n):
     got = g.attend_chunk(0, pos0, q, nh, scale_of(hd))
     want = o.attend_chunk(0, pos0, q, nh, scale_of(hd))
     assert_close(got, want, what=f"chunk dtype{dtype} pos0 {pos0} n {n}")
+    # a second call on the same workspace (split counters at a new epoch)
+    again = g.attend_chunk(0, pos0, q, nh, scale_of(hd))
+    assert np.array_equal(again, got)
 
 
 @pytest.mark.parametrize("dtype", [F32, INT8])
