@@ -123,10 +123,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kh = blockIdx.y;
+  const int kh = blockIdx.x;  // (grid x: the kv heads, see launch_prefill)
   const int gq = lane >> 4;      // lane group
   const int vec = lane & 15;     // query vector of this lane
-  const int rowb = blockIdx.x * (kPWaves * RPV);     // first row of the workgroup
+  const int rowb = blockIdx.y * (kPWaves * RPV);     // first row of the workgroup
   const int row0 = rowb + wave * RPV;                 // first row of the wave
   const bool wave_live = row0 < P.rows;               // wave-uniform
   const int row = min(row0 + vec / G, P.rows - 1);
@@ -576,7 +576,10 @@ hipError_t launch_prefill(const KvGeom& g, const KvStore& s, Workspace& ws, cons
   p.qscale = c.scale * kLog2eP;
   const int rows_per_block = kPWaves * (16 / G);
   void* args[] = {&p};
-  hipError_t e = hipLaunchKernel(fn, dim3((c.rows + rows_per_block - 1) / rows_per_block, g.nkv, ks),
+  // kv heads along grid x: workgroups go to the 8 XCDs round-robin by
+  // linear id, so with 8 kv heads every row block and split of one head
+  // runs on one XCD, and that XCD's L2 serves the head's K/V to all of them
+  hipError_t e = hipLaunchKernel(fn, dim3(g.nkv, (c.rows + rows_per_block - 1) / rows_per_block, ks),
                                  dim3(kPThreads), args, 0, st);
   if (e != hipSuccess || ks == 1) return e;
   if (g.hd == 64)
