@@ -49,7 +49,7 @@ struct PrefillParams {
   const float* vf;
   const float* q;   // [rows][n_heads][hd]
   float* out;       // [rows][n_heads][hd]
-  float* part;      // KS > 1: [KS][rows][n_heads][hd + 2] (o unnormalized, m, l)
+  float* part;      // KS > 1: o [KS][rows][n_heads][hd] (unnormalized), then (m, l) [KS][rows][n_heads][2]
   int capg, n_heads, rows, pos0, ks;
   float qscale;     // scale * log2(e)
 };
@@ -453,62 +453,79 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
                         acc[tt + 3][v] * inv);
     return;
   }
-  float* rec = P.part + (static_cast<size_t>(blockIdx.z) * P.rows * P.n_heads + rh) * (HD + 2);
-  float* op = rec + 4 * VD * gq;
+  // split records: o at [z][vector][HD], (m, l) at [z][vector][2] after
+  // every o
+  const size_t n_vec = static_cast<size_t>(P.rows) * P.n_heads;
+  float* op = P.part + (blockIdx.z * n_vec + rh) * HD + 4 * VD * gq;
 #pragma unroll
   for (int v = 0; v < 4; ++v)
 #pragma unroll
     for (int tt = 0; tt < NT; tt += 4)
       *reinterpret_cast<float4*>(op + VD * v + tt) =
           make_float4(acc[tt][v], acc[tt + 1][v], acc[tt + 2][v], acc[tt + 3][v]);
-  if (gq == 0) {
-    rec[HD] = m_run;
-    rec[HD + 1] = l_run;
-  }
+  if (gq == 0)
+    *reinterpret_cast<float2*>(P.part + P.ks * n_vec * HD + (blockIdx.z * n_vec + rh) * 2) =
+        make_float2(m_run, l_run);
 }
 
-// Combines the KS key splits of every (row, query head): one thread per dim,
-// 256 / HD (row, head) pairs per workgroup. Every record load of a thread is
-// issued before any of them is used (one round trip, not one per split).
+// Combines the KS key splits of every (row, query head): HD / 4 threads per
+// vector, 4 dims each; a workgroup serves rows of one kv head (grid x, as
+// in the chunk kernel, so it runs on the XCD that wrote the records). Every
+// record load of a thread is issued before any of them is used.
 constexpr int kMergeThreads = 256;
 template <int HD, int KS>
 __global__ __launch_bounds__(kMergeThreads) void prefill_merge(const float* __restrict__ part,
-                                                               float* __restrict__ out,
-                                                               int n_vec) {
-  const int rh = blockIdx.x * (kMergeThreads / HD) + static_cast<int>(threadIdx.x) / HD;
-  const int d = threadIdx.x % HD;
-  if (rh >= n_vec) return;
-  float o[KS], m[KS], l[KS];
+                                                               float* __restrict__ out, int rows,
+                                                               int n_heads, int G) {
+  constexpr int TPV = HD / 4;                // threads per vector
+  constexpr int VPW = kMergeThreads / TPV;   // vectors per workgroup (>= 8 >= G)
+  const int rpw = VPW / G;                   // rows per workgroup
+  const int kh = blockIdx.x;
+  const int j = static_cast<int>(threadIdx.x) / TPV, d4 = static_cast<int>(threadIdx.x) % TPV;
+  const int row = static_cast<int>(blockIdx.y) * rpw + j / G;
+  if (j >= rpw * G || row >= rows) return;
+  const size_t n_vec = static_cast<size_t>(rows) * n_heads;
+  const size_t rh = static_cast<size_t>(row) * n_heads + kh * G + j % G;
+  float4 o[KS];
+  float2 ml[KS];
 #pragma unroll
   for (int z = 0; z < KS; ++z) {
-    const float* r = part + (static_cast<size_t>(z) * n_vec + rh) * (HD + 2);
-    o[z] = r[d];
-    m[z] = r[HD];
-    l[z] = r[HD + 1];
+    o[z] = *reinterpret_cast<const float4*>(part + (z * n_vec + rh) * HD + 4 * d4);
+    ml[z] = *reinterpret_cast<const float2*>(part + KS * n_vec * HD + (z * n_vec + rh) * 2);
   }
   float M = kMinitP;
 #pragma unroll
-  for (int z = 0; z < KS; ++z) M = fmaxf(M, m[z]);
-  float L = 0.0f, O = 0.0f;
+  for (int z = 0; z < KS; ++z) M = fmaxf(M, ml[z].x);
+  float L = 0.0f;
+  float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
   for (int z = 0; z < KS; ++z) {
-    const float w = __builtin_amdgcn_exp2f(m[z] - M);
-    L += l[z] * w;
-    O += o[z] * w;
+    const float w = __builtin_amdgcn_exp2f(ml[z].x - M);
+    L += ml[z].y * w;
+    O.x += o[z].x * w;
+    O.y += o[z].y * w;
+    O.z += o[z].z * w;
+    O.w += o[z].w * w;
   }
-  out[static_cast<size_t>(rh) * HD + d] = O / L;
+  *reinterpret_cast<float4*>(out + rh * HD + 4 * d4) = make_float4(O.x / L, O.y / L, O.z / L, O.w / L);
 }
 
 template <int HD>
-void launch_merge(const float* part, float* out, int n_vec, int ks, hipStream_t st) {
-  const dim3 grid((n_vec + kMergeThreads / HD - 1) / (kMergeThreads / HD));
+void launch_merge(const float* part, float* out, int rows, int n_heads, int nkv, int ks,
+                  hipStream_t st) {
+  const int G = n_heads / nkv;
+  const int rpw = kMergeThreads / (HD / 4) / G;
+  const dim3 grid(nkv, (rows + rpw - 1) / rpw);
   static_assert(kPrefillMaxSplits == 8, "merge instances for 2, 4 and 8 splits");
   if (ks == 2)
-    hipLaunchKernelGGL((prefill_merge<HD, 2>), grid, dim3(kMergeThreads), 0, st, part, out, n_vec);
+    hipLaunchKernelGGL((prefill_merge<HD, 2>), grid, dim3(kMergeThreads), 0, st, part, out, rows,
+                       n_heads, G);
   else if (ks == 4)
-    hipLaunchKernelGGL((prefill_merge<HD, 4>), grid, dim3(kMergeThreads), 0, st, part, out, n_vec);
+    hipLaunchKernelGGL((prefill_merge<HD, 4>), grid, dim3(kMergeThreads), 0, st, part, out, rows,
+                       n_heads, G);
   else
-    hipLaunchKernelGGL((prefill_merge<HD, 8>), grid, dim3(kMergeThreads), 0, st, part, out, n_vec);
+    hipLaunchKernelGGL((prefill_merge<HD, 8>), grid, dim3(kMergeThreads), 0, st, part, out, rows,
+                       n_heads, G);
 }
 
 template <int HD>
@@ -583,9 +600,9 @@ hipError_t launch_prefill(const KvGeom& g, const KvStore& s, Workspace& ws, cons
                                  dim3(kPThreads), args, 0, st);
   if (e != hipSuccess || ks == 1) return e;
   if (g.hd == 64)
-    launch_merge<64>(ws.part, c.out, c.rows * c.n_heads, ks, st);
+    launch_merge<64>(ws.part, c.out, c.rows, c.n_heads, g.nkv, ks, st);
   else
-    launch_merge<128>(ws.part, c.out, c.rows * c.n_heads, ks, st);
+    launch_merge<128>(ws.part, c.out, c.rows, c.n_heads, g.nkv, ks, st);
   return hipGetLastError();
 }
 
