@@ -39,7 +39,7 @@ namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kPWaves = 4;
+constexpr int kPWaves = 8;
 constexpr int kPThreads = 64 * kPWaves;
 constexpr float kLog2eP = 1.4426950408889634f;
 constexpr float kMinitP = -1.0e30f;  // finite: exp2(kMinit - kMinit) == 1
@@ -99,11 +99,12 @@ __device__ __forceinline__ float xsum32(float x) {
 template <int HD>
 struct Stage {
   static constexpr int SK = 32;                   // keys per stage
-  static constexpr int NBUF = HD == 64 ? 3 : 1;   // stage buffers (two workgroups per CU)
+  static constexpr int NBUF = 3;                  // stage buffers (one workgroup per CU)
   static constexpr int UPR = HD / 8;              // 16-byte units per key of a K part
   static constexpr int PLANE = SK * HD * 2;       // bytes of one part of K or V
   static constexpr int BYTES = 6 * PLANE;
-  static constexpr int NU = SK * HD / 1024;       // staging lane: K units, or V dims
+  static constexpr int STG = kPThreads / 2;       // staging lanes of K (and of V)
+  static constexpr int NU = SK * HD / 8 / STG;    // staging lane: K units, or V dims
 };
 
 template <int HD>
@@ -143,19 +144,21 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const float* kbase = P.kf + head_el;
   const float* vbase = P.vf + head_el;
 
-  // ---- staging. K lanes (waves 0-1, t < 128): units n = t + 128 m, key
-  // n / UPR, dims 8 (n % UPR) .. + 7 (two float4 of the granule layout).
-  // V lanes (waves 2-3, t = 128 + 32 j + c): keys kv(j, e) x dims NU c ..
-  // NU c + NU - 1. The source offsets of stage 0 (stage st adds st * SK * HD:
-  // a stage is two whole granules).
-  const bool k_stager = wave < 2;  // uniform
+  // ---- staging. K lanes (the first half of the waves, t < STG): units
+  // n = t + STG m, key n / UPR, dims 8 (n % UPR) .. + 7 (two float4 of the
+  // granule layout). V lanes (t = STG + (HD / NU) j + c): keys kv(j, e) x
+  // dims NU c .. NU c + NU - 1. The source offsets of stage 0 (stage st adds
+  // st * SK * HD: a stage is two whole granules).
+  constexpr int STG = S::STG;
+  static_assert(NU == 1 || NU == 2, "staging shapes");
+  const bool k_stager = wave < kPWaves / 2;  // uniform
   uint32_t src[8];
   uint32_t dst[NU];  // K: the unit's byte offset in a part plane; V: [0] of dim NU c
   int vkey[8];
   if (k_stager) {
 #pragma unroll
     for (int m = 0; m < NU; ++m) {
-      const int n = static_cast<int>(threadIdx.x) + 128 * m;
+      const int n = static_cast<int>(threadIdx.x) + STG * m;
       const int key = n / UPR, u = n % UPR;
       src[2 * m] = static_cast<uint32_t>(k_off_tiled(HD, false, key, 8 * u));
       src[2 * m + 1] = static_cast<uint32_t>(k_off_tiled(HD, false, key, 8 * u + 4));
@@ -166,8 +169,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
     for (int e = 0; e < 8; ++e) vkey[e] = 0;
   } else {
-    const int t = static_cast<int>(threadIdx.x) - 128;
-    const int j = t >> 5, c = t & 31;
+    const int t = static_cast<int>(threadIdx.x) - STG;
+    const int j = t / (HD / NU), c = t % (HD / NU);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       vkey[e] = e < 4 ? 4 * j + e : 16 + 4 * j + e - 4;
@@ -179,7 +182,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     for (int m = 1; m < NU; ++m) dst[m] = dst[0] + 256u * m;
   }
   // the loaded stage: K lanes hold unit m in r[2 m], r[2 m + 1]; V lanes key
-  // e's NU dims in r[e] (NU = 4) or in half e % 2 of r[e / 2] (NU = 2).
+  // e's dim in component e % 4 of r[e / 4] (NU = 1) or its two dims in half
+  // e % 2 of r[e / 2] (NU = 2).
   // Buffer loads from a resource over the stage (src offsets in bytes).
 #pragma unroll
   for (int e = 0; e < 8; ++e) src[e] *= 4u;
@@ -193,10 +197,15 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
       for (int i = 0; i < 2 * NU; ++i)
         r[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, src[i], 0, 0));
-    } else if constexpr (NU == 4) {
+    } else if constexpr (NU == 1) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        r[e] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, src[e], 0, 0));
+      for (int e = 0; e < 8; e += 4) {
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          x[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, src[e + i], 0, 0));
+        r[e / 4] = make_float4(x[0], x[1], x[2], x[3]);
+      }
     } else {
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
@@ -209,9 +218,9 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     }
   };
   auto vdim = [&](int e, int m) -> float {
-    if constexpr (NU == 4) {
-      const float4 x = r[e];
-      return m == 0 ? x.x : m == 1 ? x.y : m == 2 ? x.z : x.w;
+    if constexpr (NU == 1) {
+      const float4 x = r[e / 4];
+      return e % 4 == 0 ? x.x : e % 4 == 1 ? x.y : e % 4 == 2 ? x.z : x.w;
     } else {
       const float4 x = r[e / 2];
       return (e & 1) == 0 ? (m == 0 ? x.x : x.y) : (m == 0 ? x.z : x.w);
@@ -382,7 +391,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     load_stage(st_begin);
     store_stage(st_begin, s_stage);
   }
-  if constexpr (NBUF == 3) {
+  static_assert(NBUF == 3, "three stage buffers");
+  {
     // Three buffers hold stages s, s + 1 (both stored) and s + 2 (being
     // stored); the S^T products of stage s + 1 are issued before the
     // softmax of stage s, so the matrix cores work through them while the
@@ -420,21 +430,6 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       step(st + 4, I1{}, sa, sb2);
       if (st + 5 >= st_end) break;
       step(st + 5, I2{}, sb2, sa);
-    }
-  } else {
-    // one buffer: a barrier before and after each stage's writes
-    lds_barrier();
-    for (int st = st_begin; st < st_end; ++st) {
-      if (st + 1 < st_end) load_stage(st + 1);
-      if (live(st)) {
-        f4 sc[2][2];
-        qk(s_stage, sc);
-        soft_pv_stage(st, s_stage, sc);
-      }
-      if (st + 1 >= st_end) break;  // uniform
-      lds_barrier();
-      store_stage(st + 1, s_stage);
-      lds_barrier();
     }
   }
 
@@ -543,8 +538,9 @@ void* pick_prefill(int hd, int G, int /*rows*/) {
   return hd == 64 ? prefill_for<64>(G) : prefill_for<128>(G);
 }
 
-// key splits: two workgroups per CU (one wave per SIMD cannot hide the LDS
-// and matrix-core latencies by itself), at least two stages each
+// key splits: one workgroup per CU (two waves per SIMD), at least two
+// stages each
+constexpr int kPrefillTargetBlocks = 256;
 int prefill_splits(const KvGeom& g, const AttnCall& c) {
   const int G = c.n_heads / g.nkv;
   const int rows_per_block = kPWaves * (16 / G);
@@ -552,7 +548,8 @@ int prefill_splits(const KvGeom& g, const AttnCall& c) {
   const int sk = g.hd == 64 ? Stage<64>::SK : Stage<128>::SK;
   const int stages = (c.pos0 + c.rows - 1) / sk + 1;
   int ks = 1;
-  while (ks < kPrefillMaxSplits && blocks * ks < 512 && stages / (2 * ks) >= 2) ks *= 2;
+  while (ks < kPrefillMaxSplits && blocks * ks < kPrefillTargetBlocks && stages / (2 * ks) >= 2)
+    ks *= 2;
   return ks;
 }
 
