@@ -375,9 +375,9 @@ def run_configs(torch, HipKV, F32, INT8, args):
                                               out[layer].data_ptr())
 
                 gc = capture(torch, chunk)
-                for _ in range(3):
+                for _ in range(10):
                     gc.replay()
-                msc = time_graph(torch, gc, max(3, args.config_steps // 4))
+                msc = time_graph(torch, gc, max(3, args.config_steps))
                 usc = 1000.0 * msc / L_
                 flops = sum((pos0 + c + 1) * nh * hd * 4 for c in range(rows))
                 res.update({"chunk_rows": rows, "chunk_pos0": pos0,
