@@ -147,7 +147,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   // ---- staging. K lanes (the first half of the waves, t < STG): units
   // n = t + STG m, key n / UPR, dims 8 (n % UPR) .. + 7 (two float4 of the
   // granule layout). V lanes (t = STG + (HD / NU) j + c): keys kv(j, e) x
-  // dims NU c .. NU c + NU - 1. The source offsets of stage 0 (stage st adds
+  // NU consecutive dims. The source offsets of stage 0 (stage st adds
   // st * SK * HD: a stage is two whole granules).
   constexpr int STG = S::STG;
   static_assert(NU == 1 || NU == 2, "staging shapes");
@@ -171,13 +171,17 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   } else {
     const int t = static_cast<int>(threadIdx.x) - STG;
     const int j = t / (HD / NU), c = t % (HD / NU);
+    // lane c writes units s, s + 16, .. with s = c % 16 + 16 NU (c / 16):
+    // 16 consecutive lanes write 16 consecutive units (no bank conflicts);
+    // their dims vdim(s + 16 m) = d + m are consecutive
+    const int s0 = c % 16 + 16 * NU * (c / 16);
+    const int d = VD * (c % 16) + NU * (c / 16);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       vkey[e] = e < 4 ? 4 * j + e : 16 + 4 * j + e - 4;
-      src[e] = static_cast<uint32_t>(v_off_tiled(HD, false, vkey[e], NU * c));
+      src[e] = static_cast<uint32_t>(v_off_tiled(HD, false, vkey[e], d));
     }
-    const int d = NU * c;  // dims d .. d + NU - 1: units s, s + 16, ..
-    dst[0] = static_cast<uint32_t>((j * HD + (d % VD) * 16 + d / VD) * 16);
+    dst[0] = static_cast<uint32_t>((j * HD + s0) * 16);
 #pragma unroll
     for (int m = 1; m < NU; ++m) dst[m] = dst[0] + 256u * m;
   }
