@@ -294,15 +294,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
   // a b = sum of a_i b_j over the parts; the six terms with i + j <= 2 are
   // kept (the dropped ones are below 2^-23 |a b|, the size of the fp32
-  // rounding the reference's own sums carry)
-  auto terms2 = [&](const uint4 (&a)[3], const uint4 (&b)[3], f4& c0, f4& c1) {
-    c0 = mfma_bf16(a[0], b[0], c0);
-    c1 = mfma_bf16(a[0], b[1], c1);
-    c0 = mfma_bf16(a[1], b[0], c0);
-    c1 = mfma_bf16(a[0], b[2], c1);
-    c0 = mfma_bf16(a[1], b[1], c0);
-    c1 = mfma_bf16(a[2], b[0], c1);
-  };
+  // rounding the reference's own sums carry). One accumulator chain: the
+  // matrix cores forward a dependent accumulation at full rate.
   auto terms1 = [&](const uint4 (&a)[3], const uint4 (&b)[3], f4& c) {
     c = mfma_bf16(a[2], b[0], c);
     c = mfma_bf16(a[1], b[1], c);
@@ -315,13 +308,12 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   // keys every row of the wave attends, and that the workgroup holds
   const int wave_full = min(P.pos0 + row0, last_key);
 
-  // S^T of a stage's two tiles: sc[u] holds tile u in two chains (lane l:
-  // S[vector l % 16][key 4 (l / 16) + v])
-  auto qk = [&](const char* sb, f4 (&sc)[2][2]) {
+  // S^T of a stage's two tiles: sc[u] holds tile u (lane l: S[vector l % 16]
+  // [key 4 (l / 16) + v])
+  auto qk = [&](const char* sb, f4 (&sc)[2]) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      sc[u][0] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-      sc[u][1] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      sc[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int h = 0; h < NH; ++h)
 #pragma unroll
@@ -330,20 +322,20 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
           for (int p = 0; p < 3; ++p)
             kp[p] = *reinterpret_cast<const uint4*>(sb + p * PLANE + u * 16 * UPR * 16 + klo[h][hf]);
-          terms2(kp, qp[2 * h + hf], sc[u][0], sc[u][1]);
+          terms1(kp, qp[2 * h + hf], sc[u]);
         }
     }
   };
   // Online softmax of a stage's 32 keys, then O^T += V^T P^T. MASK: the
   // stage reaches past some row's last key (causal diagonal, chunk tail).
-  auto soft_pv = [&](int st, const char* sb, const f4 (&sc)[2][2], auto mask_c) {
+  auto soft_pv = [&](int st, const char* sb, const f4 (&sc)[2], auto mask_c) {
     constexpr bool MASK = decltype(mask_c)::value;
     const int kb = st * SK;  // first key of the stage (wave-uniform)
     float s8[8];
     float mx = kMinitP;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const f4 s = sc[u][0] + sc[u][1];
+      const f4 s = sc[u];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int key = kb + 16 * u + 4 * gq + v;
@@ -382,7 +374,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   };
   // stages past every row of the wave (the causal tail) are skipped
   auto live = [&](int st) { return wave_live && st * SK <= wave_last; };  // uniform
-  auto soft_pv_stage = [&](int st, const char* sb, const f4 (&sc)[2][2]) {
+  auto soft_pv_stage = [&](int st, const char* sb, const f4 (&sc)[2]) {
     if (st * SK + SK - 1 <= wave_full)
       soft_pv(st, sb, sc, std::false_type{});
     else
@@ -408,10 +400,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       store_stage(st_begin + 1, s_stage + S::BYTES);
     }
     lds_barrier();
-    f4 sa[2][2], sb2[2][2];
+    f4 sa[2], sb2[2];
     if (st_begin < st_end && live(st_begin)) qk(s_stage, sa);
     // stage st in buffer B; cur / nxt its and the next stage's scores
-    auto step = [&](int st, auto b_c, f4 (&cur)[2][2], f4 (&nxt)[2][2]) {
+    auto step = [&](int st, auto b_c, f4 (&cur)[2], f4 (&nxt)[2]) {
       constexpr int B = decltype(b_c)::value;
       if (st + 2 < st_end) load_stage(st + 2);
       if (st + 1 < st_end && live(st + 1)) qk(s_stage + ((B + 1) % 3) * S::BYTES, nxt);
