@@ -43,6 +43,7 @@ constexpr int kPWaves = 8;
 constexpr int kPThreads = 64 * kPWaves;
 constexpr float kLog2eP = 1.4426950408889634f;
 constexpr float kMinitP = -1.0e30f;  // finite: exp2(kMinit - kMinit) == 1
+constexpr float kLazyLog2 = 8.0f;    // weights relative to the running maximum: at most 2^8
 
 struct PrefillParams {
   const float* kf;  // this layer's K, V: [nkv][capg * hd], granule layout
@@ -64,16 +65,19 @@ __device__ __forceinline__ void lds_barrier() {
 // (x, x), a lane holds its own x and the x of lane ^ 16 (one in each
 // register); v_permlane32_swap does the same for lane ^ 32. Emitted through
 // asm: the compiler's builtins fold the two results into one when both are
-// used.
+// used. The maxima take the max inside the asm too: fmaxf on asm results
+// costs two NaN-quieting v_max of its operands first.
 __device__ __forceinline__ float xmax16(float x) {
   float a = x, b = x;
-  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return fmaxf(a, b);
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 0\n\tv_max_f32 %0, %0, %1"
+      : "+v"(a), "+v"(b));
+  return a;
 }
 __device__ __forceinline__ float xmax32(float x) {
   float a = x, b = x;
-  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return fmaxf(a, b);
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 0\n\tv_max_f32 %0, %0, %1"
+      : "+v"(a), "+v"(b));
+  return a;
 }
 __device__ __forceinline__ float xsum16(float x) {
   float a = x, b = x;
@@ -344,19 +348,22 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       }
     }
     mx = xmax32(xmax16(mx));
-    const float mn = fmaxf(m_run, mx);
+    // The reference maximum m_run moves only when a score passes it by more
+    // than 2^kLazyLog2 (so every weight is at most 2^kLazyLog2: the splits
+    // stay exact and the sums far from fp32's range), and then to the
+    // stage's maximum. Otherwise alpha is exactly 1 in every lane and the
+    // rescale is skipped: after the first stages it almost never runs.
+    const float mn = mx > m_run + kLazyLog2 ? mx : m_run;
     const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
-    float pv8[8], ls = 0.0f;
+    float pv8[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      pv8[e] = __builtin_amdgcn_exp2f(s8[e] - mn);
-      ls += pv8[e];
-    }
+    for (int e = 0; e < 8; ++e) pv8[e] = __builtin_amdgcn_exp2f(s8[e] - mn);
+    float ls = pv8[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) ls += pv8[e];
     ls = xsum32(xsum16(ls));
     l_run = l_run * alpha + ls;
     m_run = mn;
-    // once the running maxima settle, alpha is exactly 1 in every lane and
-    // the rescale (a multiply by 1) is skipped
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt) acc[tt] *= alpha;
