@@ -31,9 +31,17 @@ constexpr int kTargetBlocks = 256;
 
 // Dense chunks of two or more rows run on the matrix-core rows kernels
 // (attn_rows.hpp for fp32, attn_i8_rows.hpp for int8): nvt 16-vector tiles
-// per workgroup, 16 nvt / G rows each.
+// per workgroup (int8 nvt 3: one, and a remainder tile), rows_vectors / G
+// rows each.
 bool rows_kernel(const KvGeom& g, const AttnCall& c) { return !g.ring && c.rows > 1; }
-int rows_nvt(int G, int rows) { return rows * G <= 16 ? 1 : 2; }
+// 1: one 16-column tile; 2: two; 3 (int8): one, plus a remainder tile of
+// (query, channel block) columns for up to 16 / (hd / 32) more vectors
+int rows_nvt(const KvGeom& g, int G, int rows) {
+  if (rows * G <= 16) return 1;
+  return g.int8 && rows * G <= 16 + 16 / (g.hd / 32) ? 3 : 2;
+}
+// query vectors a workgroup of the instance serves
+int rows_vectors(const KvGeom& g, int nvt) { return nvt == 3 ? 16 + 16 / (g.hd / 32) : 16 * nvt; }
 
 struct Plan {
   int nsplit, chunks_per_split;
@@ -50,8 +58,8 @@ Plan plan(const KvGeom& g, const AttnCall& c) {
   const int chunk = rowsk && !g.int8 ? kGranule : chunk_of(g);
   const int nkeys_max = g.ring ? c.ring.n_res : c.pos0 + c.rows;
   const int nchunks = (nkeys_max + chunk - 1) / chunk;
-  const int nvt = rowsk ? rows_nvt(G, c.rows) : 0;
-  const int nr = rowsk ? (16 * nvt / G < c.rows ? 16 * nvt / G : c.rows) : 1;
+  const int nvt = rowsk ? rows_nvt(g, G, c.rows) : 0;
+  const int nr = rowsk ? (rows_vectors(g, nvt) / G < c.rows ? rows_vectors(g, nvt) / G : c.rows) : 1;
   const int zgroups = (c.rows + nr - 1) / nr;
   const int units = g.nkv * zgroups;
   // whole waves of workgroups only: a launch of target + a few would run a

@@ -306,6 +306,12 @@ def test_chunk_attention(dtype, nh, nkv, hd, pos0, n):
     (8, 8, 64, 5, 63, 4),         # gqa 1: two row groups (32 + 31)
     (32, 8, 128, 16379, 5, 4),    # config 5's verify round at 16k (32 splits)
     (32, 8, 128, 4, 6, 9),        # int8: rows see 5..9 sinks (more than the merge holds at once)
+    # int8 remainder tiles (16 vectors + up to 16 / (hd / 32) in (query, block) columns)
+    (32, 8, 128, 2, 5, 4),        # gqa 4, 20 vectors: rows see 3..4 sinks
+    (24, 8, 128, 700, 6, 4),      # gqa 3, 18 vectors: a remainder of 2
+    (40, 8, 64, 300, 4, 4),       # hd 64, gqa 5, 20 vectors: 4 of 8 remainder columns
+    (16, 8, 64, 90, 12, 4),       # hd 64, gqa 2, 24 vectors: the full remainder
+    (28, 4, 128, 4000, 10, 4),    # gqa 7: row groups of 2 rows (14 vectors, one tile)
 ])
 def test_chunk_rows(dtype, nh, nkv, hd, pos0, n, ns):
     """Dense chunks of 2..63 rows (model.cpp:956-981) run on the matrix-core
