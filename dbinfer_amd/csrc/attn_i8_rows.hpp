@@ -270,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
       float mx = s[0];
 #pragma unroll
       for (int k = 1; k < 8; ++k) mx = fmaxf(mx, s[k]);
-      const float mn = fmaxf(M[T], col_max(mx));
+      const float mn = lazy_max(M[T], col_max(mx));
       const float alpha = fast_exp2(M[T] - mn);
       M[T] = mn;
       float ls = 0.0f;
@@ -281,13 +281,16 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
       }
       l[T] = fmaf(l[T], alpha, ls);
       // rescale of the output rows (queries 4 grp + i of this tile): the
-      // factor of column 4 grp + i, from that column's lane
+      // factor of column 4 grp + i, from that column's lane; skipped while
+      // every reference maximum holds
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float ar = __builtin_bit_cast(
-            float, __builtin_amdgcn_ds_bpermute(4 * (4 * grp + i), __builtin_bit_cast(int, alpha)));
+        for (int i = 0; i < 4; ++i) {
+          const float ar = __builtin_bit_cast(
+              float, __builtin_amdgcn_ds_bpermute(4 * (4 * grp + i), __builtin_bit_cast(int, alpha)));
 #pragma unroll
-        for (int t = 0; t < NTV; ++t) o[T][t][i] *= ar;
+          for (int t = 0; t < NTV; ++t) o[T][t][i] *= ar;
+        }
       }
     }
     // REM: the NJ block partials of a query sit in NJ neighbouring lanes (a
@@ -308,7 +311,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
       float mx = s[0];
 #pragma unroll
       for (int k = 1; k < 8; ++k) mx = fmaxf(mx, s[k]);
-      const float mn = fmaxf(MR, col_max(mx));
+      const float mn = lazy_max(MR, col_max(mx));
       const float alpha = fast_exp2(MR - mn);
       MR = mn;
       float ls = 0.0f;
@@ -318,8 +321,10 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
         ls += pkr[k];
       }
       lR = fmaf(lR, alpha, ls);
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-      for (int t = 0; t < NTV; ++t) oR[t] *= alpha;  // (the lane's own column)
+        for (int t = 0; t < NTV; ++t) oR[t] *= alpha;  // (the lane's own column)
+      }
     }
     // ---- PV per V block: w_b = p * vs[pos][b] (masked slots: p = 0, and
     // outside the group's keys vs = 0), three parts, against the V codes of

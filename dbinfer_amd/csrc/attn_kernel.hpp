@@ -64,6 +64,12 @@ constexpr int kMaxSplits = 64;  // one split per lane in the merge
 constexpr int kCounterStride = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMinit = -1.0e30f;  // finite: exp2(kMinit - kMinit) == 1, no NaN
+// Lazy reference maximum of the chunk-rows kernels' softmax: it moves only
+// when a score passes it by more than 2^kLazyLog2 (so every weight is at
+// most 2^kLazyLog2, exact in the three-part splits and far from fp32's
+// range); otherwise alpha is exactly 1 and the rescale is skipped.
+constexpr float kLazyLog2 = 8.0f;
+__device__ __forceinline__ float lazy_max(float m, float cm) { return cm > m + kLazyLog2 ? cm : m; }
 
 enum Kind { kF32Dense = 0, kI8Dense = 1, kF32Ring = 2, kI8Ring = 3 };
 

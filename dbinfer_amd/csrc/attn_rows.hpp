@@ -191,7 +191,7 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P)
         s[v] = k0 + 4 * kk + v <= lim[vt] ? s4[v] : -INFINITY;
         mx = fmaxf(mx, s[v]);
       }
-      const float mn = fmaxf(M[vt], col_max(mx));
+      const float mn = lazy_max(M[vt], col_max(mx));
       const float alpha = fast_exp2(M[vt] - mn);
       M[vt] = mn;
       float ls = 0.0f;
@@ -201,8 +201,10 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P)
         ls += pw[vt][v];
       }
       l[vt] = fmaf(l[vt], alpha, ls);
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {  // (the maxima moved)
 #pragma unroll
-      for (int tt = 0; tt < NT; ++tt) acc[vt][tt] *= alpha;
+        for (int tt = 0; tt < NT; ++tt) acc[vt][tt] *= alpha;
+      }
     }
 
     // ---- O^T += V^T P^T; keys past the group's last key weigh 0, and in
