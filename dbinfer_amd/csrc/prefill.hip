@@ -6,14 +6,19 @@
 // Design (CDNA4 v_mfma_f32_16x16x32_bf16 over exact three-part splits of the
 // fp32 operands, bf16x3.hpp, so the result stays within the fp32 tolerance
 // of the CPU path):
-//  - A workgroup of 4 waves owns 64 query vectors of one kv head: each wave
-//    16 vectors (16/G rows x the G query heads sharing the kv head). The
-//    workgroup walks its keys in stages of 32 (one pair of 16-key tiles).
-//  - Staging: the stage's fp32 K and V are loaded into registers while the
-//    previous stage computes, split once per workgroup into hi, mid and lo
-//    bf16 parts and written to LDS in the matrix cores' operand layout:
-//    every operand read of the waves is one 16-byte LDS load of 8 bf16, and
-//    no wave converts K or V itself. Waves 0-1 stage K, waves 2-3 V.
+//  - A workgroup of 8 waves (one per CU) owns 128 query vectors of one kv
+//    head: each wave 16 columns, 16/G rows x the G query heads sharing the
+//    kv head (G = 3, 5, 6, 7 leave 16 mod G padding columns, which compute
+//    and write nothing of use). The grid is (kv head, row block, key
+//    split): with kv heads along x, every row block and split of one head
+//    runs on one XCD, whose L2 serves the head's K/V to all of them.
+//  - The workgroup walks its keys in stages of 32 (one pair of 16-key
+//    tiles). Staging: a stage's fp32 K and V are loaded into registers while
+//    earlier stages compute, split once per workgroup into hi, mid and lo
+//    bf16 parts and written to LDS in the matrix cores' operand layout
+//    (waves 0-3 K, 4-7 V): every operand read of the waves is one 16-byte
+//    LDS load of 8 bf16, and no wave converts K or V itself. Three stage
+//    buffers: a step issues the next stage's QK^T before its own softmax.
 //  - Keys can be split over KS workgroups (grid z) to fill the GPU on short
 //    chunks; a split writes its unnormalized (o, m, l) and prefill_merge
 //    combines them.
@@ -26,8 +31,9 @@
 //    e < 4, key 4 gq + e - 4 of the second otherwise), A = V^T in the same
 //    key order. Output tile tt row i stands for dim (hd/16) i + tt, so a
 //    lane's output is hd/4 contiguous floats of its vector.
-//  - Online softmax per vector (= per lane % 16); the four lane groups
-//    holding one vector combine through two lane swaps.
+//  - Online softmax per vector (= per lane % 16) with a lazy reference
+//    maximum; the four lane groups holding one vector combine through two
+//    lane swaps.
 #include <cmath>
 #include <type_traits>
 
@@ -120,7 +126,7 @@ template <int HD, int G>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(const PrefillParams P) {
   using S = Stage<HD>;
   constexpr int SK = S::SK, NBUF = S::NBUF, UPR = S::UPR, PLANE = S::PLANE, NU = S::NU;
-  constexpr int RPV = 16 / G;    // rows per wave
+  constexpr int RPV = 16 / G;    // rows per wave (columns past RPV G pad the tile)
   constexpr int NH = HD / 64;    // 64-dim runs of a K row
   constexpr int VD = HD / 16;    // output tiles
   constexpr int NT = VD;
@@ -134,7 +140,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const int rowb = blockIdx.y * (kPWaves * RPV);     // first row of the workgroup
   const int row0 = rowb + wave * RPV;                 // first row of the wave
   const bool wave_live = row0 < P.rows;               // wave-uniform
-  const int row = min(row0 + vec / G, P.rows - 1);
+  // (a padding column repeats the wave's last row; it writes nothing)
+  const int row = min(row0 + min(vec / G, RPV - 1), P.rows - 1);
   const int head = kh * G + vec % G;
   const int limit = P.pos0 + row;  // last key of this vector
   // the workgroup's keys [0, last_key], in stages; split z takes its share
@@ -437,7 +444,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   }
 
   // lane holds O^T[dim VD (4 gq + v) + tt][vec]: dims 4 VD gq .. 4 VD gq + 4 VD - 1
-  if (!wave_live || row0 + vec / G >= P.rows) return;
+  if (!wave_live || vec >= RPV * G || row0 + vec / G >= P.rows) return;
   const size_t rh = static_cast<size_t>(row) * P.n_heads + head;
   if (P.ks == 1) {
     const float inv = 1.0f / l_run;
@@ -531,7 +538,11 @@ void* prefill_for(int G) {
   switch (G) {
     case 1: return reinterpret_cast<void*>(&prefill_kernel<HD, 1>);
     case 2: return reinterpret_cast<void*>(&prefill_kernel<HD, 2>);
+    case 3: return reinterpret_cast<void*>(&prefill_kernel<HD, 3>);
     case 4: return reinterpret_cast<void*>(&prefill_kernel<HD, 4>);
+    case 5: return reinterpret_cast<void*>(&prefill_kernel<HD, 5>);
+    case 6: return reinterpret_cast<void*>(&prefill_kernel<HD, 6>);
+    case 7: return reinterpret_cast<void*>(&prefill_kernel<HD, 7>);
     case 8: return reinterpret_cast<void*>(&prefill_kernel<HD, 8>);
     default: return nullptr;
   }

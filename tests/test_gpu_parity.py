@@ -279,6 +279,10 @@ def test_fused_decode_rejects_bad_input():
     (32, 8, 64, 1792, 256),   # config 2's last prefill chunk (matrix-core path for fp32)
     (32, 8, 128, 300, 128),   # hd 128, gqa 4
     (32, 8, 128, 1500, 64),   # hd 128, 8 key splits
+    (24, 8, 128, 300, 100),   # gqa 3 (5 rows per wave, one padding column)
+    (28, 4, 128, 1000, 64),   # gqa 7 (2 rows per wave, two padding columns)
+    (40, 8, 64, 50, 77),      # gqa 5
+    (48, 8, 64, 10, 130),     # gqa 6 (2 rows per wave, four padding columns)
     (8, 8, 64, 5, 70),        # gqa 1
     (16, 8, 128, 17, 77),     # gqa 2, ragged last wave
     (32, 4, 64, 1000, 65),    # gqa 8 (config 1 shape)
