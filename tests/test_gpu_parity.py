@@ -332,6 +332,31 @@ def test_chunk_rows(dtype, nh, nkv, hd, pos0, n, ns):
     assert np.array_equal(again, got)
 
 
+@pytest.mark.parametrize("dtype", [F32, INT8])
+@pytest.mark.parametrize("nh,nkv,hd,pos0,n", [
+    (32, 8, 64, 1000, 256),   # fp32: prefill kernel, hd 64
+    (24, 8, 128, 300, 100),   # fp32: prefill kernel at gqa 3
+    (32, 8, 128, 2000, 5),    # rows kernels (int8: the remainder tile)
+])
+def test_chunk_attention_rising_scores(dtype, nh, nkv, hd, pos0, n):
+    """Scores that climb along the keys (q x 2, K rows scaled by 1 + pos/1024)
+    move every row's running maximum from ~7 to ~30 in log2 units, past the
+    kernels' lazy reference maximum by more than 8 several times: the
+    rescale runs mid-stream and weights near 2^8 enter before it. (Scores
+    of several hundred put fp32's own rounding of a score above the 1e-4
+    tolerance for every kernel, the exact-product fp32 one included.)"""
+    g, o = pair(1, 2100, nkv, hd, n_sink=4, dtype=dtype)
+    P = g.pos_stride
+    K, V = normal(3100 + n, 1, pos0 + n, P), normal(3101 + n, 1, pos0 + n, P)
+    K *= (1.0 + np.arange(pos0 + n, dtype=np.float32) / 1024.0)[None, :, None]
+    g.append_n(0, 0, K[0], V[0])
+    o.append_n(0, 0, K[0], V[0])
+    q = normal(3102 + n, n, nh * hd) * np.float32(2.0)
+    got = g.attend_chunk(0, pos0, q, nh, scale_of(hd))
+    want = o.attend_chunk(0, pos0, q, nh, scale_of(hd), n_threads=8)
+    assert_close(got, want, what=f"rising scores dtype {dtype} hd {hd} n {n}")
+
+
 # ---------------------------------------------------------------- long context
 
 
