@@ -283,6 +283,7 @@ def test_fused_decode_rejects_bad_input():
     (28, 4, 128, 1000, 64),   # gqa 7 (2 rows per wave, two padding columns)
     (40, 8, 64, 50, 77),      # gqa 5
     (48, 8, 64, 10, 130),     # gqa 6 (2 rows per wave, four padding columns)
+    (16, 16, 128, 40, 130),   # hd 128, gqa 1 (16 rows per wave, 128 per workgroup)
     (8, 8, 64, 5, 70),        # gqa 1
     (16, 8, 128, 17, 77),     # gqa 2, ragged last wave
     (32, 4, 64, 1000, 65),    # gqa 8 (config 1 shape)
@@ -316,6 +317,8 @@ def test_chunk_attention(dtype, nh, nkv, hd, pos0, n):
     (40, 8, 64, 300, 4, 4),       # hd 64, gqa 5, 20 vectors: 4 of 8 remainder columns
     (16, 8, 64, 90, 12, 4),       # hd 64, gqa 2, 24 vectors: the full remainder
     (28, 4, 128, 4000, 10, 4),    # gqa 7: row groups of 2 rows (14 vectors, one tile)
+    (8, 8, 128, 100, 18, 4),      # gqa 1, 18 vectors: remainder of 2 rows
+    (16, 8, 128, 500, 10, 4),     # gqa 2, 20 vectors: the full remainder
 ])
 def test_chunk_rows(dtype, nh, nkv, hd, pos0, n, ns):
     """Dense chunks of 2..63 rows (model.cpp:956-981) run on the matrix-core
