@@ -360,6 +360,29 @@ def test_chunk_attention_rising_scores(dtype, nh, nkv, hd, pos0, n):
     assert_close(got, want, what=f"rising scores dtype {dtype} hd {hd} n {n}")
 
 
+# (drawn once with numpy's default_rng(2026); every gqa factor, both head dims)
+RANDOM_CHUNKS = [
+    (F32, 8, 8, 64, 47, 3), (INT8, 8, 4, 64, 833, 17), (F32, 6, 2, 128, 1147, 17),
+    (INT8, 16, 4, 128, 1304, 150), (F32, 40, 8, 64, 1189, 150), (INT8, 12, 2, 64, 1077, 150),
+    (F32, 14, 2, 128, 297, 7), (INT8, 48, 6, 128, 1563, 100), (F32, 2, 2, 64, 1048, 64),
+    (INT8, 16, 8, 64, 925, 3), (F32, 12, 4, 128, 1082, 150), (INT8, 16, 4, 128, 598, 33),
+    (F32, 10, 2, 64, 262, 7), (INT8, 12, 2, 64, 867, 150), (INT8, 24, 8, 128, 1500, 6),
+]
+
+
+@pytest.mark.parametrize("dtype,nh,nkv,hd,pos0,n", RANDOM_CHUNKS)
+def test_chunk_attention_random_shapes(dtype, nh, nkv, hd, pos0, n):
+    """Chunk calls over mixed shapes: the prefill kernel (fp32, >= 64 rows,
+    any gqa), the rows kernels with one or several row groups, and the int8
+    remainder tile, each against the oracle."""
+    g, o = pair(1, 1900, nkv, hd, n_sink=4, dtype=dtype)
+    fill_both(g, o, 1, pos0 + n, 200 + n + pos0 % 97, outlier=dtype == INT8)
+    q = normal(201 + n, n, nh * hd)
+    got = g.attend_chunk(0, pos0, q, nh, scale_of(hd))
+    want = o.attend_chunk(0, pos0, q, nh, scale_of(hd), n_threads=8)
+    assert_close(got, want, what=f"random chunk dtype {dtype} {nh}/{nkv} hd {hd} pos0 {pos0} n {n}")
+
+
 # ---------------------------------------------------------------- long context
 
 
