@@ -214,3 +214,55 @@ def test_producer_step_graph_replay(dtype, n_sink, window, bias):
             kv.attend_async(0, pos, nh, scale, q[1].data_ptr(), other[0].data_ptr())
             torch.cuda.synchronize()
         kv.close()
+
+
+@pytest.mark.parametrize("dtype,nh,nkv,hd,pos0,n", [
+    (F32, 32, 8, 64, 1792, 256),   # prefill kernel, 4 key splits and the merge launch
+    (F32, 32, 8, 128, 1500, 5),    # fp32 rows kernel and its merge launch
+    (INT8, 32, 8, 128, 1500, 5),   # int8 rows kernel: remainder tile, sinks in the merge
+])
+def test_chunk_graph_replay_matches_eager(dtype, nh, nkv, hd, pos0, n):
+    """Chunk calls captured in a graph (the bench's chunk timing): every
+    replay, with eager chunk calls on the same workspace in between, gives
+    the eager result bit for bit."""
+    torch = pytest.importorskip("torch")
+    L, cap_pos = 2, pos0 + n
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(11)
+        K = torch.randn(L, cap_pos, nkv * hd, device="cuda", generator=g)
+        V = torch.randn(L, cap_pos, nkv * hd, device="cuda", generator=g)
+        q = torch.randn(L, n * nh * hd, device="cuda", generator=g)
+        q2 = torch.randn(n * nh * hd, device="cuda", generator=g)
+        kv = HipKV(L, cap_pos, nkv, hd, 4, 0, dtype, 1e6)
+        kv.set_stream(stream.cuda_stream)
+        for l in range(L):
+            kv.append_async(l, 0, cap_pos, K[l].data_ptr(), V[l].data_ptr())
+        out = torch.zeros(L, n * nh * hd, device="cuda")
+
+        def chunk():
+            for l in range(L):
+                kv.attend_chunk_async(l, pos0, n, nh, scale, q[l].data_ptr(), out[l].data_ptr())
+
+        chunk()
+        torch.cuda.synchronize()
+        eager = out.clone()
+        graph = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(stream)
+        with torch.cuda.graph(graph, stream=cap):
+            kv.set_stream(cap.cuda_stream)
+            chunk()
+        kv.set_stream(stream.cuda_stream)
+        torch.cuda.synchronize()
+        for r in range(4):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {r}"
+            other = torch.empty_like(q2)
+            kv.attend_chunk_async(1, pos0, n, nh, scale, q2.data_ptr(), other.data_ptr())
+            torch.cuda.synchronize()
+        kv.close()
