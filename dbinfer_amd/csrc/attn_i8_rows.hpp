@@ -165,7 +165,8 @@ __global__ __launch_bounds__(kThreads) void attn_i8_rows_kernel(const AttnParams
         vsc[s][0] = t.x;
         vsc[s][1] = t.y;
       }
-      if constexpr (REM) vsr[s] = load_b32(rvs, vo + rc * 4, 0);  // (vs_bytes + ...: 0)
+      // (vo = vs_bytes for a masked position: the read lands past num_records, 0)
+      if constexpr (REM) vsr[s] = load_b32(rvs, vo + rc * 4, 0);
     }
   };
 
