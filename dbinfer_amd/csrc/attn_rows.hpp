@@ -273,41 +273,35 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P)
         L += lw[i] * f[i];
       }
     };
-    auto o_of = [&](int ql, int d, const float (&f)[kWaves]) {
-      float O = 0.0f;
+    // one thread per (query, 4 dims): the combine once per thread, float4
+    // reads of the wave states and float4 stores (the records are read by
+    // the merge launch, after this kernel)
+    constexpr int D4 = HD / 4;
+    const size_t row_stride = static_cast<size_t>(P.nkv) * record_region(P.nsplit, G, HD);
+    float* const rbase = P.part +
+                         (static_cast<size_t>(row0) * P.nkv + kh) * record_region(P.nsplit, G, HD) +
+                         static_cast<size_t>(split) * record_floats(G, HD);
+    for (int idx = threadIdx.x; idx < nq * D4; idx += kThreads) {
+      const int ql = idx / D4, d4 = idx % D4, q = q0 + ql, r = q / G, g = q % G;
+      float Mx, f[kWaves], L;
+      combine(ql, Mx, f, L);
+      float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-      for (int i = 0; i < kWaves; ++i) O += s_o[i][ql][d] * f[i];
-      return O;
-    };
-    if (nq > 0) {
+      for (int i = 0; i < kWaves; ++i) {
+        const float4 x = *reinterpret_cast<const float4*>(&s_o[i][ql][4 * d4]);
+        O.x += x.x * f[i];
+        O.y += x.y * f[i];
+        O.z += x.z * f[i];
+        O.w += x.w * f[i];
+      }
       if (P.direct) {
-        for (int idx = threadIdx.x; idx < nq * HD; idx += kThreads) {
-          const int ql = idx / HD, d = idx % HD, q = q0 + ql;
-          float Mx, f[kWaves], L;
-          combine(ql, Mx, f, L);
-          P.out[(static_cast<size_t>(row0 + q / G) * P.n_heads + kh * G + q % G) * HD + d] =
-              o_of(ql, d, f) / L;
-        }
+        *reinterpret_cast<float4*>(
+            P.out + (static_cast<size_t>(row0 + r) * P.n_heads + kh * G + g) * HD + 4 * d4) =
+            make_float4(O.x / L, O.y / L, O.z / L, O.w / L);
       } else {
-        // this tile's vectors, as (row, head) entries of the rows' records
-        for (int idx = threadIdx.x; idx < nq * (HD + 2); idx += kThreads) {
-          const int ql = idx < nq * HD ? idx / HD : (idx - nq * HD) >> 1;
-          const int q = q0 + ql, r = q / G, g = q % G;
-          const size_t head_base = static_cast<size_t>(row0 + r) * P.nkv + kh;
-          float* orec = P.part + head_base * record_region(P.nsplit, G, HD) +
-                        static_cast<size_t>(split) * record_floats(G, HD);
-          float Mx, f[kWaves], L;
-          combine(ql, Mx, f, L);
-          if (idx < nq * HD) {
-            const int d = idx % HD;
-            __hip_atomic_store(orec + g * HD + d, o_of(ql, d, f), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-          } else {
-            const int k = (idx - nq * HD) & 1;  // m, then l
-            __hip_atomic_store(orec + G * HD + 2 * g + k, k ? L : Mx, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
+        float* orec = rbase + static_cast<size_t>(r) * row_stride;
+        *reinterpret_cast<float4*>(orec + g * HD + 4 * d4) = O;
+        if (d4 == 0) *reinterpret_cast<float2*>(orec + G * HD + 2 * g) = make_float2(Mx, L);
       }
     }
     __syncthreads();  // s_o / s_ml are rewritten by the next vector tile
