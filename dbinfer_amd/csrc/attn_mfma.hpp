@@ -105,43 +105,6 @@ __device__ __forceinline__ float col_sum(float a) {
 }
 
 // NQ: query vectors of a workgroup (rows x heads)
-// produced<HD>() of the 8 elements d0..d0+7 (d0 % 8 == 0) of one head row,
-// from vector loads: the elements, their rope partners (d +- hd/2), both
-// biases and the 8 (cos, sin) pairs
-template <int HD>
-__device__ __forceinline__ void produce8(const float* x, const float* bias, const double2* cs,
-                                         int d0, float (&out)[8]) {
-  constexpr int H2 = HD / 2;
-  const int j0 = d0 % H2;
-  const bool hi = d0 >= H2;
-  float a[8], b[8], ba[8], bb[8];
-  auto ld8 = [](const float* p, float (&v)[8]) {
-    const float4 u = reinterpret_cast<const float4*>(p)[0], w = reinterpret_cast<const float4*>(p)[1];
-    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w; v[4] = w.x; v[5] = w.y; v[6] = w.z; v[7] = w.w;
-  };
-  ld8(x + j0, a);
-  ld8(x + j0 + H2, b);
-  if (bias != nullptr) {
-    ld8(bias + j0, ba);
-    ld8(bias + j0 + H2, bb);
-  }
-  double2 c2[8];
-  if (cs != nullptr) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) c2[e] = cs[j0 + e];
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float u = a[e], w = b[e];
-    if (bias != nullptr) {
-      u += ba[e];
-      w += bb[e];
-    }
-    if (cs != nullptr) rope_pair(u, w, c2[e]);
-    out[e] = hi ? w : u;
-  }
-}
-
 template <int HD, int NQ>
 struct MCfg {
   static constexpr int NBK = HD / kBlock;      // V blocks per head
@@ -333,25 +296,46 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   };
 
   // ---- q * scale * log2(e) of this lane's 8 channels of query T*QVT + qvl
-  // (raw projections: bias, then the fp64 rope, as the producer computes
-  // each element; padding queries >= nqv are 0)
+  // (padding queries >= nqv are 0)
   float qs[NT][8];
-  const bool q_prod = PROD && (P.qb != nullptr || P.qcs != nullptr);
+  const bool q_prod = PROD && (P.qb != nullptr || P.qcs != nullptr);  // uniform
   auto load_q = [&]() {
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
       const int qv = min(T * QVT + qvl, nqv - 1);
       const float* qg =
           P.q + (static_cast<size_t>(row0 + qv / G) * P.n_heads + kh * G + qv % G) * HD;
-      if (q_prod) {
-        const float* bg = P.qb != nullptr ? P.qb + (kh * G + qv % G) * HD : nullptr;
-        produce8<HD>(qg, bg, P.qcs, 8 * c8, qs[T]);
-      } else {
-        const float4 a = *reinterpret_cast<const float4*>(qg + 8 * c8);
-        const float4 b = *reinterpret_cast<const float4*>(qg + 8 * c8 + 4);
-        qs[T][0] = a.x; qs[T][1] = a.y; qs[T][2] = a.z; qs[T][3] = a.w;
-        qs[T][4] = b.x; qs[T][5] = b.y; qs[T][6] = b.z; qs[T][7] = b.w;
+      const float4 a = *reinterpret_cast<const float4*>(qg + 8 * c8);
+      const float4 b = *reinterpret_cast<const float4*>(qg + 8 * c8 + 4);
+      qs[T][0] = a.x; qs[T][1] = a.y; qs[T][2] = a.z; qs[T][3] = a.w;
+      qs[T][4] = b.x; qs[T][5] = b.y; qs[T][6] = b.z; qs[T][7] = b.w;
+    }
+  };
+  // Raw projections: q + qb, then the fp64 rope, as the producer computes
+  // each element. Every wave needs the whole of q, and producing it per wave
+  // would wait on q's loads before the stream's loads go out (the rope reads
+  // them), a round trip ahead of the stream. Instead one rope pair per
+  // thread: its raw loads go out first (they return first), the pair is
+  // produced after the first chunk's loads are issued, and the waves read q
+  // from LDS (one row: query qv is head g).
+  constexpr int H2 = HD / 2;
+  static_assert(!PROD || NQ * H2 <= kThreads, "one rope pair per thread");
+  __shared__ __align__(16) float s_qp[PROD ? NQ * HD : 4];
+  const int qp_v = threadIdx.x / H2, qp_j = threadIdx.x % H2;
+  const bool qp_on = q_prod && qp_v < nqv;
+  float qp_a = 0.0f, qp_b = 0.0f, qp_ba = 0.0f, qp_bb = 0.0f;
+  double2 qp_cs = make_double2(1.0, 0.0);
+  auto load_q_raw = [&]() {
+    if (qp_on) {
+      const float* qg = P.q + (static_cast<size_t>(row0) * P.n_heads + kh * G + qp_v) * HD;
+      qp_a = qg[qp_j];
+      qp_b = qg[qp_j + H2];
+      if (P.qb != nullptr) {
+        const float* bg = P.qb + (kh * G + qp_v) * HD;
+        qp_ba = bg[qp_j];
+        qp_bb = bg[qp_j + H2];
       }
+      if (P.qcs != nullptr) qp_cs = P.qcs[qp_j];
     }
   };
 
@@ -367,7 +351,10 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     if (threadIdx.x == 0) s_kg.done = 0;
     __syncthreads();
   }
-  load_q();
+  if (q_prod)
+    load_q_raw();
+  else
+    load_q();
   typename App::ShareIn app_knew{};
   typename App::RowIn app_in{};
   if (app_share) App::load_share(A, kh, wave, lane, app_knew);
@@ -380,6 +367,80 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   const int ns = min(P.n_sink, nkeys);  // sinks of the last row (a row r sees pos0 + r + 1 keys)
   const bool sink_wave = split == 0 && wave == 0 && ns > 0;  // wave-uniform
   const bool fresh_sink = kFuse && A.slot >= 0 && A.pos < P.n_sink;
+  // Raw projections: the step's own sink row (k + kb roped, v + vb) is
+  // produced once per workgroup into LDS with q, not per lane inline (whose
+  // loads and fp64 temporaries would set the kernel's register peak).
+  const bool fresh_prod = PROD && A.prod && fresh_sink && split == 0 && ns > 0;  // uniform
+  __shared__ __align__(16) float s_fresh[PROD ? 2 * HD : 4];
+  bool fresh_ready = false;
+  auto fresh_row = [&](float (&kx)[8], float (&vx)[8]) {
+    const float4 k0 = *reinterpret_cast<const float4*>(&s_fresh[8 * c8]);
+    const float4 k1 = *reinterpret_cast<const float4*>(&s_fresh[8 * c8 + 4]);
+    const float4 v0 = *reinterpret_cast<const float4*>(&s_fresh[HD + 8 * c8]);
+    const float4 v1 = *reinterpret_cast<const float4*>(&s_fresh[HD + 8 * c8 + 4]);
+    kx[0] = k0.x; kx[1] = k0.y; kx[2] = k0.z; kx[3] = k0.w;
+    kx[4] = k1.x; kx[5] = k1.y; kx[6] = k1.z; kx[7] = k1.w;
+    vx[0] = v0.x; vx[1] = v0.y; vx[2] = v0.z; vx[3] = v0.w;
+    vx[4] = v1.x; vx[5] = v1.y; vx[6] = v1.z; vx[7] = v1.w;
+  };
+  // thread t < hd/2: the K pair (t, t + hd/2); hd/2 <= t < 3 hd/2: V element
+  // t - hd/2 (produced<HD>() element by element)
+  float fr_a = 0.0f, fr_b = 0.0f, fr_ba = 0.0f, fr_bb = 0.0f;
+  double2 fr_cs = make_double2(1.0, 0.0);
+  auto load_fresh_raw = [&]() {
+    const int t = threadIdx.x;
+    if (t < H2) {
+      fr_a = A.k[kh * HD + t];
+      fr_b = A.k[kh * HD + t + H2];
+      if (A.kb != nullptr) {
+        fr_ba = A.kb[kh * HD + t];
+        fr_bb = A.kb[kh * HD + t + H2];
+      }
+      if (A.kcs != nullptr) fr_cs = A.kcs[t];
+    } else if (t < H2 + HD) {
+      fr_a = A.v[kh * HD + t - H2];
+      if (A.vb != nullptr) fr_ba = A.vb[kh * HD + t - H2];
+    }
+  };
+  auto produce_fresh = [&]() {
+    const int t = threadIdx.x;
+    if (t < H2) {
+      float a = fr_a, b = fr_b;
+      if (A.kb != nullptr) {
+        a += fr_ba;
+        b += fr_bb;
+      }
+      if (A.kcs != nullptr) rope_pair(a, b, fr_cs);
+      s_fresh[t] = a;
+      s_fresh[t + H2] = b;
+    } else if (t < H2 + HD) {
+      s_fresh[HD + t - H2] = A.vb != nullptr ? fr_a + fr_ba : fr_a;
+    }
+  };
+  auto produce_q = [&]() {  // workgroup-uniform (q_prod or fresh_prod)
+    if (qp_on) {
+      float u = qp_a, w = qp_b;
+      if (P.qb != nullptr) {
+        u += qp_ba;
+        w += qp_bb;
+      }
+      if (P.qcs != nullptr) rope_pair(u, w, qp_cs);
+      s_qp[qp_v * HD + qp_j] = u;
+      s_qp[qp_v * HD + qp_j + H2] = w;
+    }
+    if (fresh_prod) produce_fresh();
+    __syncthreads();
+    if (q_prod) {
+#pragma unroll
+      for (int T = 0; T < NT; ++T) {
+        const int qv = min(T * QVT + qvl, nqv - 1);
+        const float4 a = *reinterpret_cast<const float4*>(&s_qp[qv * HD + 8 * c8]);
+        const float4 b = *reinterpret_cast<const float4*>(&s_qp[qv * HD + 8 * c8 + 4]);
+        qs[T][0] = a.x; qs[T][1] = a.y; qs[T][2] = a.z; qs[T][3] = a.w;
+        qs[T][4] = b.x; qs[T][5] = b.y; qs[T][6] = b.z; qs[T][7] = b.w;
+      }
+    }
+  };
   auto sink_rows = [&](int p, float (&kx)[8], float (&vx)[8]) {
     const float* ksb = P.ksink + static_cast<size_t>(kh) * P.n_sink * HD;
     const float* vsb = P.vsink + static_cast<size_t>(kh) * P.n_sink * HD;
@@ -391,17 +452,17 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     vx[0] = v0.x; vx[1] = v0.y; vx[2] = v0.z; vx[3] = v0.w;
     vx[4] = v1.x; vx[5] = v1.y; vx[6] = v1.z; vx[7] = v1.w;
     if (fresh_sink && p == A.pos) {  // uniform
-      const float* kin = A.k + kh * HD;
-      const float* vin = A.v + kh * HD;
+      if (PROD && A.prod) {
+        // produced once per workgroup (s_fresh): read from there once it is
+        // ready, patched in after the production for the entry sinks
+        if (fresh_ready) fresh_row(kx, vx);
+      } else {
+        const float* kin = A.k + kh * HD;
+        const float* vin = A.v + kh * HD;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = 8 * c8 + e;
-        if (PROD && A.prod) {
-          kx[e] = produced<HD>(kin, A.kb != nullptr ? A.kb + kh * HD : nullptr, A.kcs, d);
-          vx[e] = produced<HD>(vin, A.vb != nullptr ? A.vb + kh * HD : nullptr, nullptr, d);
-        } else {
-          kx[e] = kin[d];
-          vx[e] = vin[d];
+        for (int e = 0; e < 8; ++e) {
+          kx[e] = kin[8 * c8 + e];
+          vx[e] = vin[8 * c8 + e];
         }
       }
     }
@@ -419,6 +480,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     return seen ? sdot : -INFINITY;
   };
   float skx[SB][8], svx[SB][8];
+  if (fresh_prod) load_fresh_raw();
   if (sink_wave) {
 #pragma unroll
     for (int u = 0; u < SB; ++u) sink_rows(min(u, ns - 1), skx[u], svx[u]);
@@ -437,6 +499,15 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
   __builtin_amdgcn_sched_barrier(0);
   issue_v(RA, ch0);
   __builtin_amdgcn_sched_barrier(0);
+  if (q_prod || fresh_prod) {  // workgroup-uniform
+    produce_q();
+    fresh_ready = true;
+    if (fresh_prod && sink_wave) {
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+        if (min(u, ns - 1) == A.pos) fresh_row(skx[u], svx[u]);  // uniform
+    }
+  }
   if (app_share) App::requant_share(A, wave, lane, app_knew, app_raw, s_kg);
 #pragma unroll
   for (int T = 0; T < NT; ++T)
