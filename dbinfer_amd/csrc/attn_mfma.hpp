@@ -540,9 +540,9 @@ __global__ __launch_bounds__(kThreads) void attn_i8_kernel(const AttnParams P, c
     for (int t = 0; t < NTV; ++t) o[T][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // the owner's V chunk block with the new row patched in, kept for the
-  // flush (plain inputs only: the producer instance has no registers to spare
-  // and writes the row's bytes)
-  constexpr bool kKeepV = !PROD;
+  // flush (the producer instance above 4 query heads writes the row's bytes
+  // instead: its registers are full)
+  constexpr bool kKeepV = !PROD || NQ <= 4;
   uint4 app_v[kKeepV ? VL : 1];
   // next >= 0: the chunk whose loads go into b as this chunk frees it
   auto compute = [&](Buf& b, const int ch, const bool first, const int next) {
