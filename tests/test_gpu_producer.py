@@ -65,6 +65,12 @@ DECODE_CASES = [
     (F32, 32, 4, 64, 0, 0, 1e4, 33, False),     # config 1 shape
     (F32, 28, 4, 128, 4, 24, 1e6, 60, True),    # config 4 ring: biases only, keys stay un-roped
     (INT8, 28, 4, 128, 4, 24, 1e6, 60, True),
+    # dense int8, q produced once per workgroup: G = 8 (one rope pair per
+    # thread of all 512) and hd 64 with G = 5, both with the steps' own sink
+    # rows produced in LDS
+    (INT8, 32, 4, 128, 4, 0, 1e6, 40, True),
+    (INT8, 40, 8, 64, 4, 0, 1e4, 36, True),
+    (INT8, 24, 8, 128, 4, 0, 5e5, 12, False),   # rope only: no bias add on the sink rows
 ]
 
 
