@@ -31,17 +31,19 @@ constexpr int kTargetBlocks = 256;
 
 // Dense chunks of two or more rows run on the matrix-core rows kernels
 // (attn_rows.hpp for fp32, attn_i8_rows.hpp for int8): nvt 16-vector tiles
-// per workgroup (int8 nvt 3: one, and a remainder tile), rows_vectors / G
+// per workgroup (nvt 3: one, and a remainder tile), rows_vectors / G
 // rows each.
 bool rows_kernel(const KvGeom& g, const AttnCall& c) { return !g.ring && c.rows > 1; }
-// 1: one 16-column tile; 2: two; 3 (int8): one, plus a remainder tile of
-// (query, channel block) columns for up to 16 / (hd / 32) more vectors
+// 1: one 16-column tile; 2: two; 3: one, plus a remainder tile for a few
+// more vectors (int8: (query, channel block) columns for up to 16 / (hd / 32);
+// fp32: 4 x 4 blocks for up to 4)
+int rows_rem(const KvGeom& g) { return g.int8 ? 16 / (g.hd / 32) : 4; }
 int rows_nvt(const KvGeom& g, int G, int rows) {
   if (rows * G <= 16) return 1;
-  return g.int8 && rows * G <= 16 + 16 / (g.hd / 32) ? 3 : 2;
+  return rows * G <= 16 + rows_rem(g) ? 3 : 2;
 }
 // query vectors a workgroup of the instance serves
-int rows_vectors(const KvGeom& g, int nvt) { return nvt == 3 ? 16 + 16 / (g.hd / 32) : 16 * nvt; }
+int rows_vectors(const KvGeom& g, int nvt) { return nvt == 3 ? 16 + rows_rem(g) : 16 * nvt; }
 
 struct Plan {
   int nsplit, chunks_per_split;

@@ -7,7 +7,7 @@
 // score and output is an fp32 accumulation of exact products, well inside
 // the reference's fp32 tolerance):
 //  - Grid (split, kv head, row group), 8 waves per workgroup. A workgroup
-//    serves NV = 16 * NVT query vectors (row r, head g: r * G + g) of up to
+//    serves NV = 16 * NVT (NVT 3: 20) query vectors (row r, head g: r * G + g) of up to
 //    NR = NV / G rows, so every K/V byte of the kv head crosses HBM once per
 //    row group (one group for a C5 verify round: 5 rows x 4 heads = 20).
 //  - Keys in 16-position tiles (one granule of the layout of
@@ -24,6 +24,16 @@
 //    4 kk + j). A lane's output is then hd/4 contiguous dims of its vector.
 //  - Online softmax per vector (lane % 16): a lane's 4 keys, then the four
 //    lane groups through two permlane swaps.
+//  - Remainder tile (NVT 3, e.g. 5 rows x 4 heads = 16 + 4 vectors): the 4
+//    vectors past the first 16 on v_mfma_f32_4x4x1_16b_f32, 16 blocks of
+//    4 x 4 instead of a 16-column tile three quarters padding. QK^T: block
+//    l / 4 takes keys 4 (n / 4) .. + 3 (rows, the lane's own K operand) and
+//    vectors 16 .. 19 (columns: q of vector 16 + n % 4) over the lane
+//    group's dims; the four lane groups' partial scores sum by two permlane
+//    swaps. PV: block l / 4 takes key 4 kk + j (its weights fetched from
+//    the lane that holds them) and dims VD (4 (n / 4) + r) + tt (rows, the
+//    lane's own V operand); the lane groups' partial outputs (disjoint keys)
+//    sum once, at the end. A quarter of the 16-column tile's matrix cycles.
 //  - Split-K records as attn_kernel; the records are merged by a second
 //    launch (attn_rows_merge), one workgroup per (row, head).
 #pragma once
@@ -33,9 +43,15 @@
 namespace dbi {
 namespace {
 
+constexpr int kR4 = 0x124;  // DPP row_ror:4 (lane n of a row reads n - 4 mod 16)
+
+// NVT 1 / 2: one / two 16-vector tiles; 3: one 16-vector tile and a
+// remainder tile of 4 vectors on v_mfma_f32_4x4x1_16b_f32 (see the kernel)
 template <int HD, int G, int NVT>
 struct RCfg {
-  static constexpr int NV = 16 * NVT;  // query vectors per workgroup (padded)
+  static constexpr bool REM = NVT == 3;
+  static constexpr int NTL = REM ? 2 : NVT;           // vector tiles held
+  static constexpr int NV = REM ? 20 : 16 * NVT;      // query vectors per workgroup (padded)
   static constexpr int NR = NV / G;    // rows per workgroup
   static constexpr int NA = HD / 32;   // K units per half per lane (lane columns 4a + kk)
   static constexpr int VD = HD / 16;   // V dims per lane per key
@@ -43,18 +59,17 @@ struct RCfg {
   static constexpr int NT = HD / 16;   // PV output tiles
   static constexpr int OP = HD + 4;    // LDS row pitch of a wave's outputs (bank spread)
   static_assert(HD == 64 || HD == 128, "head dim");
-  static_assert(G >= 1 && G <= 16 * NVT, "query heads per kv head");
+  static_assert(G >= 1 && G <= NV, "query heads per kv head");
 };
-
-// Rows one workgroup of the (hd, G, NVT) instance serves.
-__host__ __device__ constexpr int rows_per_group(int G, int NVT) { return 16 * NVT / G; }
 
 template <int HD, int G, int NVT>
 __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P) {
   using C = RCfg<HD, G, NVT>;
   constexpr int NA = C::NA, VD = C::VD, VU = C::VU, NT = C::NT, NR = C::NR, OP = C::OP;
+  constexpr int NTL = C::NTL;
+  constexpr bool REM = C::REM;
   constexpr int TILE = kGranule;
-  constexpr int NCH = NVT == 1 ? 4 : 2;
+  constexpr int NCH = NTL == 1 ? 4 : 2;
 
   __shared__ __align__(16) float s_o[kWaves][16][OP];
   __shared__ float s_ml[kWaves][16][2];
@@ -90,11 +105,13 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P)
 
   // ---- q operands of the lane's vectors, dims 4 (4a + kk) + h hd/2 .. + 3,
   // in the log2 domain; padding vectors (>= nv) are 0
-  float4 qv[NVT][2][NA];
-  int lim[NVT];  // last key of each of the lane's vectors (causal)
+  // (the remainder tile: vector 16 + lane % 4, see below)
+  float4 qv[NTL][2][NA];
+  int lim[NTL];  // last key of each of the lane's vectors (causal)
+  auto vec_of = [&](int vt) { return REM && vt == 1 ? 16 + (n & 3) : vt * 16 + n; };
 #pragma unroll
-  for (int vt = 0; vt < NVT; ++vt) {
-    const int q = min(vt * 16 + n, nv - 1);
+  for (int vt = 0; vt < NTL; ++vt) {
+    const int q = min(vec_of(vt), nv - 1);
     lim[vt] = P.pos0 + row0 + q / G;
     const float* qp =
         P.q + (static_cast<size_t>(row0 + q / G) * P.n_heads + kh * G + q % G) * HD + 4 * kk;
@@ -132,18 +149,18 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P)
   issue_v(t);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int vt = 0; vt < NVT; ++vt) {
-    const float fq = vt * 16 + n < nv ? P.qscale : 0.0f;
+  for (int vt = 0; vt < NTL; ++vt) {
+    const float fq = vec_of(vt) < nv ? P.qscale : 0.0f;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int a = 0; a < NA; ++a) qv[vt][h][a] *= fq;
   }
 
-  float M[NVT], l[NVT];
-  f32x4 acc[NVT][NT];
+  float M[NTL], l[NTL];
+  f32x4 acc[NTL][NT];
 #pragma unroll
-  for (int vt = 0; vt < NVT; ++vt) {
+  for (int vt = 0; vt < NTL; ++vt) {
     M[vt] = kMinit;
     l[vt] = 0.0f;
 #pragma unroll
@@ -154,9 +171,9 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P)
     const int k0 = t * TILE;  // first key of the tile
     // ---- S^T in NCH independent chains per vector tile (4 independent
     // chains in all keep the matrix core's dependent issue covered)
-    f32x4 sc[NVT][NCH];
+    f32x4 sc[NTL][NCH];
 #pragma unroll
-    for (int vt = 0; vt < NVT; ++vt)
+    for (int vt = 0; vt < NTL; ++vt)
 #pragma unroll
       for (int e = 0; e < NCH; ++e) sc[vt][e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -166,12 +183,15 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P)
         const float4 x = kb[h][a];
         const float xe[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) {
+        for (int vt = 0; vt < NTL; ++vt) {
           const float4 y = qv[vt][h][a];
           const float ye[4] = {y.x, y.y, y.z, y.w};
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            sc[vt][e % NCH] = __builtin_amdgcn_mfma_f32_16x16x4f32(xe[e], ye[e], sc[vt][e % NCH], 0, 0, 0);
+            sc[vt][e % NCH] =
+                REM && vt == 1
+                    ? __builtin_amdgcn_mfma_f32_4x4x1f32(xe[e], ye[e], sc[vt][e % NCH], 0, 0, 0)
+                    : __builtin_amdgcn_mfma_f32_16x16x4f32(xe[e], ye[e], sc[vt][e % NCH], 0, 0, 0);
         }
       }
     __builtin_amdgcn_sched_barrier(0);
@@ -179,19 +199,31 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P)
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- online softmax per vector (lane % 16)
-    float pw[NVT][4];
+    float pw[NTL][4];
 #pragma unroll
-    for (int vt = 0; vt < NVT; ++vt) {
+    for (int vt = 0; vt < NTL; ++vt) {
+      const bool rem = REM && vt == 1;
       f32x4 s4 = sc[vt][0];
 #pragma unroll
       for (int e = 1; e < NCH; ++e) s4 += sc[vt][e];
+      // the remainder tile: lane l holds the partial sums of block l / 4 (the
+      // lane group's dims) at keys 4 (n / 4) + v; the four lane groups sum
+      // to the scores of vector 16 + n % 4
+      if (rem) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) s4[v] = col_sum(s4[v]);
+      }
+      const int kq = rem ? 4 * (n >> 2) : 4 * kk;  // the lane's first key in the tile
       float s[4], mx = -INFINITY;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        s[v] = k0 + 4 * kk + v <= lim[vt] ? s4[v] : -INFINITY;
+        s[v] = k0 + kq + v <= lim[vt] ? s4[v] : -INFINITY;
         mx = fmaxf(mx, s[v]);
       }
-      const float mn = lazy_max(M[vt], col_max(mx));
+      // (remainder: the max over the lanes n, n ^ 4, n ^ 8, n ^ 12 of a row)
+      const float cm = rem ? fmaxf(fmaxf(mx, dpp<kR4>(mx)), dpp<kX8>(fmaxf(mx, dpp<kR4>(mx))))
+                           : col_max(mx);
+      const float mn = lazy_max(M[vt], cm);
       const float alpha = fast_exp2(M[vt] - mn);
       M[vt] = mn;
       float ls = 0.0f;
@@ -226,10 +258,20 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P)
         for (int d = 0; d < VD; ++d) vd[d] = ok ? vd[d] : 0.0f;
       }
 #pragma unroll
-      for (int vt = 0; vt < NVT; ++vt)
+      for (int vt = 0; vt < NTL; ++vt) {
+        if (REM && vt == 1) {
+          // block l / 4 takes key 4 kk + j: the weight of vector 16 + n % 4
+          // there, from the lane whose scores hold it (lane 4 kk + n % 4)
+          const float pr = __shfl(pw[1][j], 4 * kk + (n & 3));
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt)
-          acc[vt][tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[tt], pw[vt][j], acc[vt][tt], 0, 0, 0);
+          for (int tt = 0; tt < NT; ++tt)
+            acc[1][tt] = __builtin_amdgcn_mfma_f32_4x4x1f32(vd[tt], pr, acc[1][tt], 0, 0, 0);
+        } else {
+#pragma unroll
+          for (int tt = 0; tt < NT; ++tt)
+            acc[vt][tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[tt], pw[vt][j], acc[vt][tt], 0, 0, 0);
+        }
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     issue_v(t + kWaves);
@@ -239,20 +281,45 @@ __global__ __launch_bounds__(kThreads) void attn_rows_kernel(const AttnParams P)
   // ---- per vector tile: wave states to LDS, the cross-wave combine, then
   // the output (single split) or this split's record of each row
 #pragma unroll
-  for (int vt = 0; vt < NVT; ++vt) {
-    const float lt = col_sum(l[vt]);
-    if (kk == 0) {
-      s_ml[wave][n][0] = M[vt];
-      s_ml[wave][n][1] = lt;
+  for (int vt = 0; vt < NTL; ++vt) {
+    if (REM && vt == 1) {
+      // lane l: the sums of its 4 keys (vector 16 + n % 4), the same in every
+      // lane group; O^T partials over the lane group's keys at dims
+      // VD (4 (n / 4) + v) + tt
+      float lt = l[1] + dpp<kR4>(l[1]);
+      lt += dpp<kX8>(lt);
+      if (lane < 4) {
+        s_ml[wave][lane][0] = M[1];
+        s_ml[wave][lane][1] = lt;
+      }
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[1][tt][v] = col_sum(acc[1][tt][v]);
+      if (kk == 0) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+          for (int u = 0; u < VU; ++u)
+            *reinterpret_cast<float4*>(&s_o[wave][n & 3][VD * (4 * (n >> 2) + v) + 4 * u]) =
+                make_float4(acc[1][4 * u][v], acc[1][4 * u + 1][v], acc[1][4 * u + 2][v],
+                            acc[1][4 * u + 3][v]);
+      }
+    } else {
+      const float lt = col_sum(l[vt]);
+      if (kk == 0) {
+        s_ml[wave][n][0] = M[vt];
+        s_ml[wave][n][1] = lt;
+      }
+      // lane holds O^T[dim VD (4 kk + v) + tt][vector n]
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int u = 0; u < VU; ++u)
+          *reinterpret_cast<float4*>(&s_o[wave][n][VD * (4 * kk + v) + 4 * u]) =
+              make_float4(acc[vt][4 * u][v], acc[vt][4 * u + 1][v], acc[vt][4 * u + 2][v],
+                          acc[vt][4 * u + 3][v]);
     }
-    // lane holds O^T[dim VD (4 kk + v) + tt][vector n]
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-#pragma unroll
-      for (int u = 0; u < VU; ++u)
-        *reinterpret_cast<float4*>(&s_o[wave][n][VD * (4 * kk + v) + 4 * u]) =
-            make_float4(acc[vt][4 * u][v], acc[vt][4 * u + 1][v], acc[vt][4 * u + 2][v],
-                        acc[vt][4 * u + 3][v]);
     __syncthreads();
     const int q0 = vt * 16;
     const int nq = min(16, nv - q0);  // vectors of this tile (uniform)

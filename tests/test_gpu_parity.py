@@ -311,11 +311,12 @@ def test_chunk_attention(dtype, nh, nkv, hd, pos0, n):
     (8, 8, 64, 5, 63, 4),         # gqa 1: two row groups (32 + 31)
     (32, 8, 128, 16379, 5, 4),    # config 5's verify round at 16k (32 splits)
     (32, 8, 128, 4, 6, 9),        # int8: rows see 5..9 sinks (more than the merge holds at once)
-    # int8 remainder tiles (16 vectors + up to 16 / (hd / 32) in (query, block) columns)
+    # remainder tiles: 16 vectors + up to 16 / (hd / 32) in (query, block)
+    # columns (int8) or up to 4 in 4 x 4 blocks (fp32)
     (32, 8, 128, 2, 5, 4),        # gqa 4, 20 vectors: rows see 3..4 sinks
     (24, 8, 128, 700, 6, 4),      # gqa 3, 18 vectors: a remainder of 2
-    (40, 8, 64, 300, 4, 4),       # hd 64, gqa 5, 20 vectors: 4 of 8 remainder columns
-    (16, 8, 64, 90, 12, 4),       # hd 64, gqa 2, 24 vectors: the full remainder
+    (40, 8, 64, 300, 4, 4),       # hd 64, gqa 5, 20 vectors: 4 of 8 remainder columns (fp32: all 4)
+    (16, 8, 64, 90, 12, 4),       # hd 64, gqa 2, 24 vectors: the full remainder (fp32: two tiles)
     (28, 4, 128, 4000, 10, 4),    # gqa 7: row groups of 2 rows (14 vectors, one tile)
     (8, 8, 128, 100, 18, 4),      # gqa 1, 18 vectors: remainder of 2 rows
     (16, 8, 128, 500, 10, 4),     # gqa 2, 20 vectors: the full remainder
